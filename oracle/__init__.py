@@ -1,0 +1,230 @@
+"""CPU oracle for the ytensor_amd hot path — TEST INFRASTRUCTURE ONLY.
+
+Two libraries share one C ABI shape:
+
+* ``liboracle.so`` — the from-scratch restatement in ``ytoracle.cpp`` of
+  YTensor's CPU algorithms (SnifferCaptain/ytensor v0.13). Always built.
+* ``_ref/libytref.so`` — the reference itself compiled from its own sources
+  by ``make ref`` (only where ``/root/reference`` exists). Optional.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker / the timed CPU baseline.
+The product path (``ytensor_amd``) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libytref.so")
+REF_ROOT = "/root/reference"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+
+def build(ref: bool | None = None) -> None:
+    """Compile liboracle.so (and _ref/libytref.so when the reference exists)."""
+    subprocess.check_call(["make", "-s", "-C", HERE, "all"])
+    if ref is None:
+        ref = os.path.isdir(REF_ROOT)
+    if ref:
+        subprocess.check_call(["make", "-s", "-C", HERE, "ref"])
+
+
+def _bind(lib: ctypes.CDLL, prefix: str) -> ctypes.CDLL:
+    sig = {
+        "seed": (None, [ctypes.c_uint32]),
+        "randn": (None, [_P, _L]),
+        "bf16_round": (None, [_P, _P, _L]),
+        "bf16_to_f32": (None, [_P, _P, _L]),
+        "f16_round": (None, [_P, _P, _L]),
+        "f16_to_f32": (None, [_P, _P, _L]),
+        "sgemm": (None, [_P, _P, _P, _I, _I, _I, _F, _F, _L, _L, _L, _L, _L, _L]),
+        "flash_attention": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F] + [_L] * 8 + [_P, _L, _P, _L, _L]),
+        "sdpa_gqa": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I]),
+        "rms_norm": (None, [_P, _P, _L, _I, _F]),
+        "rope_precompute": (None, [_I, _I, _F, _P, _P]),
+        "rope": (None, [_P, _I, _I, _I, _I, _P, _P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, f"{prefix}_{name}", None)
+        if fn is None:
+            continue
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def _ptr(a: np.ndarray | None) -> int | None:
+    return None if a is None else a.ctypes.data
+
+
+class CpuPath:
+    """numpy-facing wrapper over one of the two libraries."""
+
+    def __init__(self, path: str, prefix: str):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built (run `make -C {HERE}`)")
+        self.lib = _bind(ctypes.CDLL(path), prefix)
+        self.prefix = prefix
+        self.path = path
+
+    def _fn(self, name):
+        return getattr(self.lib, f"{self.prefix}_{name}")
+
+    # --- RNG (YTensor::seed / YTensor::randn) ---------------------------------
+    def seed(self, s: int) -> None:
+        self._fn("seed")(s)
+
+    def randn(self, *shape: int) -> np.ndarray:
+        out = np.empty(shape, dtype=np.float32)
+        self._fn("randn")(_ptr(out), out.size)
+        return out
+
+    # --- type conversions ------------------------------------------------------
+    def bf16_round(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, dtype=np.uint16)
+        self._fn("bf16_round")(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def bf16_to_f32(self, h: np.ndarray) -> np.ndarray:
+        h = np.ascontiguousarray(h, dtype=np.uint16)
+        out = np.empty(h.shape, dtype=np.float32)
+        self._fn("bf16_to_f32")(_ptr(h), _ptr(out), h.size)
+        return out
+
+    def f16_round(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, dtype=np.uint16)
+        self._fn("f16_round")(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def f16_to_f32(self, h: np.ndarray) -> np.ndarray:
+        h = np.ascontiguousarray(h, dtype=np.uint16)
+        out = np.empty(h.shape, dtype=np.float32)
+        self._fn("f16_to_f32")(_ptr(h), _ptr(out), h.size)
+        return out
+
+    # --- GEMM ------------------------------------------------------------------
+    def sgemm(self, A: np.ndarray, B: np.ndarray, *, b_trans: bool = False, alpha: float = 1.0,
+              beta: float = 0.0, C: np.ndarray | None = None) -> np.ndarray:
+        """C = alpha*A@B + beta*C. A [m,k] row-major; B [k,n] row-major, or
+        (b_trans) W [n,k] row-major passed as the column-major view B = W^T."""
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        B = np.ascontiguousarray(B, dtype=np.float32)
+        m, k = A.shape
+        if b_trans:
+            n = B.shape[0]
+            rsb, csb = 1, k
+        else:
+            n = B.shape[1]
+            rsb, csb = n, 1
+        if C is None:
+            C = np.zeros((m, n), dtype=np.float32)
+        else:
+            C = np.ascontiguousarray(C, dtype=np.float32).copy()
+        self._fn("sgemm")(_ptr(A), _ptr(B), _ptr(C), m, n, k, alpha, beta, k, 1, rsb, csb, n, 1)
+        return C
+
+    # --- attention ---------------------------------------------------------------
+    def flash_attention(self, Q, K, V, scale, mask=None, bias=None) -> np.ndarray:
+        """One matrix: Q [q,d], K [kv,d], V [kv,dv] contiguous; mask bool [q,kv]."""
+        Q = np.ascontiguousarray(Q, dtype=np.float32)
+        K = np.ascontiguousarray(K, dtype=np.float32)
+        V = np.ascontiguousarray(V, dtype=np.float32)
+        q_len, d = Q.shape
+        kv_len, dv = V.shape
+        O = np.zeros((q_len, dv), dtype=np.float32)
+        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self._fn("flash_attention")(
+            _ptr(Q), _ptr(K), _ptr(V), _ptr(O), q_len, kv_len, d, dv, scale,
+            d, 1, d, 1, dv, 1, dv, 1,
+            _ptr(m), kv_len, _ptr(b), kv_len if b is not None else 0, 1)
+        return O
+
+    def sdpa_gqa(self, Q, K, V, scale=0.0, causal=True) -> np.ndarray:
+        """Q [B,Hq,S,D], K/V [B,Hkv,KV,D] contiguous float32 -> O [B,Hq,S,D]."""
+        Q = np.ascontiguousarray(Q, dtype=np.float32)
+        K = np.ascontiguousarray(K, dtype=np.float32)
+        V = np.ascontiguousarray(V, dtype=np.float32)
+        B, Hq, S, D = Q.shape
+        Hkv, KV = K.shape[1], K.shape[2]
+        O = np.zeros_like(Q)
+        self._fn("sdpa_gqa")(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), B, Hq, Hkv, S, KV, D, scale, int(causal))
+        return O
+
+    # --- RMSNorm / RoPE ----------------------------------------------------------
+    def rms_norm(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        n = x.shape[-1]
+        self._fn("rms_norm")(_ptr(x), _ptr(w), x.size // n, n, eps)
+        return x
+
+    def rope_tables(self, dim: int, max_len: int, theta: float):
+        c = np.empty((max_len, dim), dtype=np.float32)
+        s = np.empty((max_len, dim), dtype=np.float32)
+        self._fn("rope_precompute")(dim, max_len, theta, _ptr(c), _ptr(s))
+        return c, s
+
+    def rope(self, x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+        """x [B,H,L,D]; cos/sin [L,D] (already sliced to the positions)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        B, H, L, D = x.shape
+        cos = np.ascontiguousarray(cos[:L], dtype=np.float32)
+        sin = np.ascontiguousarray(sin[:L], dtype=np.float32)
+        self._fn("rope")(_ptr(x), B, H, L, D, _ptr(cos), _ptr(sin))
+        return x
+
+    def set_num_threads(self, t: int) -> None:
+        fn = getattr(self.lib, f"{self.prefix}_set_num_threads", None)
+        if fn is not None:
+            fn.argtypes = [_I]
+            fn(t)
+
+
+_oracle = None
+_ref = None
+
+
+def oracle() -> CpuPath:
+    """The restatement (always available once built)."""
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(LIB_PATH):
+            build(ref=False)
+        _oracle = CpuPath(LIB_PATH, "oracle")
+    return _oracle
+
+
+def reference() -> CpuPath | None:
+    """The compiled reference, or None when it was not built here."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PATH):
+        _ref = CpuPath(REF_PATH, "ref")
+    return _ref
+
+
+# --- the configs' input recipes (YTensor::seed + randn) ---
+
+def bf16_inputs(path: CpuPath, seed: int, shapes, scales) -> list[np.ndarray]:
+    """Draw each shape in order from one seeded stream, scale in fp32, round to
+    bf16 with YTensor's rounding; returns uint16 bit arrays."""
+    path.seed(seed)
+    outs = []
+    for shp, sc in zip(shapes, scales):
+        x = path.randn(*shp)
+        if sc != 1.0:
+            x = (x * np.float32(sc)).astype(np.float32)
+        outs.append(path.bf16_round(x))
+    return outs

@@ -1,0 +1,150 @@
+// ref_shim.cpp — C-ABI harness around the REFERENCE itself (YTensor v0.13),
+// compiled from the reference's own headers and example source where they lie
+// under /root/reference. Build: oracle/Makefile target `ref`, output only into
+// oracle/_ref/. This file contains no reference code: it only calls the
+// reference's public functions so that tests can compare the restatement in
+// ytoracle.cpp against the real thing, and so that bench.py can time the real
+// CPU path ("kind": "reference").
+//
+// TEST INFRASTRUCTURE ONLY — never linked into the product.
+
+#include "ytensor.hpp"
+#include "qwen3.hpp"
+
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#define REXPORT extern "C" __attribute__((visibility("default")))
+
+REXPORT int ref_abi_version(void) { return 1; }
+
+REXPORT void ref_seed(uint32_t s) { yt::YTensor<float, 1>::seed(s); }
+
+REXPORT void ref_randn(float* out, int64_t n) {
+    auto t = yt::YTensor<float, 1>::randn(static_cast<int>(n));
+    std::memcpy(out, t.data(), sizeof(float) * static_cast<size_t>(n));
+}
+
+REXPORT void ref_bf16_round(const float* x, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        yt::bfloat16 b(x[i]);
+        std::memcpy(&out[i], &b, 2);
+    }
+}
+
+REXPORT void ref_bf16_to_f32(const uint16_t* x, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        yt::bfloat16 b;
+        std::memcpy(&b, &x[i], 2);
+        out[i] = static_cast<float>(b);
+    }
+}
+
+REXPORT void ref_f16_round(const float* x, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        yt::float16 h(x[i]);
+        std::memcpy(&out[i], &h, 2);
+    }
+}
+
+REXPORT void ref_f16_to_f32(const uint16_t* x, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        yt::float16 h;
+        std::memcpy(&h, &x[i], 2);
+        out[i] = static_cast<float>(h);
+    }
+}
+
+REXPORT void ref_set_num_threads(int t) { yt::kernel::avx2::set_num_threads(t); }
+
+REXPORT void ref_sgemm(const float* A, const float* B, float* C, int m, int n, int k, float alpha, float beta,
+                       int64_t rsa, int64_t csa, int64_t rsb, int64_t csb, int64_t rsc, int64_t csc) {
+    yt::kernel::avx2::sgemm(A, B, C, m, n, k, alpha, beta, rsa, csa, rsb, csb, rsc, csc);
+}
+
+// YTensor<float,2>::matmul through the tensor API (AVX2 backend): A [m,k] row-major;
+// B either [k,n] row-major (b_trans=0) or a transposed view of W [n,k] (b_trans=1),
+// which is what yt::function::linear passes (src/function/ops.inl:84-91).
+REXPORT void ref_matmul(const float* A, const float* B, float* C, int m, int n, int k, int b_trans) {
+    yt::YTensor<float, 2> a(m, k);
+    std::memcpy(a.data(), A, sizeof(float) * static_cast<size_t>(m) * k);
+    yt::YTensor<float, 2> out;
+    if (b_trans) {
+        yt::YTensor<float, 2> w(n, k);
+        std::memcpy(w.data(), B, sizeof(float) * static_cast<size_t>(n) * k);
+        out = yt::function::linear(a, w);
+    } else {
+        yt::YTensor<float, 2> b(k, n);
+        std::memcpy(b.data(), B, sizeof(float) * static_cast<size_t>(k) * n);
+        out = a.matmul(b);
+    }
+    auto c = out.contiguous();
+    std::memcpy(C, c.data(), sizeof(float) * static_cast<size_t>(m) * n);
+}
+
+REXPORT void ref_flash_attention(const float* Q, const float* K, const float* V, float* O, int q_len, int kv_len,
+                                 int head_dim, int value_dim, float scale, int64_t rsq, int64_t csq, int64_t rsk,
+                                 int64_t csk, int64_t rsv, int64_t csv, int64_t rso, int64_t cso,
+                                 const uint8_t* mask, int64_t mask_stride, const float* bias, int64_t rsbias,
+                                 int64_t csbias) {
+    std::vector<char> mb;
+    const bool* mp = nullptr;
+    if (mask) {
+        size_t cnt = static_cast<size_t>(q_len) * static_cast<size_t>(mask_stride);
+        mb.resize(cnt);
+        for (size_t i = 0; i < cnt; ++i) mb[i] = mask[i] ? 1 : 0;
+        mp = reinterpret_cast<const bool*>(mb.data());
+    }
+    yt::kernel::avx2::flash_attention(Q, K, V, O, q_len, kv_len, head_dim, value_dim, scale, rsq, csq, rsk, csk,
+                                      rsv, csv, rso, cso, mp, mask_stride, bias, rsbias, csbias);
+}
+
+// scaledDotProductAttention(FLASH_AVX2) with GQA exactly as the qwen3 example
+// builds it (example/qwen3/src/qwen3.cpp:250-264): q [B,Hkv,G,S,D] view,
+// k/v unsqueeze(2).repeat(1,1,G,1,1), bool causal mask [S,kv].
+REXPORT void ref_sdpa_gqa(const float* Q, const float* K, const float* V, float* O, int B, int Hq, int Hkv,
+                          int q_len, int kv_len, int D, float scale, int causal) {
+    const int G = Hq / Hkv;
+    yt::YTensor<float, 4> q4(B, Hq, q_len, D), k4(B, Hkv, kv_len, D), v4(B, Hkv, kv_len, D);
+    std::memcpy(q4.data(), Q, sizeof(float) * q4.size());
+    std::memcpy(k4.data(), K, sizeof(float) * k4.size());
+    std::memcpy(v4.data(), V, sizeof(float) * v4.size());
+    auto q5 = q4.reshape(B, Hkv, G, q_len, D);
+    yt::YTensor<float, 5> k5(k4.unsqueeze(2).repeat(1, 1, G, 1, 1));
+    yt::YTensor<float, 5> v5(v4.unsqueeze(2).repeat(1, 1, G, 1, 1));
+    yt::YTensor<bool, 2> mask(q_len, kv_len);
+    const int start = kv_len - q_len;
+    for (int i = 0; i < q_len; ++i)
+        for (int j = 0; j < kv_len; ++j) mask.at(i, j) = causal ? (j <= start + i) : true;
+    auto o5 = yt::function::scaledDotProductAttention(q5, k5, v5, scale, &mask, nullptr,
+                                                      yt::function::sdpaBackend::FLASH_AVX2);
+    auto oc = o5.contiguous();
+    std::memcpy(O, oc.data(), sizeof(float) * static_cast<size_t>(B) * Hq * q_len * D);
+}
+
+REXPORT void ref_rms_norm(float* x, const float* w, int64_t rows, int n, float eps) {
+    yt::YTensor<float, 2> t(static_cast<int>(rows), n);
+    std::memcpy(t.data(), x, sizeof(float) * static_cast<size_t>(rows) * n);
+    yt::YTensor<float, 1> wt(n);
+    std::memcpy(wt.data(), w, sizeof(float) * n);
+    yt::function::rmsNorm_(t, wt, -1, eps);
+    std::memcpy(x, t.data(), sizeof(float) * static_cast<size_t>(rows) * n);
+}
+
+REXPORT void ref_rope_precompute(int dim, int max_len, float theta, float* cosv, float* sinv) {
+    qwen3::RoPECache rc;
+    rc.precompute(dim, max_len, theta);
+    std::memcpy(cosv, rc.cos.data(), sizeof(float) * static_cast<size_t>(dim) * max_len);
+    std::memcpy(sinv, rc.sin.data(), sizeof(float) * static_cast<size_t>(dim) * max_len);
+}
+
+REXPORT void ref_rope(float* x, int B, int H, int L, int D, const float* cosv, const float* sinv) {
+    yt::YTensor<float, 4> k(B, H, L, D);
+    std::memcpy(k.data(), x, sizeof(float) * k.size());
+    yt::YTensor<float, 2> c(L, D), s(L, D);
+    std::memcpy(c.data(), cosv, sizeof(float) * static_cast<size_t>(L) * D);
+    std::memcpy(s.data(), sinv, sizeof(float) * static_cast<size_t>(L) * D);
+    qwen3::ops::rope_k(k, c, s);
+    std::memcpy(x, k.data(), sizeof(float) * k.size());
+}

@@ -1,0 +1,607 @@
+// ytoracle.cpp — CPU restatement of YTensor's (SnifferCaptain/ytensor v0.13)
+// CPU algorithms on the MI355X hot path.
+//
+// TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP
+// kernels in ytensor_amd/csrc and the "port" CPU baseline in bench.py. The
+// product path (libythip.so) never links, loads or calls it.
+//
+// Every function restates one reference algorithm, cited as file:line relative
+// to the reference root. Summation orders follow the reference so that the
+// fp32 results are bit-identical to YTensor's AVX2 path where the reference
+// order is fixed by intrinsics (sequential FMA chains, 2x8-lane GEMV
+// accumulators, the hsum_ps tree). The build uses -ffp-contract=off and
+// writes every FMA the reference performs as std::fma, so the compiler cannot
+// reassociate or contract differently from what is written here.
+//
+// Pinning (what checks each function): see tests/test_oracle_*.py.
+//   - randn / bf16 / fp16: golden vectors written by the compiled reference
+//     (tests/golden) plus a closed-form known-answer table.
+//   - sgemm / gemv / flash / rmsnorm / rope / qwen3: bit-exact or ulp-level
+//     comparison against the compiled reference (oracle/_ref) on fixtures, plus
+//     closed forms (identity, permutation, small integers, single visible key,
+//     Q=0 mean, decode == last prefill row) and fp64 brute force.
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <random>
+#include <vector>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define OEXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+inline uint32_t f2u(float x) { uint32_t u; std::memcpy(&u, &x, 4); return u; }
+inline float u2f(uint32_t u) { float x; std::memcpy(&x, &u, 4); return x; }
+
+// ---------------------------------------------------------------------------
+// Types
+// ---------------------------------------------------------------------------
+
+// include/types/bfloat16.hpp:78-80 — "round_to_nearest_even": adds bit16>>1 and
+// shifts. Not IEEE RNE (a value with bit16 = 0 and low half exactly 0x8000
+// truncates; NaN is not special-cased).
+inline uint16_t bf16_round(float x) {
+    uint32_t u = f2u(x);
+    return static_cast<uint16_t>((u + ((u & 0x00010000u) >> 1)) >> 16);
+}
+// include/types/bfloat16.hpp:285-291
+inline float bf16_to_f32(uint16_t h) { return u2f(static_cast<uint32_t>(h) << 16); }
+
+// include/types/float_spec.hpp:435-491 (FloatSpec<1,5,10>::fromFloat32):
+// zero/subnormal fp32 -> signed 0, inf/NaN kept (NaN mantissa = 1), underflow
+// (realExp <= 0) flushes to signed 0, overflow -> inf, otherwise mantissa RNE.
+inline uint16_t f16_round(float x) {
+    uint32_t bits = f2u(x);
+    uint32_t s = (bits >> 31) & 1u, e = (bits >> 23) & 0xFFu, m = bits & 0x7FFFFFu;
+    uint32_t ne, nm;
+    if (e == 0) { ne = 0; nm = 0; }
+    else if (e == 0xFF) { ne = 31; nm = m != 0 ? 1 : 0; }
+    else {
+        int real = static_cast<int>(e) - 127 + 15;
+        if (real <= 0) { ne = 0; nm = 0; }
+        else if (real >= 31) { ne = 31; nm = 0; }
+        else {
+            ne = static_cast<uint32_t>(real);
+            nm = m >> 13;
+            uint32_t rem = m & 0x1FFFu, half = 0x1000u;
+            if (rem > half || (rem == half && (nm & 1u))) {
+                nm++;
+                if (nm >= 0x400u) { nm = 0; ne++; if (ne >= 31) { ne = 31; nm = 0; } }
+            }
+        }
+    }
+    return static_cast<uint16_t>((s << 15) | (ne << 10) | nm);
+}
+// include/types/float_spec.hpp:299-370 (toFloat32), specialised to fp16.
+inline float f16_to_f32(uint16_t h) {
+    uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, r;
+    if (e == 0) {
+        if (m == 0) r = s << 31;
+        else {
+            int shift = 0;
+            while ((m & 0x200u) == 0 && shift < 10) { m <<= 1; shift++; }
+            m = (m << 1) & 0x3FFu;
+            int ee = 1 - shift;
+            int ne = ee - 15 + 127;
+            r = (ne <= 0) ? ((s << 31) | (m << 13)) : ((s << 31) | (static_cast<uint32_t>(ne) << 23) | (m << 13));
+        }
+    } else if (e == 31) {
+        r = (s << 31) | (0xFFu << 23) | (m != 0 ? 1u : 0u);
+    } else {
+        r = (s << 31) | ((e - 15 + 127) << 23) | (m << 13);
+    }
+    return u2f(r);
+}
+
+// ---------------------------------------------------------------------------
+// RNG: include/ytensor_infos.hpp:81 (global std::mt19937), ytensor_core.inl:729-732
+// (seed), ytensor_core.hpp:44-58 (randn: a fresh normal_distribution<double>
+// per tensor, values drawn in row-major order, then static_cast<T>).
+// ---------------------------------------------------------------------------
+std::mt19937 g_gen;
+
+// ---------------------------------------------------------------------------
+// hsum_ps: src/kernel/avx2/gemm_utils.inl:117-126
+//   ((v0+v4)+(v1+v5)) + ((v2+v6)+(v3+v7))
+// ---------------------------------------------------------------------------
+inline float hsum8(const float v[8]) {
+    float a0 = v[0] + v[4], a1 = v[1] + v[5], a2 = v[2] + v[6], a3 = v[3] + v[7];
+    return (a0 + a1) + (a2 + a3);
+}
+
+// gemv_dot_ncols<N> for one column: src/kernel/avx2/sgemv.inl:32-52.
+// Two 8-lane accumulators over 16-element steps, one 8-step, hsum(acc0+acc1),
+// then a scalar tail.
+inline float dot_2x8(const float* a, const float* b, int k) {
+    float acc0[8] = {0}, acc1[8] = {0};
+    int p = 0;
+    for (; p + 16 <= k; p += 16)
+        for (int l = 0; l < 8; ++l) {
+            acc0[l] = std::fma(a[p + l], b[p + l], acc0[l]);
+            acc1[l] = std::fma(a[p + 8 + l], b[p + 8 + l], acc1[l]);
+        }
+    for (; p + 8 <= k; p += 8)
+        for (int l = 0; l < 8; ++l) acc0[l] = std::fma(a[p + l], b[p + l], acc0[l]);
+    float t[8];
+    for (int l = 0; l < 8; ++l) t[l] = acc0[l] + acc1[l];
+    float s = hsum8(t);
+    for (; p < k; ++p) s = std::fma(a[p], b[p], s);
+    return s;
+}
+
+// sdot_contiguous: src/kernel/avx2/sdot.inl:13-35 (4 accumulators over 32-steps).
+inline float dot_4x8(const float* x, const float* y, int n) {
+    float acc[4][8] = {{0}};
+    int i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int q = 0; q < 4; ++q)
+            for (int l = 0; l < 8; ++l) acc[q][l] = std::fma(x[i + 8 * q + l], y[i + 8 * q + l], acc[q][l]);
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; ++l) acc[0][l] = std::fma(x[i + l], y[i + l], acc[0][l]);
+    float t[8];
+    for (int l = 0; l < 8; ++l) t[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+    float s = hsum8(t);
+    for (; i < n; ++i) s = std::fma(x[i], y[i], s);
+    return s;
+}
+
+inline float dot_strided(const float* x, const float* y, int n, int64_t incx, int64_t incy) {
+    // src/kernel/avx2/sdot.inl:5-10
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) s = std::fma(x[i * incx], y[i * incy], s);
+    return s;
+}
+
+// ---------------------------------------------------------------------------
+// M=1 GEMV: src/kernel/avx2/sgemv.inl:443-717 (gemv_row_simd)
+// ---------------------------------------------------------------------------
+void gemv_row(const float* A, const float* B, float* C, int n, int k, float alpha, float beta,
+              int64_t csa, int64_t rsb, int64_t csb, int64_t csc) {
+    if (csa == 1 && csb == 1 && rsb == n && csc == 1) {
+        // gemv_row_rowmajor_block (sgemv.inl:98-230): C = beta*C, then for each
+        // p: C[j] = fma(alpha*A[p], B[p][j], C[j]) in p order. Column tails
+        // (width % 8) use a scalar sum of up to 8 products added to C.
+        if (beta == 0.0f) std::fill(C, C + n, 0.0f);
+        else if (beta != 1.0f) for (int j = 0; j < n; ++j) C[j] *= beta;
+        const int vec_w = (n / 8) * 8;
+        int p = 0;
+        auto tail = [&](int p0, int cnt) {
+            for (int j = vec_w; j < n; ++j) {
+                // c += a0*b0 + a1*b1 + ... as contracted by the reference build:
+                // s = fma(a0, b0, a1*b1); s = fma(a_q, b_q, s) for q >= 2; c = c + s.
+                auto bq = [&](int q) { return B[static_cast<int64_t>(p0 + q) * n + j]; };
+                float s = std::fma(alpha * A[p0], bq(0), (alpha * A[p0 + 1]) * bq(1));
+                for (int q = 2; q < cnt; ++q) s = std::fma(alpha * A[p0 + q], bq(q), s);
+                C[j] += s;
+            }
+        };
+        for (; p + 8 <= k; p += 8) {
+            for (int q = 0; q < 8; ++q) {
+                float a = alpha * A[p + q];
+                const float* b = B + static_cast<int64_t>(p + q) * n;
+                for (int j = 0; j < vec_w; ++j) C[j] = std::fma(a, b[j], C[j]);
+            }
+            tail(p, 8);
+        }
+        for (; p + 4 <= k; p += 4) {
+            for (int q = 0; q < 4; ++q) {
+                float a = alpha * A[p + q];
+                const float* b = B + static_cast<int64_t>(p + q) * n;
+                for (int j = 0; j < vec_w; ++j) C[j] = std::fma(a, b[j], C[j]);
+            }
+            tail(p, 4);
+        }
+        for (; p < k; ++p) {
+            float a = alpha * A[p];
+            const float* b = B + static_cast<int64_t>(p) * n;
+            for (int j = 0; j < vec_w; ++j) C[j] = std::fma(a, b[j], C[j]);
+            for (int j = vec_w; j < n; ++j) C[j] = std::fma(a, b[j], C[j]);
+        }
+        return;
+    }
+    if (csa == 1 && rsb == 1 && csc == 1) {
+        // gemv_row_colmajor_kernel<4> (sgemv.inl:379-425): full groups of 4
+        // columns use gemv_dot_ncols<4>; leftover columns use sdot_contiguous.
+        const int full = (n / 4) * 4;
+        for (int j = 0; j < n; ++j) {
+            const float* bcol = B + static_cast<int64_t>(j) * csb;
+            float s = (j < full) ? dot_2x8(A, bcol, k) : dot_4x8(A, bcol, k);
+            C[j] = (beta == 0.0f) ? alpha * s : alpha * s + beta * C[j];
+        }
+        return;
+    }
+    // Remaining strided layouts (sgemv.inl:459-717): sequential per-column dot
+    // products. Not on the configured path; ulp-level only.
+    for (int j = 0; j < n; ++j) {
+        float s = dot_strided(A, B + static_cast<int64_t>(j) * csb, k, csa, rsb);
+        C[j * csc] = alpha * s + beta * C[j * csc];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Blocked GEMM: src/kernel/avx2/sgemm.inl:268-340 (sgemm_rowmajor) and the
+// exact-layout dispatch at 611-715. For alpha=1, beta=0 every exact-layout
+// route (row/row/row, col/col/col, W^T cache, A^T cache) computes each output
+// as one FMA chain over k = 0..K-1 starting from +0: later kc panels reload C
+// and continue the chain (kernel_row_full_accum_fast, 174-202).
+// Implementation: row-major staging of B, then C[i][:] updated rank-1 per p in
+// p order (identical chain per element), OpenMP over rows.
+// ---------------------------------------------------------------------------
+void gemm_chain(const float* A, int64_t rsa, int64_t csa, const float* B, int64_t rsb, int64_t csb,
+                float* C, int64_t rsc, int64_t csc, int m, int n, int k) {
+    std::vector<float> Bt(static_cast<size_t>(k) * n);
+#pragma omp parallel for schedule(static)
+    for (int p = 0; p < k; ++p)
+        for (int j = 0; j < n; ++j) Bt[static_cast<size_t>(p) * n + j] = B[p * rsb + j * csb];
+#pragma omp parallel
+    {
+        std::vector<float> crow(n);
+#pragma omp for schedule(static)
+        for (int i = 0; i < m; ++i) {
+            std::fill(crow.begin(), crow.end(), 0.0f);
+            for (int p = 0; p < k; ++p) {
+                const float a = A[i * rsa + p * csa];
+                const float* b = &Bt[static_cast<size_t>(p) * n];
+                float* c = crow.data();
+                for (int j = 0; j < n; ++j) c[j] = std::fma(a, b[j], c[j]);
+            }
+            for (int j = 0; j < n; ++j) C[i * rsc + j * csc] = crow[j];
+        }
+    }
+}
+
+constexpr int KC_DEFAULT = 500;  // include/kernel/avx2/gemm_utils.hpp:55 (g_gemm_kc)
+
+void sgemm_full(const float* A, const float* B, float* C, int m, int n, int k, float alpha, float beta,
+                int64_t rsa, int64_t csa, int64_t rsb, int64_t csb, int64_t rsc, int64_t csc) {
+    // src/kernel/avx2/sgemm.inl:594-609: empty and degenerate shapes.
+    if (m == 0 || n == 0) return;
+    if (k == 0 || alpha == 0.0f) {
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j) {
+                float& c = C[i * rsc + j * csc];
+                c = (beta == 0.0f) ? 0.0f : (beta != 1.0f ? c * beta : c);
+            }
+        return;
+    }
+    if (m == 1 && n == 1) {
+        float s = (csa == 1 && rsb == 1) ? dot_4x8(A, B, k) : dot_strided(A, B, k, csa, rsb);
+        *C = alpha * s + beta * (*C);
+        return;
+    }
+    if (k == 1) {
+        // sger (src/kernel/avx2/sger.inl:5-78): C = (alpha*x_i)*y_j [+ beta*C]
+        for (int i = 0; i < m; ++i) {
+            float a = alpha * A[i * rsa];
+            for (int j = 0; j < n; ++j) {
+                float& c = C[i * rsc + j * csc];
+                c = (beta == 0.0f) ? a * B[j * csb] : std::fma(a, B[j * csb], beta * c);
+            }
+        }
+        return;
+    }
+    if (m == 1) { gemv_row(A, B, C, n, k, alpha, beta, csa, rsb, csb, csc); return; }
+    if (n == 1) {
+        // gemv_col_simd (sgemv.inl:719-768) -> gemv_col_rowmajor_contiguous_range
+        // (sgemv.inl:58-96): one 8-lane accumulator over 8-steps, hsum, FMA tail,
+        // C = fma(alpha, sum, beta*C).
+        for (int i = 0; i < m; ++i) {
+            const float* a = A + i * rsa;
+            float s;
+            if (csa == 1 && rsb == 1) {
+                float acc[8] = {0};
+                int p = 0;
+                for (; p + 8 <= k; p += 8)
+                    for (int l = 0; l < 8; ++l) acc[l] = std::fma(a[p + l], B[p + l], acc[l]);
+                s = hsum8(acc);
+                for (; p < k; ++p) s = std::fma(a[p], B[p], s);
+            } else {
+                s = dot_strided(a, B, k, csa, rsb);
+            }
+            C[i * rsc] = std::fma(alpha, s, beta * C[i * rsc]);
+        }
+        return;
+    }
+    const bool a_exact = (csa == 1 && rsa == k) || (rsa == 1 && csa == m);
+    const bool b_exact = (csb == 1 && rsb == n) || (rsb == 1 && csb == k);
+    const bool c_row_exact = (csc == 1 && rsc == n);
+    const bool c_col_exact = (rsc == 1 && csc == m);
+    if (alpha == 1.0f && beta == 0.0f && a_exact && b_exact && (c_row_exact || c_col_exact)) {
+        gemm_chain(A, rsa, csa, B, rsb, csb, C, rsc, csc, m, n, k);
+        return;
+    }
+    // Generic path (sgemm.inl:717-787): per kc=500 panel, an FMA chain from 0
+    // combined into C by the store kernels.
+    const bool c_rowmajor = (csc == 1 && rsc >= n);
+    std::vector<float> part(static_cast<size_t>(m) * n);
+    for (int pp = 0; pp < k; pp += KC_DEFAULT) {
+        const int kc = std::min(KC_DEFAULT, k - pp);
+        const bool first = (pp == 0);
+        gemm_chain(A + pp * csa, rsa, csa, B + pp * rsb, rsb, csb, part.data(), n, 1, m, n, kc);
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j) {
+                float& c = C[i * rsc + j * csc];
+                const float t = part[static_cast<size_t>(i) * n + j];
+                if (c_rowmajor && alpha == 1.0f) {
+                    // kernel_row_zero / kernel_row_load continue the chain; the
+                    // first panel with beta != 0 pre-scales C.
+                    if (first) c = (beta == 0.0f) ? t : t + c * beta;  // approximate for beta != 0
+                    else c = c + t;
+                } else if (c_rowmajor) {
+                    // kernel_row_alphabeta (gemm_utils.inl:267-292)
+                    float v = t * alpha;
+                    if (first && beta != 0.0f) v = std::fma(beta, c, v);
+                    else if (!first) v = v + c;
+                    c = v;
+                } else {
+                    // kernel_row_generic_store (gemm_utils.inl:294-315)
+                    float v = alpha * t;
+                    v = first ? v + beta * c : v + c;
+                    c = v;
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Flash attention, one (batch, head) matrix.
+// src/kernel/avx2/flash_attention.inl:274-443 (_flashAttentionImpl, prefill)
+// and 202-272 (_flashAttentionDecodeGemvImpl, q_len == 1).
+// mask: nullptr = all visible; otherwise byte mask [q_len, mask_stride].
+// ---------------------------------------------------------------------------
+constexpr int NR = 16;  // include/kernel/avx2/gemm_utils.hpp:48 (NR_ROW): keys per tile
+
+struct MaskView {
+    const uint8_t* data; int64_t stride;
+    bool operator()(int r, int c) const { return data == nullptr || data[r * stride + c] != 0; }
+};
+
+void flash_decode(const float* Q, const float* K, const float* V, float* O, int kv_len, int hd, int dv,
+                  float scale, int64_t csq, int64_t rsk, int64_t csk, int64_t rsv, int64_t csv, int64_t cso,
+                  MaskView mask, const float* bias, int64_t rsb, int64_t csb) {
+    (void)rsb;
+    std::vector<float> s(kv_len);
+    // scores = scale * (q . k_j) through gemv_row_simd(Q, K^T, ..., alpha=scale)
+    gemv_row(Q, K, s.data(), kv_len, hd, scale, 0.0f, csq, csk, rsk, 1);
+    float mx = -std::numeric_limits<float>::infinity();
+    bool any = false;
+    for (int c = 0; c < kv_len; ++c) {
+        if (!mask(0, c)) { s[c] = -std::numeric_limits<float>::infinity(); continue; }
+        s[c] += bias ? bias[c * csb] : 0.0f;
+        mx = std::max(mx, s[c]);
+        any = true;
+    }
+    auto zero = [&]() { for (int d = 0; d < dv; ++d) O[d * cso] = 0.0f; };
+    if (!any) { zero(); return; }
+    float sum = 0.0f;
+    for (int c = 0; c < kv_len; ++c) {
+        if (!mask(0, c)) { s[c] = 0.0f; continue; }
+        s[c] = std::exp(s[c] - mx);
+        sum += s[c];
+    }
+    if (sum == 0.0f) { zero(); return; }
+    const float inv = 1.0f / sum;
+    for (int c = 0; c < kv_len; ++c) s[c] *= inv;
+    // O = P . V through gemv_row_simd(scores, V, ...)
+    gemv_row(s.data(), V, O, dv, kv_len, 1.0f, 0.0f, 1, rsv, csv, cso);
+}
+
+void flash_prefill(const float* Q, const float* K, const float* V, float* O, int q_len, int kv_len, int hd,
+                   int dv, float scale, int64_t rsq, int64_t csq, int64_t rsk, int64_t csk, int64_t rsv,
+                   int64_t csv, int64_t rso, int64_t cso, MaskView mask, const float* bias, int64_t rsb,
+                   int64_t csb) {
+    if (q_len == 0 || kv_len == 0 || hd == 0 || dv == 0) return;
+    const float NEG_INF = -std::numeric_limits<float>::infinity();
+    for (int i = 0; i < q_len; ++i) {
+        float* orow = O + i * rso;
+        for (int d = 0; d < dv; ++d) orow[d * cso] = 0.0f;
+        float row_max = NEG_INF, row_l = 0.0f;
+        float score[NR], prob[NR];
+        bool vis[NR];
+        for (int kj = 0; kj < kv_len; kj += NR) {
+            const int nr = std::min(NR, kv_len - kj);
+            // Score tile: FMA chain over d from 0 (dispatch_fma_row, gemm_utils.inl:225-260).
+            bool any_vis = false;
+            for (int j = 0; j < nr; ++j) {
+                vis[j] = mask(i, kj + j);
+                any_vis |= vis[j];
+            }
+            if (!any_vis) continue;  // the row contributes nothing to this tile (flash_attention.inl:377-379)
+            for (int j = 0; j < nr; ++j) {
+                float acc = 0.0f;
+                const float* q = Q + i * rsq;
+                const float* k = K + static_cast<int64_t>(kj + j) * rsk;
+                for (int d = 0; d < hd; ++d) acc = std::fma(q[d * csq], k[d * csk], acc);
+                score[j] = acc;
+            }
+            // flash_attention.inl:361-398: scale (+bias), running max, exp, new l.
+            float tile_max = NEG_INF;
+            for (int j = 0; j < nr; ++j) {
+                if (!vis[j]) { prob[j] = 0.0f; continue; }
+                const float sc = bias ? score[j] * scale + bias[i * rsb + (kj + j) * csb] : score[j] * scale;
+                prob[j] = sc;
+                tile_max = std::max(tile_max, sc);
+            }
+            const float prev_max = row_max;
+            const float new_max = std::max(prev_max, tile_max);
+            const float prev_scale = std::isfinite(prev_max) ? std::exp(prev_max - new_max) : 0.0f;
+            float tile_sum = 0.0f;
+            for (int j = 0; j < nr; ++j) {
+                if (!vis[j]) continue;
+                const float p = std::exp(prob[j] - new_max);
+                prob[j] = p;
+                tile_sum += p;
+            }
+            const float l_scaled = row_l * prev_scale;  // shared with the rescale below
+            const float new_l = l_scaled + tile_sum;
+            if (new_l == 0.0f) continue;
+            const float rescale = row_l == 0.0f ? 0.0f : (l_scaled / new_l);
+            // flash_attention.inl:402-404: rows whose (l, max) did not change are skipped.
+            if (new_l == row_l && new_max == row_max) continue;
+            const float inv_new_l = 1.0f / new_l;
+            // _flashAccumulateRowContiguous (160-200): O = O*rescale, then FMA of
+            // (p_j * inv_new_l) * v_j over the tile's keys, skipping p_j == 0.
+            for (int d = 0; d < dv; ++d) {
+                float acc = (rescale == 0.0f) ? 0.0f : orow[d * cso] * rescale;
+                for (int j = 0; j < nr; ++j) {
+                    if (prob[j] == 0.0f) continue;
+                    acc = std::fma(prob[j] * inv_new_l, V[static_cast<int64_t>(kj + j) * rsv + d * csv], acc);
+                }
+                orow[d * cso] = acc;
+            }
+            row_max = new_max;
+            row_l = new_l;
+        }
+    }
+}
+
+}  // namespace
+
+// ===========================================================================
+// Exported C ABI (ctypes from tests/ and bench.py)
+// ===========================================================================
+
+OEXPORT int oracle_abi_version(void) { return 1; }
+
+OEXPORT void oracle_bf16_round(const float* x, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = bf16_round(x[i]);
+}
+OEXPORT void oracle_bf16_to_f32(const uint16_t* x, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = bf16_to_f32(x[i]);
+}
+OEXPORT void oracle_f16_round(const float* x, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f16_round(x[i]);
+}
+OEXPORT void oracle_f16_to_f32(const uint16_t* x, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(x[i]);
+}
+
+// YTensor<float,N>::seed(s): reseeds the shared generator.
+OEXPORT void oracle_seed(uint32_t s) { g_gen.seed(s); }
+// YTensor<float,N>::randn(...): n values, one fresh normal_distribution<double>.
+OEXPORT void oracle_randn(float* out, int64_t n) {
+    std::normal_distribution<double> dist(0.0, 1.0);
+    for (int64_t i = 0; i < n; ++i) out[i] = static_cast<float>(dist(g_gen));
+}
+
+OEXPORT void oracle_sgemm(const float* A, const float* B, float* C, int m, int n, int k, float alpha, float beta,
+                          int64_t rsa, int64_t csa, int64_t rsb, int64_t csb, int64_t rsc, int64_t csc) {
+    sgemm_full(A, B, C, m, n, k, alpha, beta, rsa, csa, rsb, csb, rsc, csc);
+}
+
+// One-matrix flash attention with the reference's kernel signature
+// (include/kernel/avx2/flash_attention.hpp:21-44); mask bytes are bools.
+OEXPORT void oracle_flash_attention(const float* Q, const float* K, const float* V, float* O, int q_len,
+                                    int kv_len, int head_dim, int value_dim, float scale, int64_t rsq,
+                                    int64_t csq, int64_t rsk, int64_t csk, int64_t rsv, int64_t csv, int64_t rso,
+                                    int64_t cso, const uint8_t* mask, int64_t mask_stride, const float* bias,
+                                    int64_t rsbias, int64_t csbias) {
+    MaskView mv{mask, mask_stride};
+    if (q_len == 1)
+        flash_decode(Q, K, V, O, kv_len, head_dim, value_dim, scale, csq, rsk, csk, rsv, csv, cso, mv, bias,
+                     rsbias, csbias);
+    else
+        flash_prefill(Q, K, V, O, q_len, kv_len, head_dim, value_dim, scale, rsq, csq, rsk, csk, rsv, csv, rso,
+                      cso, mv, bias, rsbias, csbias);
+}
+
+// Batched GQA SDPA over contiguous [B,H,S,D] tensors, as the qwen3 example
+// drives it (example/qwen3/src/qwen3.cpp:252-264): q-head h reads kv-head
+// h / (Hq/Hkv); causal mask ki <= (kv_len - q_len) + qi (qwen3.cpp:46-55,
+// 104-126); scale 0 means 1/sqrt(D) (src/function/ops.inl:378-381).
+// OpenMP over (batch, head) as broadcastInplace does (src/kernel/broadcast.inl:391-445).
+OEXPORT void oracle_sdpa_gqa(const float* Q, const float* K, const float* V, float* O, int B, int Hq, int Hkv,
+                             int q_len, int kv_len, int D, float scale, int causal) {
+    if (scale == 0.0f) scale = 1.0f / std::sqrt(static_cast<float>(D));
+    const int G = Hq / Hkv;
+    std::vector<uint8_t> mask;
+    if (causal) {
+        mask.resize(static_cast<size_t>(q_len) * kv_len);
+        const int off = kv_len - q_len;
+        for (int i = 0; i < q_len; ++i)
+            for (int j = 0; j < kv_len; ++j) mask[static_cast<size_t>(i) * kv_len + j] = (j <= off + i) ? 1 : 0;
+    }
+    const uint8_t* mp = causal ? mask.data() : nullptr;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int bh = 0; bh < B * Hq; ++bh) {
+        const int b = bh / Hq, h = bh % Hq, kh = h / G;
+        const float* q = Q + (static_cast<int64_t>(b) * Hq + h) * q_len * D;
+        const float* k = K + (static_cast<int64_t>(b) * Hkv + kh) * kv_len * D;
+        const float* v = V + (static_cast<int64_t>(b) * Hkv + kh) * kv_len * D;
+        float* o = O + (static_cast<int64_t>(b) * Hq + h) * q_len * D;
+        oracle_flash_attention(q, k, v, o, q_len, kv_len, D, D, scale, D, 1, D, 1, D, 1, D, 1, mp, kv_len,
+                               nullptr, 0, 0);
+    }
+}
+
+// rmsNorm_ over the last axis of a contiguous [rows, n] tensor:
+// src/function/normalization.inl:256-267 -> _rmsAxes_ (33-54): mean of x*x by
+// YTensor::mean(axis) (src/ytensor_math.inl:532-553, running mean
+// m += (x - m)/(j+1)), then a /= sqrt(m + eps); _applyScale_ (88-101): a *= w.
+OEXPORT void oracle_rms_norm(float* x, const float* w, int64_t rows, int n, float eps) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        float* a = x + r * n;
+        float m = 0.0f;
+        for (int j = 0; j < n; ++j) {
+            const float sq = a[j] * a[j];
+            m += (sq - m) / static_cast<float>(j + 1);
+        }
+        const float den = std::sqrt(m + eps);
+        for (int j = 0; j < n; ++j) {
+            a[j] /= den;
+            a[j] *= w[j];
+        }
+    }
+}
+
+// RoPECache::precompute: example/qwen3/src/qwen3.cpp:161-175. Tables [max_len, dim].
+OEXPORT void oracle_rope_precompute(int dim, int max_len, float theta, float* cosv, float* sinv) {
+    const int half = dim / 2;
+    for (int t = 0; t < max_len; ++t)
+        for (int i = 0; i < half; ++i) {
+            const float freq = 1.0f / std::pow(theta, 2.0f * i / dim);
+            const float angle = t * freq;
+            cosv[t * dim + i] = cosv[t * dim + i + half] = std::cos(angle);
+            sinv[t * dim + i] = sinv[t * dim + i + half] = std::sin(angle);
+        }
+}
+
+// ops::rope on one tensor [B,H,L,D] (contiguous): example/qwen3/src/qwen3.cpp:522-559.
+// Position li reads table row li (the caller passes tables sliced to the
+// positions). x1' = x1*c - x2*s ; x2' = x2*c + x1*s over halves [0,D/2), [D/2,D).
+OEXPORT void oracle_rope(float* x, int B, int H, int L, int D, const float* cosv, const float* sinv) {
+    const int half = D / 2;
+    for (int64_t bhl = 0; bhl < static_cast<int64_t>(B) * H * L; ++bhl) {
+        const int li = static_cast<int>(bhl % L);
+        float* r = x + bhl * D;
+        for (int d = 0; d < half; ++d) {
+            const float c = cosv[li * D + d], s = sinv[li * D + d];
+            const float x1 = r[d], x2 = r[d + half];
+            r[d] = std::fma(x1, c, -(x2 * s));
+            r[d + half] = std::fma(x2, c, x1 * s);
+        }
+    }
+}
+
+OEXPORT int oracle_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+OEXPORT void oracle_set_num_threads(int t) {
+#ifdef _OPENMP
+    if (t > 0) omp_set_num_threads(t);
+#else
+    (void)t;
+#endif
+}
