@@ -1,0 +1,144 @@
+/*
+ * ythip.h — C ABI of libythip.so, the MI355X (gfx950) back end for YTensor's
+ * two hot operators (SnifferCaptain/ytensor v0.13): the blocked GEMM behind
+ * YTensor::matmul / yt::function::linear, and the SDPA / flash-attention
+ * forward behind yt::function::scaledDotProductAttention, plus the fused
+ * RMSNorm+RoPE that sits between them in the Qwen3 example.
+ *
+ * Conventions (shared by every entry point):
+ *   - All tensor pointers are DEVICE pointers; sizes are int, element strides
+ *     int64 (as in the reference's kernel API), in ELEMENTS, not bytes.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Calls are
+ *     asynchronous on that stream and re-entrant across streams.
+ *   - Return value: 0 on success, a negative YTHIP_E* code for argument errors
+ *     (nothing was launched), or a positive hipError_t from the launch.
+ *     ythip_last_error() returns the calling thread's last message.
+ *   - No entry point allocates device memory: scratch space is passed in.
+ *   - No C++ exceptions cross this boundary.
+ */
+#ifndef YTHIP_H
+#define YTHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types: the reference's fp32 / float16 / bfloat16 type set
+ * (include/ytensor_types.hpp:137-175; include/types/bfloat16.hpp;
+ * include/types/float_spec.hpp:533). */
+enum ythip_dtype { YTHIP_F32 = 0, YTHIP_F16 = 1, YTHIP_BF16 = 2 };
+
+enum ythip_status {
+    YTHIP_OK = 0,
+    YTHIP_EINVAL = -1,      /* bad argument (shape, stride, pointer, dtype) */
+    YTHIP_EUNSUPPORTED = -2 /* valid but not implemented combination */
+};
+
+/* Attention mask kinds. */
+enum ythip_mask_kind {
+    YTHIP_MASK_NONE = 0,   /* every key visible */
+    YTHIP_MASK_CAUSAL = 1, /* key j visible to query i iff j <= (kv_len - q_len) + i
+                              (example/qwen3/src/qwen3.cpp:46-55) */
+    YTHIP_MASK_BOOL = 2    /* byte mask [q_len, mask_ld]; nonzero = visible
+                              (include/kernel/avx2/flash_attention.hpp:21-44 `const bool* mask`) */
+};
+
+/* ABI version of this header; bumped on any signature change. */
+int ythip_abi_version(void);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* ythip_last_error(void);
+
+/*
+ * Batched strided GEMM:  C[b] = alpha * A[b] . B[b] + beta * C[b]
+ *   A[b]: m x k at A + b*sa_b, element (i,p) at i*rsa + p*csa
+ *   B[b]: k x n at B + b*sb_b, element (p,j) at p*rsb + j*csb   (sb_b = 0: shared weight)
+ *   C[b]: m x n at C + b*sc_b, element (i,j) at i*rsc + j*csc
+ * Replaces yt::kernel::avx2::sgemm (include/kernel/avx2/sgemm.hpp:51-58) and
+ * hgemm (include/kernel/avx2/hgemm.hpp:26-33) for device-resident operands, and
+ * the per-matrix loop of YTensor::matmul (src/ytensor_math.inl:954-1051).
+ * dtype_in: F32, F16 or BF16 (A and B share it). Accumulation is fp32.
+ * dtype_out: same as dtype_in, or F32 (fp32 diagnostics output) for 16-bit input.
+ * `linear(x, W)` is B = W^T, i.e. rsb = 1, csb = ldW (src/function/ops.inl:84-91).
+ * Semantics at the edges follow sgemm.inl:594-604: m == 0 or n == 0 is a no-op;
+ * k == 0 or alpha == 0 scales C by beta (beta == 0 writes zeros).
+ */
+int ythip_gemm(int dtype_in, int dtype_out, int batch, int m, int n, int k,
+               const void* A, int64_t sa_b, int64_t rsa, int64_t csa,
+               const void* B, int64_t sb_b, int64_t rsb, int64_t csb,
+               void* C, int64_t sc_b, int64_t rsc, int64_t csc,
+               float alpha, float beta, void* stream);
+
+/*
+ * Attention forward, prefill (any q_len >= 1):
+ *   O[b,h] = softmax(scale * Q[b,h] . K[b,h/G]^T + bias, masked) . V[b,h/G],  G = Hq / Hkv
+ * Q: [B,Hq,q_len,d], K: [B,Hkv,kv_len,d], V: [B,Hkv,kv_len,dv], O: [B,Hq,q_len,dv];
+ * each *_str gives the 4 element strides (batch, head, row, col); col stride must be 1.
+ * scale == 0 means 1/sqrt(d) (src/function/ops.inl:378-381).
+ * bias (fp32, optional): [q_len, kv_len] at bias + i*rs_bias + j*cs_bias, added after scaling.
+ * Rows with no visible key produce zeros (src/kernel/avx2/flash_attention.inl:241-244, 327-331).
+ * Replaces the per-(batch, head) loop of _scaledDotProductAttentionFlash
+ * (src/function/ops.inl:109-234) over yt::kernel::avx2::flash_attention
+ * (include/kernel/avx2/flash_attention.hpp:21-69). Supported: d == dv in {64, 128}.
+ */
+int ythip_attn_prefill(int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv,
+                       const void* Q, const int64_t q_str[4],
+                       const void* K, const int64_t k_str[4],
+                       const void* V, const int64_t v_str[4],
+                       void* O, const int64_t o_str[4],
+                       float scale, int mask_kind, const uint8_t* mask, int64_t mask_ld,
+                       const float* bias, int64_t rs_bias, int64_t cs_bias, void* stream);
+
+/*
+ * Single-query decode attention over a KV cache (the q_len == 1 path,
+ * src/kernel/avx2/flash_attention.inl:202-272), split over the context:
+ *   Q: [B,Hq,d] with strides q_str[0..1] (batch, head), contiguous d
+ *   Kc/Vc: [B,Hkv,max_ctx,d] with strides kv_str (batch, head, pos); contiguous d
+ *   kv_len: device int32[B] (keys [0, kv_len[b]) are visible) or NULL = max_ctx for all
+ *   O: [B,Hq,d] with strides o_str[0..1]
+ * workspace: device scratch of ythip_attn_decode_workspace_size(B, Hq, max_ctx, d) bytes.
+ */
+size_t ythip_attn_decode_workspace_size(int B, int Hq, int max_ctx, int d);
+int ythip_attn_decode(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
+                      const void* Q, const int64_t q_str[2],
+                      const void* Kc, const void* Vc, const int64_t kv_str[3],
+                      const int32_t* kv_len, void* O, const int64_t o_str[2],
+                      float scale, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Fused per-head RMSNorm + rotate-half RoPE on the fused qkv projection output,
+ * scattering Q to [B,Hq,S,d] and K/V into cache rows cache_pos + s:
+ *   qkv: rows of (Hq + 2*Hkv)*d elements, row (b*S + s) at qkv + (b*S+s)*ld_qkv;
+ *        q heads, then k heads, then v heads (example/qwen3/src/qwen3.cpp:233-238)
+ *   q, k <- rmsNorm_(x, w, -1, eps) (src/function/normalization.inl:256-267)
+ *   q, k <- rope with table row (pos0 + s) (example/qwen3/src/qwen3.cpp:522-559)
+ *   v    <- copied unchanged
+ * wq / wk (fp32 [d]) may be NULL to skip that norm; cos/sin (fp32 [*, ld_tab],
+ * from RoPECache::precompute, qwen3.cpp:161-175) may be NULL to skip RoPE.
+ * Output strides are (batch, head, row); d is contiguous. K/V outputs may be NULL.
+ */
+int ythip_rmsnorm_rope(int dtype, int B, int S, int Hq, int Hkv, int d,
+                       const void* qkv, int64_t ld_qkv,
+                       const float* wq, const float* wk, float eps,
+                       const float* cos_tab, const float* sin_tab, int64_t ld_tab, int pos0,
+                       void* Qout, const int64_t q_str[3],
+                       void* Kout, const int64_t k_str[3],
+                       void* Vout, const int64_t v_str[3],
+                       int cache_pos, void* stream);
+
+/*
+ * RMSNorm over the last axis of [rows, n] (the hidden-state norms of the Qwen3
+ * layers, src/function/normalization.inl:256-267): y = x / sqrt(mean(x^2)+eps) * w.
+ * x/y rows at stride ld_x / ld_y (in place allowed); w fp32 [n].
+ */
+int ythip_rms_norm(int dtype, int rows, int n, const void* x, int64_t ld_x,
+                   const float* w, float eps, void* y, int64_t ld_y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YTHIP_H */

@@ -240,19 +240,28 @@ void gemm_chain(const float* A, int64_t rsa, int64_t csa, const float* B, int64_
 #pragma omp parallel for schedule(static)
     for (int p = 0; p < k; ++p)
         for (int j = 0; j < n; ++j) Bt[static_cast<size_t>(p) * n + j] = B[p * rsb + j * csb];
+    // Cache blocking over (8 rows) x (1024 columns); the k loop stays innermost
+    // per block in p order, so each element's chain is unchanged.
+    constexpr int RB = 8, JB = 1024;
+    const int nrb = (m + RB - 1) / RB, njb = (n + JB - 1) / JB;
 #pragma omp parallel
     {
-        std::vector<float> crow(n);
-#pragma omp for schedule(static)
-        for (int i = 0; i < m; ++i) {
-            std::fill(crow.begin(), crow.end(), 0.0f);
+        std::vector<float> cblk(static_cast<size_t>(RB) * JB);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t blk = 0; blk < static_cast<int64_t>(nrb) * njb; ++blk) {
+            const int i0 = static_cast<int>(blk / njb) * RB, j0 = static_cast<int>(blk % njb) * JB;
+            const int ri = std::min(RB, m - i0), jw = std::min(JB, n - j0);
+            std::fill(cblk.begin(), cblk.end(), 0.0f);
             for (int p = 0; p < k; ++p) {
-                const float a = A[i * rsa + p * csa];
-                const float* b = &Bt[static_cast<size_t>(p) * n];
-                float* c = crow.data();
-                for (int j = 0; j < n; ++j) c[j] = std::fma(a, b[j], c[j]);
+                const float* b = &Bt[static_cast<size_t>(p) * n + j0];
+                for (int r = 0; r < ri; ++r) {
+                    const float a = A[(i0 + r) * rsa + p * csa];
+                    float* c = &cblk[static_cast<size_t>(r) * JB];
+                    for (int j = 0; j < jw; ++j) c[j] = std::fma(a, b[j], c[j]);
+                }
             }
-            for (int j = 0; j < n; ++j) C[i * rsc + j * csc] = crow[j];
+            for (int r = 0; r < ri; ++r)
+                for (int j = 0; j < jw; ++j) C[(i0 + r) * rsc + (j0 + j) * csc] = cblk[static_cast<size_t>(r) * JB + j];
         }
     }
 }
@@ -399,27 +408,36 @@ void flash_prefill(const float* Q, const float* K, const float* V, float* O, int
                    int64_t csb) {
     if (q_len == 0 || kv_len == 0 || hd == 0 || dv == 0) return;
     const float NEG_INF = -std::numeric_limits<float>::infinity();
+    // K packed per 16-key tile as [d][16] (pack_b_generic, flash_attention.inl:302-305)
+    // so each score chain over d runs for 16 keys side by side.
+    const int ntiles = (kv_len + NR - 1) / NR;
+    std::vector<float> kp(static_cast<size_t>(ntiles) * hd * NR, 0.0f);
+    for (int t = 0; t < ntiles; ++t)
+        for (int j = 0; j < NR && t * NR + j < kv_len; ++j)
+            for (int d = 0; d < hd; ++d)
+                kp[(static_cast<size_t>(t) * hd + d) * NR + j] = K[static_cast<int64_t>(t * NR + j) * rsk + d * csk];
+    std::vector<float> acc(dv);
     for (int i = 0; i < q_len; ++i) {
         float* orow = O + i * rso;
         for (int d = 0; d < dv; ++d) orow[d * cso] = 0.0f;
+        const float* q = Q + i * rsq;
         float row_max = NEG_INF, row_l = 0.0f;
         float score[NR], prob[NR];
         bool vis[NR];
         for (int kj = 0; kj < kv_len; kj += NR) {
             const int nr = std::min(NR, kv_len - kj);
-            // Score tile: FMA chain over d from 0 (dispatch_fma_row, gemm_utils.inl:225-260).
             bool any_vis = false;
             for (int j = 0; j < nr; ++j) {
                 vis[j] = mask(i, kj + j);
                 any_vis |= vis[j];
             }
             if (!any_vis) continue;  // the row contributes nothing to this tile (flash_attention.inl:377-379)
-            for (int j = 0; j < nr; ++j) {
-                float acc = 0.0f;
-                const float* q = Q + i * rsq;
-                const float* k = K + static_cast<int64_t>(kj + j) * rsk;
-                for (int d = 0; d < hd; ++d) acc = std::fma(q[d * csq], k[d * csk], acc);
-                score[j] = acc;
+            // Score tile: FMA chain over d from 0 (dispatch_fma_row, gemm_utils.inl:225-260).
+            for (int j = 0; j < NR; ++j) score[j] = 0.0f;
+            const float* kt = &kp[static_cast<size_t>(kj / NR) * hd * NR];
+            for (int d = 0; d < hd; ++d) {
+                const float qd = q[d * csq];
+                for (int j = 0; j < NR; ++j) score[j] = std::fma(qd, kt[d * NR + j], score[j]);
             }
             // flash_attention.inl:361-398: scale (+bias), running max, exp, new l.
             float tile_max = NEG_INF;
@@ -447,15 +465,15 @@ void flash_prefill(const float* Q, const float* K, const float* V, float* O, int
             if (new_l == row_l && new_max == row_max) continue;
             const float inv_new_l = 1.0f / new_l;
             // _flashAccumulateRowContiguous (160-200): O = O*rescale, then FMA of
-            // (p_j * inv_new_l) * v_j over the tile's keys, skipping p_j == 0.
-            for (int d = 0; d < dv; ++d) {
-                float acc = (rescale == 0.0f) ? 0.0f : orow[d * cso] * rescale;
-                for (int j = 0; j < nr; ++j) {
-                    if (prob[j] == 0.0f) continue;
-                    acc = std::fma(prob[j] * inv_new_l, V[static_cast<int64_t>(kj + j) * rsv + d * csv], acc);
-                }
-                orow[d * cso] = acc;
+            // (p_j * inv_new_l) * v_j over the tile's keys in key order, skipping p_j == 0.
+            for (int d = 0; d < dv; ++d) acc[d] = (rescale == 0.0f) ? 0.0f : orow[d * cso] * rescale;
+            for (int j = 0; j < nr; ++j) {
+                if (prob[j] == 0.0f) continue;
+                const float w = prob[j] * inv_new_l;
+                const float* vr = V + static_cast<int64_t>(kj + j) * rsv;
+                for (int d = 0; d < dv; ++d) acc[d] = std::fma(w, vr[d * csv], acc[d]);
             }
+            for (int d = 0; d < dv; ++d) orow[d * cso] = acc[d];
             row_max = new_max;
             row_l = new_l;
         }

@@ -1,0 +1,51 @@
+"""CPU checks of the C-ABI boundary: libythip.so loads (no GPU needed to dlopen
+it) and exports every function include/ythip.h declares; argument errors are
+reported without touching the GPU."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ythip.h")
+
+
+def _declared() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ythip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for n in ("ythip_gemm", "ythip_attn_prefill", "ythip_attn_decode", "ythip_rmsnorm_rope", "ythip_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from ytensor_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libythip.so is not built (python -m ytensor_amd.build)")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(_declared()) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_abi_version_and_argument_errors():
+    import ytensor_amd
+    lib = ytensor_amd.load()
+    assert lib.ythip_abi_version() == 1
+    # invalid dtype / negative sizes are rejected before any HIP call
+    st = lib.ythip_gemm(7, 0, 1, 2, 2, 2, None, 0, 2, 1, None, 0, 2, 1, None, 0, 2, 1, 1.0, 0.0, None)
+    assert st == -1 and b"dtype" in lib.ythip_last_error()
+    st = lib.ythip_gemm(0, 0, 1, -2, 2, 2, None, 0, 2, 1, None, 0, 2, 1, None, 0, 2, 1, 1.0, 0.0, None)
+    assert st == -1
+    # m == 0: a no-op that succeeds (src/kernel/avx2/sgemm.inl:594)
+    assert lib.ythip_gemm(0, 0, 1, 0, 2, 2, None, 0, 2, 1, None, 0, 2, 1, None, 0, 2, 1, 1.0, 0.0, None) == 0
+    st = lib.ythip_rmsnorm_rope(2, 1, 1, 1, 1, 96, None, 0, None, None, 1e-6, None, None, 0, 0,
+                                None, None, None, None, None, None, 0, None)
+    assert st == -2  # head dim 96 unsupported

@@ -1,0 +1,185 @@
+"""GPU parity: ythip_attn_prefill / ythip_attn_decode against the oracle's
+restatement of YTensor's FLASH_AVX2 path (src/kernel/avx2/flash_attention.inl).
+
+Tolerances: fp32 max|g-r|/max|r| <= 1e-4; bf16/fp16 <= 2e-2 and MAE <= 1e-3
+(16-bit outputs: max(1e-3, 1.1 * output-rounding floor)) against the fp32 CPU
+result on the up-converted inputs.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from helpers import check16, dev_f32, host_f32, make_input
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(orc, g, r, dtype, label):
+    if dtype == "f32":
+        e = rel_err(g, r)
+        print(f"{label}: rel={e:.3e}", flush=True)
+        assert e <= 1e-4, f"{label}: {e}"
+    else:
+        check16(orc, g, r, dtype, True, label)
+
+
+@pytest.mark.parametrize("S", [512, 2048, 8192])
+def test_config3_causal_prefill_bf16(orc, yt, S):
+    """B=1, 16 q heads, 8 kv heads, d=128, Q,K,V ~ N(0,1) from seed 1
+    (drawn in that order), [B,H,S,D], scale 1/sqrt(128), causal."""
+    orc.seed(1)
+    Q = orc.randn(1, 16, S, 128)
+    K = orc.randn(1, 8, S, 128)
+    V = orc.randn(1, 8, S, 128)
+    Qd, Qh = make_input(orc, Q, "bf16")
+    Kd, Kh = make_input(orc, K, "bf16")
+    Vd, Vh = make_input(orc, V, "bf16")
+    r = orc.sdpa_gqa(Qh, Kh, Vh, 1.0 / math.sqrt(128), True)
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, 1.0 / math.sqrt(128), mask="causal"))
+    check16(orc, g, r, "bf16", True, f"prefill S={S}")
+
+
+CASES = [
+    # (B, Hq, Hkv, Sq, Skv, D, mask)
+    (1, 2, 1, 5, 9, 64, None),
+    (1, 4, 2, 13, 13, 128, "causal"),
+    (2, 4, 4, 70, 70, 128, "causal"),
+    (1, 2, 1, 33, 70, 128, "causal"),     # kv longer than q: causal offset kv-q
+    (1, 2, 2, 130, 130, 64, "causal"),
+    (1, 2, 1, 200, 333, 128, None),
+    (1, 2, 1, 17, 40, 128, "bool"),       # bool mask with a fully masked row
+    (1, 2, 1, 17, 40, 128, "bias"),       # additive bias
+    (1, 4, 1, 64, 64, 128, "causal"),     # GQA 4:1
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(map(str, c)))
+def test_prefill_cases(orc, yt, case, dtype):
+    B, Hq, Hkv, Sq, Skv, D, mk = case
+    rng = np.random.default_rng(Sq * 7 + Skv)
+    Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, dtype)
+    Kd, Kh = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    scale = 1.0 / math.sqrt(D)
+    mask = bias = None
+    mask_np = None
+    bias_np = None
+    if mk == "causal":
+        mask = "causal"
+        mask_np = np.tril(np.ones((Sq, Skv), bool), Skv - Sq)
+    elif mk == "bool":
+        mask_np = rng.random((Sq, Skv)) > 0.4
+        mask_np[3] = False
+        mask = torch.from_numpy(mask_np).cuda()
+    elif mk == "bias":
+        bias_np = rng.standard_normal((Sq, Skv)).astype(np.float32)
+        bias = dev_f32(bias_np)
+    r = np.zeros((B, Hq, Sq, D), np.float32)
+    for b in range(B):
+        for h in range(Hq):
+            kh = h // (Hq // Hkv)
+            r[b, h] = orc.flash_attention(Qh[b, h], Kh[b, kh], Vh[b, kh], scale, mask_np, bias_np)
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask=mask, bias=bias))
+    if mk == "bool":
+        assert np.all(g[:, :, 3] == 0.0)  # fully masked row -> zeros (flash_attention.inl:327-331)
+    _check(orc, g, r, dtype, f"{case} {dtype}")
+
+
+def test_prefill_strided_views(orc, yt):
+    """q/k/v as [B,S,H,D] memory viewed as [B,H,S,D] (the qwen3 permute views)."""
+    rng = np.random.default_rng(4)
+    B, Hq, Hkv, S, D = 2, 4, 2, 48, 128
+    Qm = rng.standard_normal((B, S, Hq, D)).astype(np.float32)
+    Km = rng.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    Vm = rng.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Qm, "bf16")
+    Kd, Kh = make_input(orc, Km, "bf16")
+    Vd, Vh = make_input(orc, Vm, "bf16")
+    g = host_f32(yt.scaled_dot_product_attention(Qd.permute(0, 2, 1, 3), Kd.permute(0, 2, 1, 3),
+                                                  Vd.permute(0, 2, 1, 3), 0.0, mask="causal"))
+    r = orc.sdpa_gqa(Qh.transpose(0, 2, 1, 3), Kh.transpose(0, 2, 1, 3), Vh.transpose(0, 2, 1, 3), 0.0, True)
+    check16(orc, g, r, "bf16", True, "strided")
+
+
+def _decode_inputs(orc, B, ctx, seed=2):
+    orc.seed(seed)
+    K = orc.randn(B, 8, ctx, 128)
+    V = orc.randn(B, 8, ctx, 128)
+    Q = orc.randn(B, 16, 1, 128)
+    return Q, K, V
+
+
+@pytest.mark.parametrize("B,ctx", [(1, 1024), (1, 8192), (16, 1024), (16, 8192)])
+def test_config4_decode_bf16(orc, yt, B, ctx):
+    """one query per sequence over a [B,8,ctx,128] cache; K, V, Q ~
+    N(0,1) from seed 2 drawn in that order; no mask beyond the cache length."""
+    Q, K, V = _decode_inputs(orc, B, ctx)
+    Qd, Qh = make_input(orc, Q, "bf16")
+    Kd, Kh = make_input(orc, K, "bf16")
+    Vd, Vh = make_input(orc, V, "bf16")
+    r = orc.sdpa_gqa(Qh, Kh, Vh, 0.0, True)
+    g = host_f32(yt.decode_attention(Qd, Kd, Vd))
+    check16(orc, g.reshape(r.shape), r, "bf16", True, f"decode B={B} ctx={ctx}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_decode_ragged_lengths(orc, yt, dtype):
+    """Per-sequence cache lengths (kv_len[b]); keys past the length are invisible."""
+    B, Hq, Hkv, ctx, D = 4, 8, 2, 300, 128
+    lens = np.array([1, 77, 300, 128], np.int32)
+    rng = np.random.default_rng(9)
+    Q = rng.standard_normal((B, Hq, 1, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, ctx, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, ctx, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, dtype)
+    Kd, Kh = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    g = host_f32(yt.decode_attention(Qd, Kd, Vd, kv_len=torch.from_numpy(lens).cuda()))
+    r = np.zeros_like(Q)
+    for b in range(B):
+        L = int(lens[b])
+        r[b] = orc.sdpa_gqa(Qh[b:b + 1], np.ascontiguousarray(Kh[b:b + 1, :, :L]),
+                            np.ascontiguousarray(Vh[b:b + 1, :, :L]), 0.0, True)[0]
+    _check(orc, g.reshape(r.shape), r, dtype, f"ragged {dtype}")
+
+
+def test_decode_equals_last_prefill_row(orc, yt):
+    """Decode of the last query == the last row of causal prefill (same inputs)."""
+    rng = np.random.default_rng(12)
+    B, Hq, Hkv, S, D = 1, 16, 8, 257, 128
+    Q = rng.standard_normal((B, Hq, S, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    Qd, _ = make_input(orc, Q, "f32")
+    Kd, _ = make_input(orc, K, "f32")
+    Vd, _ = make_input(orc, V, "f32")
+    pre = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, 0.0, mask="causal"))[:, :, -1]
+    dec = host_f32(yt.decode_attention(Qd[:, :, -1:].contiguous(), Kd, Vd)).reshape(pre.shape)
+    assert rel_err(dec, pre) <= 1e-5
+
+
+def test_single_visible_key_and_zero_query(orc, yt):
+    """Closed forms: one visible key -> O = that V row; Q = 0 -> mean of visible V rows."""
+    rng = np.random.default_rng(13)
+    S, D = 40, 128
+    K = rng.standard_normal((1, 1, S, D)).astype(np.float32)
+    V = rng.standard_normal((1, 1, S, D)).astype(np.float32)
+    Q = rng.standard_normal((1, 1, S, D)).astype(np.float32)
+    m = np.zeros((S, S), bool)
+    m[:, 7] = True
+    g = host_f32(yt.scaled_dot_product_attention(dev_f32(Q), dev_f32(K), dev_f32(V), 0.0,
+                                                 mask=torch.from_numpy(m).cuda()))
+    assert np.allclose(g[0, 0], np.broadcast_to(V[0, 0, 7], (S, D)), rtol=0, atol=1e-6)
+    Z = np.zeros_like(Q)
+    g = host_f32(yt.scaled_dot_product_attention(dev_f32(Z), dev_f32(K), dev_f32(V), 0.0, mask="causal"))
+    expect = np.cumsum(V[0, 0].astype(np.float64), axis=0) / np.arange(1, S + 1)[:, None]
+    assert np.allclose(g[0, 0], expect, rtol=1e-5, atol=1e-5)

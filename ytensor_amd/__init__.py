@@ -1,0 +1,29 @@
+"""ytensor_amd — MI355X (gfx950) back end for YTensor's GEMM and attention hot path.
+
+The product is libythip.so (C ABI in include/ythip.h; HIP kernels in csrc/).
+This package loads it through ctypes and exposes torch-facing operators that
+mirror yt::function (see ops.py). Every operator loads the library on first
+use and fails loudly when it has not been built: there is no CPU fallback.
+"""
+from ._lib import YthipError, lib, LIB_PATH  # noqa: F401
+from .ops import (  # noqa: F401
+    decode_attention,
+    gemm,
+    linear,
+    matmul,
+    rms_norm,
+    rms_norm_rope,
+    scaled_dot_product_attention,
+)
+
+
+def load():
+    """Load libythip.so now; raises ImportError if it is missing and
+    AttributeError if it lacks a symbol that include/ythip.h declares."""
+    return lib()
+
+
+__all__ = [
+    "YthipError", "lib", "gemm", "matmul", "linear", "scaled_dot_product_attention",
+    "decode_attention", "rms_norm", "rms_norm_rope",
+]

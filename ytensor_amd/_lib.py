@@ -1,0 +1,73 @@
+"""ctypes binding of libythip.so (include/ythip.h).
+
+The library is loaded from this package directory only. If it is missing the
+import fails loudly: there is no CPU fallback anywhere in the product path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libythip.so")
+
+F32, F16, BF16 = 0, 1, 2
+MASK_NONE, MASK_CAUSAL, MASK_BOOL = 0, 1, 2
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_LP = ctypes.POINTER(ctypes.c_int64)
+
+# Every symbol include/ythip.h declares, with its ctypes signature.
+SIGNATURES = {
+    "ythip_abi_version": (_I, []),
+    "ythip_last_error": (ctypes.c_char_p, []),
+    "ythip_gemm": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _F, _F, _P]),
+    "ythip_attn_prefill": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _LP, _P, _LP, _P, _LP, _P, _LP,
+                                _F, _I, _P, _L, _P, _L, _L, _P]),
+    "ythip_attn_decode_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I]),
+    "ythip_attn_decode": (_I, [_I, _I, _I, _I, _I, _I, _P, _LP, _P, _P, _LP, _P, _P, _LP, _F, _P,
+                               ctypes.c_size_t, _P]),
+    "ythip_rmsnorm_rope": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _P, _L, _I,
+                                _P, _LP, _P, _LP, _P, _LP, _I, _P]),
+    "ythip_rms_norm": (_I, [_I, _I, _I, _P, _L, _P, _F, _P, _L, _P]),
+}
+
+
+class YthipError(RuntimeError):
+    """A non-zero status from libythip (argument error or HIP error)."""
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise ImportError(
+            f"{path} is not built; run `python -m ytensor_amd.build` (hipcc, gfx950). "
+            "ytensor_amd has no CPU fallback.")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError here = the library lacks a declared symbol
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = load()
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib().ythip_last_error().decode(errors="replace")
+        raise YthipError(f"{what} failed with status {status}: {msg}")
+
+
+def i64array(vals) -> ctypes.Array:
+    return (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])

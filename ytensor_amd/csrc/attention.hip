@@ -1,0 +1,665 @@
+// attention.hip — attention forward for gfx950: MFMA flash-attention prefill,
+// split-context decode, and an any-layout row-wise kernel.
+//
+// Reference semantics (src/kernel/avx2/flash_attention.inl):
+//   prefill 274-443: blockwise online softmax over key tiles, masked entries
+//   excluded (not -1e9), bias added after scaling, rows with no visible key
+//   give 0 (327-331); decode 202-272: scores, max, exp, sum, normalise, P.V.
+//   GQA as in the qwen3 example (example/qwen3/src/qwen3.cpp:250-264): query
+//   head h reads key/value head h / (Hq / Hkv).
+//
+// Prefill kernel (16-bit inputs, d in {64, 128}):
+//   * Workgroup = 4 waves x 32 queries = 128 queries of one (batch, head);
+//     key/value blocks of 64 keys double-buffered in LDS.
+//   * S^T = K . Q^T on v_mfma_f32_16x16x32: src0 = K rows, src1 = Q rows, so
+//     lane l holds 16 scores of ONE query (l % 16) -> the online softmax is
+//     lane-local plus two cross-group shuffles (xor 16, 32) for the max.
+//   * O^T = V^T . P^T: src0 = V^T rows (d), src1 = P (the lane's own
+//     probabilities, packed to 16-bit), so each lane's accumulators belong to
+//     its own query and the rescale is a per-lane scalar. V is transposed to
+//     [d][key] on its way into LDS (4 keys x 8 d per thread).
+//   * exp2 with log2(e) folded into the scale (exp(x) = 2^(x*log2 e)).
+//   * Causal: heaviest query blocks launch first; key blocks past the diagonal
+//     are never loaded; waves skip blocks entirely in their future.
+// Decode kernel: one workgroup per (batch, kv head, context split) serves all
+//   G = Hq/Hkv query heads of the group, so each K/V byte is read once;
+//   16 lanes per key (8 elements each), DPP/shuffle dot-product reduction,
+//   per-lane online softmax, then a cross-slot merge in LDS; a second kernel
+//   merges the splits (log-sum-exp).
+
+#include <cfloat>
+
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace ythip {
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+struct AttnArgs {
+    const void* Q;
+    const void* K;
+    const void* V;
+    void* O;
+    int64_t qs0, qs1, qs2, ks0, ks1, ks2, vs0, vs1, vs2, os0, os1, os2;
+    int B, Hq, Hkv, Sq, Skv, D, Dv;
+    float scale_log2;  // scale * log2(e)
+    const uint8_t* mask;
+    int64_t mask_ld;
+    int causal;
+    const float* bias;
+    int64_t brs, bcs;
+    int nqb;
+};
+
+__device__ __forceinline__ uint32_t half_of(u32x4 v, int i) { return (v[i >> 1] >> (16 * (i & 1))) & 0xffffu; }
+
+// MODE 0: no mask; 1: causal; 2: byte mask and/or bias read per element.
+template <class T, int D, int MODE>
+__global__ __launch_bounds__(256, 2) void attn_fwd_mfma(AttnArgs a) {
+    using raw = typename T::raw;
+    constexpr int BQ = 128, BKV = 64, WQ = 32;
+    constexpr int KCH = D / 8;   // 16-byte chunks per K row
+    constexpr int DT = D / 16;   // output d tiles
+    constexpr int KS = D / 32;   // d steps of the score MFMA
+    constexpr int K_PT = BKV * KCH / 256;
+    constexpr int V_GROUPS = (BKV / 4) * (D / 8);  // 4 keys x 8 d per group
+
+    __shared__ u32x4 sK[2][BKV * KCH];
+    __shared__ u32x2 sV[2][D * (BKV / 4)];
+
+    const int qb = (MODE == 1) ? (a.nqb - 1 - (int)blockIdx.x) : (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (a.Hq / a.Hkv);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int q0 = qb * BQ + wave * WQ;
+
+    const raw* Qp = static_cast<const raw*>(a.Q) + b * a.qs0 + h * a.qs1;
+    const raw* Kp = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1;
+    const raw* Vp = static_cast<const raw*>(a.V) + b * a.vs0 + kvh * a.vs1;
+
+    u32x4 qf[2][KS];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int q = q0 + qt * 16 + l16;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (q < a.Sq) v = *reinterpret_cast<const u32x4*>(Qp + (int64_t)q * a.qs2 + ks * 32 + g * 8);
+            qf[qt][ks] = v;
+        }
+    }
+
+    const int off = a.Skv - a.Sq;  // causal: key j visible to query i iff j <= i + off
+    int kv_end = a.Skv;
+    if (MODE == 1) kv_end = min(a.Skv, qb * BQ + BQ + off);
+    const int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;
+
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    f32x4 o[2][DT];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 rk[K_PT];
+    u32x4 rv[4];
+    const int v_kq = tid & 15, v_dc = tid >> 4;  // V group: keys 4*v_kq.., d 8*v_dc..
+
+    auto load_kv = [&](int kb) {
+        const int k0 = kb * BKV;
+#pragma unroll
+        for (int i = 0; i < K_PT; ++i) {
+            const int id = tid + i * 256;
+            const int key = id / KCH, c = id % KCH;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (k0 + key < a.Skv) v = *reinterpret_cast<const u32x4*>(Kp + (int64_t)(k0 + key) * a.ks2 + c * 8);
+            rk[i] = v;
+        }
+        if (V_GROUPS == 256 || tid < V_GROUPS) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + v_kq * 4 + r;
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if (key < a.Skv) v = *reinterpret_cast<const u32x4*>(Vp + (int64_t)key * a.vs2 + v_dc * 8);
+                rv[r] = v;
+            }
+        }
+    };
+    auto store_kv = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < K_PT; ++i) {
+            const int id = tid + i * 256;
+            const int key = id / KCH, c = id % KCH;
+            sK[st][key * KCH + (c ^ (key & 7))] = rk[i];
+        }
+        if (V_GROUPS == 256 || tid < V_GROUPS) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int row = v_dc * 8 + i;
+                u32x2 w = {half_of(rv[0], i) | (half_of(rv[1], i) << 16), half_of(rv[2], i) | (half_of(rv[3], i) << 16)};
+                sV[st][row * 16 + (v_kq ^ (row & 15))] = w;
+            }
+        }
+    };
+
+    if (nkb > 0) {
+        load_kv(0);
+        store_kv(0);
+    }
+    __syncthreads();
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int cur = kb & 1;
+        if (kb + 1 < nkb) load_kv(kb + 1);
+        const int k0 = kb * BKV;
+        // Wave-uniform: does this block hold any key visible to this wave's queries?
+        const bool active = (MODE != 1) || (k0 <= q0 + WQ - 1 + off);
+        if (active) {
+            f32x4 s[2][4];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt) {
+                    const int key = kt * 16 + l16;
+                    const u32x4 kf = sK[cur][key * KCH + ((ks * 4 + g) ^ (key & 7))];
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma_chunk(T{}, kf, qf[qt][ks], s[qt][kt]);
+                }
+            }
+            const bool need_mask = (MODE == 2) || (k0 + BKV > a.Skv) ||
+                                   (MODE == 1 && k0 + BKV - 1 > q0 + off);
+            u32x4 pk[2][2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                const int qa = q0 + qt * 16 + l16;
+                float v[4][4];
+                float mx = -INFINITY;
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float x = s[qt][kt][r] * a.scale_log2;
+                        if (need_mask) {
+                            const int key = k0 + kt * 16 + g * 4 + r;
+                            bool vis = key < a.Skv;
+                            if (MODE == 1) vis = vis && (key <= qa + off);
+                            if (MODE == 2 && vis && qa < a.Sq) {
+                                if (a.mask != nullptr) vis = a.mask[(int64_t)qa * a.mask_ld + key] != 0;
+                                if (vis && a.bias != nullptr)
+                                    x += a.bias[(int64_t)qa * a.brs + (int64_t)key * a.bcs] * LOG2E;
+                            }
+                            x = vis ? x : -INFINITY;
+                        }
+                        v[kt][r] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float m_new = fmaxf(m[qt], mx);
+                const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+                const float alpha = exp2f(m[qt] - m_use);
+                float sum = 0.f;
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        v[kt][r] = exp2f(v[kt][r] - m_use);
+                        sum += v[kt][r];
+                    }
+                l[qt] = l[qt] * alpha + sum;
+                m[qt] = m_new;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    pk[qt][kk] = u32x4{pack2<T>(v[2 * kk][0], v[2 * kk][1]), pack2<T>(v[2 * kk][2], v[2 * kk][3]),
+                                       pack2<T>(v[2 * kk + 1][0], v[2 * kk + 1][1]),
+                                       pack2<T>(v[2 * kk + 1][2], v[2 * kk + 1][3])};
+                }
+            }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const int row = dt * 16 + l16;
+                    const int qa_ = 8 * kk + g, qb_ = 8 * kk + 4 + g;
+                    const u32x2 va = sV[cur][row * 16 + (qa_ ^ (row & 15))];
+                    const u32x2 vb = sV[cur][row * 16 + (qb_ ^ (row & 15))];
+                    const u32x4 vf = {va[0], va[1], vb[0], vb[1]};
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) o[qt][dt] = mfma_chunk(T{}, vf, pk[qt][kk], o[qt][dt]);
+                }
+            }
+        }
+        if (kb + 1 < nkb) store_kv(cur ^ 1);
+        __syncthreads();
+    }
+
+    raw* Op = static_cast<raw*>(a.O) + b * a.os0 + h * a.os1;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        float L = l[qt];
+        L += __shfl_xor(L, 16, 64);
+        L += __shfl_xor(L, 32, 64);
+        const float inv = L > 0.f ? 1.0f / L : 0.f;
+        const int q = q0 + qt * 16 + l16;
+        if (q >= a.Sq) continue;
+        raw* orow = Op + (int64_t)q * a.os2;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int d = dt * 16 + g * 4;
+            const f32x4 v = o[qt][dt] * inv;
+            u32x2 p = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+            *reinterpret_cast<u32x2*>(orow + d) = p;
+        }
+    }
+}
+
+// Any layout / any dtype / d, dv <= 256: one wave per (batch, head, query row).
+// Scores for the whole row are kept in LDS (kv_len <= ROW_MAX), then max,
+// exp, sum and P.V in key order (the decode formulation of the reference).
+constexpr int ROW_MAX = 16384;
+
+template <class T>
+__global__ __launch_bounds__(64) void attn_rowwise(AttnArgs a) {
+    extern __shared__ float sc[];
+    const int qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (a.Hq / a.Hkv);
+    const int lane = threadIdx.x;
+    const int64_t qo = b * a.qs0 + h * a.qs1 + (int64_t)qi * a.qs2;
+    const int64_t ko = b * a.ks0 + kvh * a.ks1;
+    const int64_t vo = b * a.vs0 + kvh * a.vs1;
+    const float scale = a.scale_log2 / LOG2E;
+    const int off = a.Skv - a.Sq;
+    float mx = -INFINITY;
+    for (int j = lane; j < a.Skv; j += 64) {
+        bool vis = true;
+        if (a.causal) vis = j <= qi + off;
+        if (vis && a.mask != nullptr) vis = a.mask[(int64_t)qi * a.mask_ld + j] != 0;
+        float x = -INFINITY;
+        if (vis) {
+            float acc = 0.f;
+            for (int d = 0; d < a.D; ++d)
+                acc = fmaf(load_as_f32<T>(a.Q, qo + d), load_as_f32<T>(a.K, ko + (int64_t)j * a.ks2 + d), acc);
+            x = acc * scale;
+            if (a.bias != nullptr) x += a.bias[(int64_t)qi * a.brs + (int64_t)j * a.bcs];
+        }
+        sc[j] = x;
+        mx = fmaxf(mx, x);
+    }
+#pragma unroll
+    for (int off2 = 32; off2 >= 1; off2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off2, 64));
+    float sum = 0.f;
+    for (int j = lane; j < a.Skv; j += 64) {
+        const float p = (sc[j] == -INFINITY) ? 0.f : expf(sc[j] - mx);
+        sc[j] = p;
+        sum += p;
+    }
+#pragma unroll
+    for (int off2 = 32; off2 >= 1; off2 >>= 1) sum += __shfl_xor(sum, off2, 64);
+    __syncthreads();
+    const float inv = sum > 0.f ? 1.0f / sum : 0.f;
+    const int64_t oo = b * a.os0 + h * a.os1 + (int64_t)qi * a.os2;
+    for (int d = lane; d < a.Dv; d += 64) {
+        float acc = 0.f;
+        if (sum > 0.f)
+            for (int j = 0; j < a.Skv; ++j)
+                if (sc[j] != 0.f) acc = fmaf(sc[j] * inv, load_as_f32<T>(a.V, vo + (int64_t)j * a.vs2 + d), acc);
+        store_from_f32<T>(a.O, oo + d, acc);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode
+// ---------------------------------------------------------------------------
+struct DecodeArgs {
+    const void* Q;
+    const void* K;
+    const void* V;
+    void* O;
+    int64_t qs0, qs1, os0, os1, ks0, ks1, ks2;
+    const int32_t* kv_len;
+    int B, Hq, Hkv, max_ctx, splits, chunk;
+    float scale_log2;
+    float* ws;  // [B, Hq, splits, D + 2]
+};
+
+constexpr int DEC_GMAX = 8;
+
+// D = 8 * LPK (LPK lanes per key, 8 elements each); G query heads per kv head.
+template <class T, int D, int G>
+__global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
+    using raw = typename T::raw;
+    constexpr int LPK = D / 8;          // lanes per key
+    constexpr int SLOTS = 256 / LPK;    // keys in flight per workgroup
+    constexpr int UNR = 2;
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int slot = tid / LPK, part = tid % LPK;
+    const int len = a.kv_len ? min(a.kv_len[b], a.max_ctx) : a.max_ctx;
+    const int kbeg = split * a.chunk;
+    const int kend = min(len, kbeg + a.chunk);
+
+    float q[G][8];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        const int h = kvh * G + gi;
+        const raw* qp = static_cast<const raw*>(a.Q) + b * a.qs0 + h * a.qs1 + part * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[gi][e] = load_as_f32<T>(qp, e) * a.scale_log2;
+    }
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        m[gi] = -INFINITY;
+        l[gi] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[gi][e] = 0.f;
+    }
+    const raw* Kb = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1 + part * 8;
+    const raw* Vb = static_cast<const raw*>(a.V) + b * a.ks0 + kvh * a.ks1 + part * 8;
+
+    for (int k0 = kbeg + slot; k0 < kend; k0 += SLOTS * UNR) {
+        float kx[UNR][8], vx[UNR][8];
+        bool ok[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int key = k0 + u * SLOTS;
+            ok[u] = key < kend;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) { kx[u][e] = 0.f; vx[u][e] = 0.f; }
+            if (ok[u]) {
+                const raw* kp = Kb + (int64_t)key * a.ks2;
+                const raw* vp = Vb + (int64_t)key * a.ks2;
+                if constexpr (sizeof(raw) == 2) {
+                    const u32x4 kw = *reinterpret_cast<const u32x4*>(kp);
+                    const u32x4 vw = *reinterpret_cast<const u32x4*>(vp);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kx[u][2 * e] = lo_as_f32(T{}, kw[e]);
+                        kx[u][2 * e + 1] = hi_as_f32(T{}, kw[e]);
+                        vx[u][2 * e] = lo_as_f32(T{}, vw[e]);
+                        vx[u][2 * e + 1] = hi_as_f32(T{}, vw[e]);
+                    }
+                } else {
+                    const f32x4 k_lo = *reinterpret_cast<const f32x4*>(kp);
+                    const f32x4 k_hi = *reinterpret_cast<const f32x4*>(kp + 4);
+                    const f32x4 v_lo = *reinterpret_cast<const f32x4*>(vp);
+                    const f32x4 v_hi = *reinterpret_cast<const f32x4*>(vp + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kx[u][e] = k_lo[e]; kx[u][e + 4] = k_hi[e];
+                        vx[u][e] = v_lo[e]; vx[u][e + 4] = v_hi[e];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                float s = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s = fmaf(q[gi][e], kx[u][e], s);
+#pragma unroll
+                for (int w = LPK / 2; w >= 1; w >>= 1) s += __shfl_xor(s, w, LPK);
+                if (!ok[u]) continue;
+                const float m_new = fmaxf(m[gi], s);
+                const float corr = exp2f(m[gi] - m_new);
+                const float p = exp2f(s - m_new);
+                l[gi] = fmaf(l[gi], corr, p);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[gi][e] = fmaf(o[gi][e], corr, p * vx[u][e]);
+                m[gi] = m_new;
+            }
+        }
+    }
+
+    // Merge the SLOTS key slots of this workgroup: LDS holds per slot (m, l) and o.
+    __shared__ float s_ml[SLOTS][G][2];
+    __shared__ float s_o[SLOTS][G][D];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        if (part == 0) {
+            s_ml[slot][gi][0] = m[gi];
+            s_ml[slot][gi][1] = l[gi];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_o[slot][gi][part * 8 + e] = o[gi][e];
+    }
+    __syncthreads();
+    float* ws = a.ws;
+    for (int idx = tid; idx < G * D; idx += 256) {
+        const int gi = idx / D, d = idx % D;
+        float M = -INFINITY;
+        for (int sl = 0; sl < SLOTS; ++sl) M = fmaxf(M, s_ml[sl][gi][0]);
+        float L = 0.f, acc = 0.f;
+        if (M != -INFINITY) {
+            for (int sl = 0; sl < SLOTS; ++sl) {
+                const float ms = s_ml[sl][gi][0];
+                if (ms == -INFINITY) continue;
+                const float w = exp2f(ms - M);
+                L = fmaf(s_ml[sl][gi][1], w, L);
+                acc = fmaf(s_o[sl][gi][d], w, acc);
+            }
+        }
+        const int h = kvh * G + gi;
+        float* dst = ws + (((int64_t)b * a.Hq + h) * a.splits + split) * (D + 2);
+        dst[2 + d] = acc;
+        if (d == 0) {
+            dst[0] = M;
+            dst[1] = L;
+        }
+    }
+}
+
+template <class T, int D>
+__global__ __launch_bounds__(D) void attn_decode_merge(DecodeArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const float* src = a.ws + ((int64_t)b * a.Hq + h) * a.splits * (D + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, src[s * (D + 2)]);
+    float L = 0.f, acc = 0.f;
+    if (M != -INFINITY) {
+        for (int s = 0; s < a.splits; ++s) {
+            const float ms = src[s * (D + 2)];
+            if (ms == -INFINITY) continue;
+            const float w = exp2f(ms - M);
+            L = fmaf(src[s * (D + 2) + 1], w, L);
+            acc = fmaf(src[s * (D + 2) + 2 + d], w, acc);
+        }
+    }
+    const float out = L > 0.f ? acc / L : 0.f;
+    store_from_f32<T>(a.O, b * a.os0 + h * a.os1 + d, out);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+namespace {
+
+bool al(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+template <class T, int D>
+hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
+    a.nqb = (a.Sq + 127) / 128;
+    dim3 grid(a.nqb, a.Hq, a.B);
+    if (mode == 0) attn_fwd_mfma<T, D, 0><<<grid, 256, 0, s>>>(a);
+    else if (mode == 1) attn_fwd_mfma<T, D, 1><<<grid, 256, 0, s>>>(a);
+    else attn_fwd_mfma<T, D, 2><<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_rowwise(const AttnArgs& a, hipStream_t s) {
+    dim3 grid(a.Sq, a.Hq, a.B);
+    attn_rowwise<T><<<grid, 64, sizeof(float) * a.Skv, s>>>(a);
+    return hipGetLastError();
+}
+
+template <class T>
+int prefill_typed(AttnArgs a, hipStream_t s) {
+    constexpr int es = sizeof(typename T::raw);
+    const bool simple_mask = a.mask == nullptr && a.bias == nullptr;
+    const int mode = a.causal ? 1 : (simple_mask ? 0 : 2);
+    const bool mfma_ok = es == 2 && (a.D == 64 || a.D == 128) && a.Dv == a.D && !(a.causal && !simple_mask) &&
+                         al(a.Q, 16) && al(a.K, 16) && al(a.V, 16) && al(a.O, 8) &&
+                         a.qs0 % 8 == 0 && a.qs1 % 8 == 0 && a.qs2 % 8 == 0 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
+                         a.ks2 % 8 == 0 && a.vs0 % 8 == 0 && a.vs1 % 8 == 0 && a.vs2 % 8 == 0 &&
+                         a.os0 % 4 == 0 && a.os1 % 4 == 0 && a.os2 % 4 == 0;
+    if (mfma_ok) {
+        if constexpr (es == 2) {
+            if (a.D == 128) return status_of(launch_prefill_mfma<T, 128>(a, mode, s));
+            return status_of(launch_prefill_mfma<T, 64>(a, mode, s));
+        }
+    }
+    if (a.Skv > ROW_MAX)
+        return fail(YTHIP_EUNSUPPORTED,
+                    "ythip_attn_prefill: this layout/dtype uses the row-wise kernel, limited to kv_len <= %d",
+                    ROW_MAX);
+    return status_of(launch_rowwise<T>(a, s));
+}
+
+int decode_splits(int B, int Hq, int max_ctx) {
+    const int bh = B * Hq > 0 ? B * Hq : 1;
+    int s = (1024 + bh - 1) / bh;
+    const int by_len = (max_ctx + 127) / 128;
+    if (s > by_len) s = by_len;
+    if (s > 64) s = 64;
+    if (s < 1) s = 1;
+    return s;
+}
+
+template <class T, int D, int G>
+hipError_t launch_decode_g(const DecodeArgs& a, hipStream_t s) {
+    dim3 grid(a.splits, a.Hkv, a.B);
+    attn_decode_split<T, D, G><<<grid, 256, 0, s>>>(a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    attn_decode_merge<T, D><<<dim3(a.Hq, a.B), D, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+template <class T, int D>
+hipError_t launch_decode_d(const DecodeArgs& a, int G, hipStream_t s) {
+    switch (G) {
+        case 1: return launch_decode_g<T, D, 1>(a, s);
+        case 2: return launch_decode_g<T, D, 2>(a, s);
+        case 4: return launch_decode_g<T, D, 4>(a, s);
+        case 8: return launch_decode_g<T, D, 8>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <class T>
+hipError_t launch_decode(const DecodeArgs& a, int D, int G, hipStream_t s) {
+    if (D == 128) return launch_decode_d<T, 128>(a, G, s);
+    return launch_decode_d<T, 64>(a, G, s);
+}
+
+}  // namespace
+
+}  // namespace ythip
+
+using namespace ythip;
+
+extern "C" {
+
+__attribute__((visibility("default"))) int ythip_attn_prefill(
+    int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv, const void* Q, const int64_t q_str[4],
+    const void* K, const int64_t k_str[4], const void* V, const int64_t v_str[4], void* O, const int64_t o_str[4],
+    float scale, int mask_kind, const uint8_t* mask, int64_t mask_ld, const float* bias, int64_t rs_bias,
+    int64_t cs_bias, void* stream) {
+    if (B < 0 || Hq < 0 || Hkv < 0 || q_len < 0 || kv_len < 0 || d < 0 || dv < 0)
+        return fail(YTHIP_EINVAL, "ythip_attn_prefill: negative size");
+    if ((int64_t)B * Hq * q_len == 0 || dv == 0) return 0;
+    if (Hkv == 0 || Hq % Hkv != 0) return fail(YTHIP_EINVAL, "ythip_attn_prefill: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+    if (d == 0 || d > 256 || dv > 256) return fail(YTHIP_EUNSUPPORTED, "ythip_attn_prefill: head dims %d/%d (1..256)", d, dv);
+    if (!Q || !K || !V || !O || !q_str || !k_str || !v_str || !o_str)
+        return fail(YTHIP_EINVAL, "ythip_attn_prefill: NULL tensor or stride array");
+    if (q_str[3] != 1 || k_str[3] != 1 || v_str[3] != 1 || o_str[3] != 1)
+        return fail(YTHIP_EUNSUPPORTED, "ythip_attn_prefill: the last (head-dim) stride must be 1");
+    if (mask_kind < 0 || mask_kind > 2) return fail(YTHIP_EINVAL, "ythip_attn_prefill: mask_kind %d", mask_kind);
+    if (mask_kind == YTHIP_MASK_BOOL && (mask == nullptr || mask_ld < kv_len))
+        return fail(YTHIP_EINVAL, "ythip_attn_prefill: bool mask needs a pointer and mask_ld >= kv_len");
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)d);  // src/function/ops.inl:378-381
+    AttnArgs a{};
+    a.Q = Q; a.K = K; a.V = V; a.O = O;
+    a.qs0 = q_str[0]; a.qs1 = q_str[1]; a.qs2 = q_str[2];
+    a.ks0 = k_str[0]; a.ks1 = k_str[1]; a.ks2 = k_str[2];
+    a.vs0 = v_str[0]; a.vs1 = v_str[1]; a.vs2 = v_str[2];
+    a.os0 = o_str[0]; a.os1 = o_str[1]; a.os2 = o_str[2];
+    a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.Sq = q_len; a.Skv = kv_len; a.D = d; a.Dv = dv;
+    a.scale_log2 = scale * LOG2E;
+    a.causal = mask_kind == YTHIP_MASK_CAUSAL;
+    a.mask = mask_kind == YTHIP_MASK_BOOL ? mask : nullptr;
+    a.mask_ld = mask_ld;
+    a.bias = bias; a.brs = rs_bias; a.bcs = cs_bias;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (kv_len == 0) {
+        // No key at all: every row is fully masked -> zeros (flash_attention.inl:241-244).
+        a.Skv = 0;
+    }
+    switch (dtype) {
+        case YTHIP_F32: return prefill_typed<F32>(a, s);
+        case YTHIP_F16: return prefill_typed<F16>(a, s);
+        case YTHIP_BF16: return prefill_typed<BF16>(a, s);
+        default: return fail(YTHIP_EINVAL, "ythip_attn_prefill: invalid dtype %d", dtype);
+    }
+}
+
+__attribute__((visibility("default"))) size_t ythip_attn_decode_workspace_size(int B, int Hq, int max_ctx, int d) {
+    if (B <= 0 || Hq <= 0 || max_ctx <= 0 || d <= 0) return 0;
+    return (size_t)B * Hq * decode_splits(B, Hq, max_ctx) * (d + 2) * sizeof(float);
+}
+
+__attribute__((visibility("default"))) int ythip_attn_decode(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
+                                                             const void* Q, const int64_t q_str[2], const void* Kc,
+                                                             const void* Vc, const int64_t kv_str[3],
+                                                             const int32_t* kv_len, void* O, const int64_t o_str[2],
+                                                             float scale, void* workspace, size_t ws_bytes,
+                                                             void* stream) {
+    if (B < 0 || Hq < 0 || Hkv < 0 || max_ctx < 0) return fail(YTHIP_EINVAL, "ythip_attn_decode: negative size");
+    if ((int64_t)B * Hq == 0) return 0;
+    if (Hkv == 0 || Hq % Hkv != 0) return fail(YTHIP_EINVAL, "ythip_attn_decode: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+    const int G = Hq / Hkv;
+    if (d != 64 && d != 128) return fail(YTHIP_EUNSUPPORTED, "ythip_attn_decode: head dim %d (supported: 64, 128)", d);
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return fail(YTHIP_EUNSUPPORTED, "ythip_attn_decode: group size %d (supported: 1, 2, 4, 8)", G);
+    if (!Q || !Kc || !Vc || !O || !q_str || !kv_str || !o_str)
+        return fail(YTHIP_EINVAL, "ythip_attn_decode: NULL tensor or stride array");
+    const size_t need = ythip_attn_decode_workspace_size(B, Hq, max_ctx > 0 ? max_ctx : 1, d);
+    if (workspace == nullptr || ws_bytes < need)
+        return fail(YTHIP_EINVAL, "ythip_attn_decode: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+    const int es = dtype == YTHIP_F32 ? 4 : 2;
+    if (dtype != YTHIP_F32 && dtype != YTHIP_F16 && dtype != YTHIP_BF16)
+        return fail(YTHIP_EINVAL, "ythip_attn_decode: invalid dtype %d", dtype);
+    if (!al(Q, es) || !al(Kc, 16) || !al(Vc, 16) || kv_str[0] % (16 / es) || kv_str[1] % (16 / es) ||
+        kv_str[2] % (16 / es))
+        return fail(YTHIP_EUNSUPPORTED, "ythip_attn_decode: K/V cache rows must be 16-byte aligned");
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)d);
+    DecodeArgs a{};
+    a.Q = Q; a.K = Kc; a.V = Vc; a.O = O;
+    a.qs0 = q_str[0]; a.qs1 = q_str[1]; a.os0 = o_str[0]; a.os1 = o_str[1];
+    a.ks0 = kv_str[0]; a.ks1 = kv_str[1]; a.ks2 = kv_str[2];
+    a.kv_len = kv_len;
+    a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_ctx = max_ctx;
+    a.splits = decode_splits(B, Hq, max_ctx > 0 ? max_ctx : 1);
+    a.chunk = max_ctx > 0 ? (max_ctx + a.splits - 1) / a.splits : 0;
+    a.scale_log2 = scale * LOG2E;
+    a.ws = static_cast<float*>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case YTHIP_F32: return status_of(launch_decode<F32>(a, d, G, s));
+        case YTHIP_F16: return status_of(launch_decode<F16>(a, d, G, s));
+        default: return status_of(launch_decode<BF16>(a, d, G, s));
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,104 @@
+// common.hpp — shared device types and helpers for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "../../include/ythip.h"
+
+namespace ythip {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage tags: the kernels move 16-bit data as raw uint16_t bits and convert
+// explicitly, so that the rounding is the one written here.
+struct BF16 { using raw = uint16_t; static constexpr int code = YTHIP_BF16; };
+struct F16 { using raw = uint16_t; static constexpr int code = YTHIP_F16; };
+struct F32 { using raw = float; static constexpr int code = YTHIP_F32; };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16, IEEE round-to-nearest-even; NaN stays NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    _Float16 x = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h));
+    return static_cast<float>(x);
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    _Float16 x = static_cast<_Float16>(f);  // v_cvt_f16_f32: RNE
+    return __builtin_bit_cast(uint16_t, x);
+}
+
+template <class T> __device__ __forceinline__ float load_as_f32(const void* p, int64_t i);
+template <> __device__ __forceinline__ float load_as_f32<F32>(const void* p, int64_t i) {
+    return static_cast<const float*>(p)[i];
+}
+template <> __device__ __forceinline__ float load_as_f32<BF16>(const void* p, int64_t i) {
+    return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <> __device__ __forceinline__ float load_as_f32<F16>(const void* p, int64_t i) {
+    return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <class T> __device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v);
+template <> __device__ __forceinline__ void store_from_f32<F32>(void* p, int64_t i, float v) {
+    static_cast<float*>(p)[i] = v;
+}
+template <> __device__ __forceinline__ void store_from_f32<BF16>(void* p, int64_t i, float v) {
+    static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+}
+template <> __device__ __forceinline__ void store_from_f32<F16>(void* p, int64_t i, float v) {
+    static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_f16_bits(v));
+}
+
+template <class T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<BF16>(float a, float b) {
+    return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+}
+template <> __device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
+    return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+}
+
+__device__ __forceinline__ float lo_as_f32(BF16, uint32_t w) { return bf16_bits_to_f32(w & 0xffffu); }
+__device__ __forceinline__ float hi_as_f32(BF16, uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float lo_as_f32(F16, uint32_t w) { return f16_bits_to_f32(w & 0xffffu); }
+__device__ __forceinline__ float hi_as_f32(F16, uint32_t w) { return f16_bits_to_f32(w >> 16); }
+
+// MFMA on one 16-byte operand chunk per lane, 16x16 fp32 output tile.
+//   16-bit: one v_mfma_f32_16x16x32_{bf16,f16}: lane l supplies row (l%16) and
+//           k = 8*(l/16) + 0..7 of the 32-wide k block.
+//   fp32  : four v_mfma_f32_16x16x4_f32, lane l supplies row (l%16) and
+//           k = 4*(l/16) + j on step j; together the 16 k of the block.
+// Any k assignment is valid as long as both operands use the same one.
+__device__ __forceinline__ f32x4 mfma_chunk(BF16, u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_chunk(F16, u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_chunk(F32, u32x4 a, u32x4 b, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[0]), __uint_as_float(b[0]), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[1]), __uint_as_float(b[1]), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[2]), __uint_as_float(b[2]), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[3]), __uint_as_float(b[3]), c, 0, 0, 0);
+    return c;
+}
+
+// Elements per 16-byte chunk.
+template <class T> struct Vec { static constexpr int n = 16 / sizeof(typename T::raw); };
+
+}  // namespace ythip

@@ -1,0 +1,392 @@
+// gemm.hip — MFMA GEMM for gfx950 (CDNA4), the device replacement of YTensor's
+// blocked AVX2 sgemm / hgemm (src/kernel/avx2/sgemm.inl:268-340, 586-787;
+// src/kernel/avx2/hgemm.inl:139-273).
+//
+// Design (MI355X-first, not a translation of the CPU Goto loop):
+//  * Block tile BM x BN, k step of 128 bytes per row (64 bf16/fp16 or 32 fp32).
+//    Both operands are staged in LDS K-contiguous, [rows][8 chunks of 16 B],
+//    so every MFMA operand is one ds_read_b128 per lane.
+//  * LDS chunk swizzle: chunk c of row r lives at c ^ ((r ^ (r >> 3)) & 7).
+//    16 consecutive rows reading the same logical chunk hit 8 distinct 16-byte
+//    slots per 8-lane group, and the NN transposing writes (rows 4 apart) also
+//    spread over all 8 slots.
+//  * Two LDS stages; the next k step is fetched into registers while the
+//    current one runs on the matrix cores; one barrier per k step.
+//  * A row-major B ("NN", B[k][n]) is transposed in registers on its way to
+//    LDS (8 k-rows x 4 columns per thread, v_perm-style half-word shuffles), so
+//    the compute loop is the same for NN and NT ("linear": B = W^T).
+//  * MFMA operands are swapped (src0 = B rows, src1 = A rows): each lane then
+//    holds 4 consecutive output columns of one row, stored as one vector.
+//  * Tiles are assigned XCD-aware: the hardware places workgroup w on XCD
+//    w % 8; each XCD receives a contiguous, M-grouped range of tiles so its
+//    32 CUs share A and B panels in their own L2.
+
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace ythip {
+
+struct GemmArgs {
+    const void* A;
+    const void* B;
+    void* C;
+    int m, n, k;
+    int64_t rsa, rsb, csb, rsc;  // csa == 1 and csc == 1 on this path
+    int64_t sa_b, sb_b, sc_b;
+    float alpha, beta;
+    int tiles_m, tiles_n;
+    int c_vec_ok;  // C rows allow 4-element vector stores
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
+
+__device__ __forceinline__ void tile_coords(int w, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int T = tiles_m * tiles_n;
+    if ((T & 7) == 0) {
+        const int per = T >> 3;
+        w = (w & 7) * per + (w >> 3);
+    }
+    constexpr int GROUP = 4;
+    const int in_group = GROUP * tiles_n;
+    const int g = w / in_group;
+    const int first = g * GROUP;
+    const int gsize = min(tiles_m - first, GROUP);
+    const int r = w - g * in_group;
+    tm = first + r % gsize;
+    tn = r / gsize;
+}
+
+template <class T, class TO, int BM, int BN, int WM, int WN, bool NN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs a) {
+    using raw = typename T::raw;
+    constexpr int THREADS = 64 * WM * WN;
+    constexpr int VEC = 16 / sizeof(raw);      // elements per 16-byte chunk
+    constexpr int BK = 8 * VEC;                 // elements per k step (128 bytes)
+    constexpr int WTM = BM / WM, WTN = BN / WN; // wave tile
+    constexpr int FM = WTM / 16, FN = WTN / 16;
+    constexpr int A_CHUNKS = BM * 8, B_CHUNKS = BN * 8;
+    constexpr int A_PT = (A_CHUNKS + THREADS - 1) / THREADS;
+    constexpr int B_PT = (B_CHUNKS + THREADS - 1) / THREADS;
+    constexpr int NN_GROUPS = 8 * (BN / 4);     // VEC k-rows x 4 columns each
+    constexpr int NN_PT = (NN_GROUPS + THREADS - 1) / THREADS;
+    constexpr int STAGE = (BM + BN) * 8;        // u32x4 slots per stage
+
+    __shared__ u32x4 lds[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int bz = blockIdx.y;
+
+    const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
+    const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b;
+
+    const int KT = (a.k + BK - 1) / BK;
+
+    u32x4 ra[A_PT];
+    u32x4 rb[NN ? 1 : B_PT];
+    // NN staging: VEC rows of 4 columns each (8 bytes for 16-bit, 16 bytes for fp32)
+    using nn_row_t = typename std::conditional<sizeof(raw) == 2, u32x2, u32x4>::type;
+    nn_row_t rn[NN ? NN_PT : 1][NN ? VEC : 1];
+
+    auto load_global = [&](int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i) {
+            const int id = tid + i * THREADS;
+            const int r = id >> 3, c = id & 7;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if ((A_CHUNKS % THREADS == 0 || id < A_CHUNKS) && m0 + r < a.m && k0 + c * VEC < a.k)
+                v = *reinterpret_cast<const u32x4*>(Ap + (int64_t)(m0 + r) * a.rsa + (k0 + c * VEC));
+            ra[i] = v;
+        }
+        if constexpr (!NN) {
+#pragma unroll
+            for (int i = 0; i < B_PT; ++i) {
+                const int id = tid + i * THREADS;
+                const int r = id >> 3, c = id & 7;
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if ((B_CHUNKS % THREADS == 0 || id < B_CHUNKS) && n0 + r < a.n && k0 + c * VEC < a.k)
+                    v = *reinterpret_cast<const u32x4*>(Bp + (int64_t)(n0 + r) * a.csb + (k0 + c * VEC));
+                rb[i] = v;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NN_PT; ++i) {
+                const int id = tid + i * THREADS;
+                const int g = id % (BN / 4), kc = id / (BN / 4);
+                const int col = n0 + g * 4;
+                const bool ok = (NN_GROUPS % THREADS == 0 || id < NN_GROUPS) && col < a.n;
+#pragma unroll
+                for (int r = 0; r < VEC; ++r) {
+                    const int kk = k0 + kc * VEC + r;
+                    nn_row_t v = {};
+                    if (ok && kk < a.k) v = *reinterpret_cast<const nn_row_t*>(Bp + (int64_t)kk * a.rsb + col);
+                    rn[i][r] = v;
+                }
+            }
+        }
+    };
+
+    auto store_lds = [&](int stage) {
+        u32x4* sA = lds + stage * STAGE;
+        u32x4* sB = sA + BM * 8;
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i) {
+            const int id = tid + i * THREADS;
+            if (A_CHUNKS % THREADS == 0 || id < A_CHUNKS) {
+                const int r = id >> 3, c = id & 7;
+                sA[r * 8 + swz(r, c)] = ra[i];
+            }
+        }
+        if constexpr (!NN) {
+#pragma unroll
+            for (int i = 0; i < B_PT; ++i) {
+                const int id = tid + i * THREADS;
+                if (B_CHUNKS % THREADS == 0 || id < B_CHUNKS) {
+                    const int r = id >> 3, c = id & 7;
+                    sB[r * 8 + swz(r, c)] = rb[i];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NN_PT; ++i) {
+                const int id = tid + i * THREADS;
+                if (NN_GROUPS % THREADS == 0 || id < NN_GROUPS) {
+                    const int g = id % (BN / 4), kc = id / (BN / 4);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        u32x4 o;
+                        if constexpr (sizeof(raw) == 2) {
+                            // out[j] = column j's VEC k-values: half-word j of each row, paired.
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const uint32_t lo = rn[i][2 * q][j >> 1];
+                                const uint32_t hi = rn[i][2 * q + 1][j >> 1];
+                                o[q] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+                            }
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) o[q] = rn[i][q][j];
+                        }
+                        const int row = g * 4 + j;
+                        sB[row * 8 + swz(row, kc)] = o;
+                    }
+                }
+            }
+        }
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+
+    const int lrow = lane & 15;
+    const int lgrp = lane >> 4;
+
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) load_global(kt + 1);
+        const u32x4* sA = lds + cur * STAGE;
+        const u32x4* sB = sA + BM * 8;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int chunk = ks * 4 + lgrp;
+            u32x4 fa[FM], fb[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int r = wm * WTM + i * 16 + lrow;
+                fa[i] = sA[r * 8 + swz(r, chunk)];
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int r = wn * WTN + j * 16 + lrow;
+                fb[j] = sB[r * 8 + swz(r, chunk)];
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma_chunk(T{}, fb[j], fa[i], acc[i][j]);
+        }
+        if (kt + 1 < KT) store_lds(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds C[m][n..n+3] for m = row lrow, n = 4*lgrp + r.
+    using oraw = typename TO::raw;
+    oraw* Cp = static_cast<oraw*>(a.C) + bz * a.sc_b;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * WTM + i * 16 + lrow;
+        if (m >= a.m) continue;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = n0 + wn * WTN + j * 16 + lgrp * 4;
+            if (n >= a.n) continue;
+            oraw* crow = Cp + (int64_t)m * a.rsc;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = a.alpha * acc[i][j][r];
+            const bool full = a.c_vec_ok && (n + 3 < a.n);
+            if (a.beta != 0.0f) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (n + r < a.n) v[r] += a.beta * load_as_f32<TO>(crow, n + r);
+            }
+            if (full) {
+                if constexpr (sizeof(oraw) == 2) {
+                    u32x2 p = {pack2<TO>(v[0], v[1]), pack2<TO>(v[2], v[3])};
+                    *reinterpret_cast<u32x2*>(crow + n) = p;
+                } else {
+                    *reinterpret_cast<f32x4*>(crow + n) = f32x4{v[0], v[1], v[2], v[3]};
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (n + r < a.n) store_from_f32<TO>(crow, n + r, v[r]);
+            }
+        }
+    }
+}
+
+// Any-stride fallback: one output per thread, fp32 accumulation in k order.
+struct GenericArgs {
+    const void* A;
+    const void* B;
+    void* C;
+    int m, n, k;
+    int64_t rsa, csa, rsb, csb, rsc, csc, sa_b, sb_b, sc_b;
+    float alpha, beta;
+};
+
+template <class T, class TO>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(GenericArgs a) {
+    const int j = blockIdx.x * 16 + (threadIdx.x & 15);
+    const int i = blockIdx.y * 16 + (threadIdx.x >> 4);
+    const int b = blockIdx.z;
+    if (i >= a.m || j >= a.n) return;
+    const int64_t ao = b * a.sa_b + i * a.rsa, bo = b * a.sb_b + j * a.csb;
+    float acc = 0.0f;
+    for (int p = 0; p < a.k; ++p)
+        acc = fmaf(load_as_f32<T>(a.A, ao + p * a.csa), load_as_f32<T>(a.B, bo + p * a.rsb), acc);
+    const int64_t co = b * a.sc_b + i * a.rsc + j * a.csc;
+    float v = a.alpha * acc;
+    if (a.beta != 0.0f) v += a.beta * load_as_f32<TO>(a.C, co);
+    store_from_f32<TO>(a.C, co, v);
+}
+
+// C = beta * C (k == 0 or alpha == 0), sgemm.inl:594-604.
+template <class TO>
+__global__ __launch_bounds__(256) void gemm_scale_kernel(void* C, int m, int n, int64_t rsc, int64_t csc,
+                                                         int64_t sc_b, float beta) {
+    const int j = blockIdx.x * 16 + (threadIdx.x & 15);
+    const int i = blockIdx.y * 16 + (threadIdx.x >> 4);
+    if (i >= m || j >= n) return;
+    const int64_t co = blockIdx.z * sc_b + i * rsc + j * csc;
+    const float v = (beta == 0.0f) ? 0.0f : beta * load_as_f32<TO>(C, co);
+    store_from_f32<TO>(C, co, v);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+namespace {
+
+template <class T, class TO, int BM, int BN, int WM, int WN>
+hipError_t launch_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s) {
+    GemmArgs a = a0;
+    a.tiles_m = (a.m + BM - 1) / BM;
+    a.tiles_n = (a.n + BN - 1) / BN;
+    dim3 grid(a.tiles_m * a.tiles_n, batch);
+    dim3 block(64 * WM * WN);
+    if (nn)
+        gemm_mfma_kernel<T, TO, BM, BN, WM, WN, true><<<grid, block, 0, s>>>(a);
+    else
+        gemm_mfma_kernel<T, TO, BM, BN, WM, WN, false><<<grid, block, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+template <class T, class TO>
+hipError_t launch_mfma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
+    auto tiles = [&](int bm, int bn) {
+        return (int64_t)((a.m + bm - 1) / bm) * ((a.n + bn - 1) / bn) * batch;
+    };
+    if (tiles(256, 256) >= 160) return launch_tile<T, TO, 256, 256, 2, 4>(a, nn, batch, s);
+    if (tiles(128, 128) >= 96) return launch_tile<T, TO, 128, 128, 2, 2>(a, nn, batch, s);
+    return launch_tile<T, TO, 64, 64, 2, 2>(a, nn, batch, s);
+}
+
+template <class T, class TO>
+hipError_t launch_generic(const GenericArgs& a, int batch, hipStream_t s) {
+    dim3 grid((a.n + 15) / 16, (a.m + 15) / 16, batch);
+    gemm_generic_kernel<T, TO><<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+template <class TO>
+hipError_t launch_scale(void* C, int m, int n, int64_t rsc, int64_t csc, int64_t sc_b, float beta, int batch,
+                        hipStream_t s) {
+    dim3 grid((n + 15) / 16, (m + 15) / 16, batch);
+    gemm_scale_kernel<TO><<<grid, 256, 0, s>>>(C, m, n, rsc, csc, sc_b, beta);
+    return hipGetLastError();
+}
+
+bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+template <class T, class TO>
+int gemm_typed(int batch, int m, int n, int k, const void* A, int64_t sa_b, int64_t rsa, int64_t csa,
+               const void* B, int64_t sb_b, int64_t rsb, int64_t csb, void* C, int64_t sc_b, int64_t rsc,
+               int64_t csc, float alpha, float beta, hipStream_t s) {
+    using raw = typename T::raw;
+    using oraw = typename TO::raw;
+    constexpr int VEC = 16 / sizeof(raw);
+    if (k == 0 || alpha == 0.0f) return status_of(launch_scale<TO>(C, m, n, rsc, csc, sc_b, beta, batch, s));
+
+    const int es = sizeof(raw);
+    const bool a_ok = csa == 1 && (rsa % VEC) == 0 && (sa_b % VEC) == 0 && aligned(A, 16) && (k % VEC) == 0;
+    const bool nt = rsb == 1 && (csb % VEC) == 0 && (sb_b % VEC) == 0 && aligned(B, 16);
+    const bool nn = !nt && csb == 1 && (rsb % 4) == 0 && (sb_b % 4) == 0 && (n % 4) == 0 && aligned(B, 4 * es);
+    const bool c_ok = csc == 1;
+    if (a_ok && (nt || nn) && c_ok) {
+        GemmArgs g{};
+        g.A = A; g.B = B; g.C = C;
+        g.m = m; g.n = n; g.k = k;
+        g.rsa = rsa; g.rsb = rsb; g.csb = csb; g.rsc = rsc;
+        g.sa_b = sa_b; g.sb_b = sb_b; g.sc_b = sc_b;
+        g.alpha = alpha; g.beta = beta;
+        g.c_vec_ok = (rsc % 4 == 0) && (sc_b % 4 == 0) && aligned(C, 4 * sizeof(oraw));
+        return status_of(launch_mfma<T, TO>(g, nn, batch, s));
+    }
+    GenericArgs g{A, B, C, m, n, k, rsa, csa, rsb, csb, rsc, csc, sa_b, sb_b, sc_b, alpha, beta};
+    return status_of(launch_generic<T, TO>(g, batch, s));
+}
+
+}  // namespace
+
+int gemm_dispatch(int dtype_in, int dtype_out, int batch, int m, int n, int k, const void* A, int64_t sa_b,
+                  int64_t rsa, int64_t csa, const void* B, int64_t sb_b, int64_t rsb, int64_t csb, void* C,
+                  int64_t sc_b, int64_t rsc, int64_t csc, float alpha, float beta, hipStream_t s) {
+#define YTHIP_GEMM(TI, TOUT) \
+    return gemm_typed<TI, TOUT>(batch, m, n, k, A, sa_b, rsa, csa, B, sb_b, rsb, csb, C, sc_b, rsc, csc, alpha, beta, s)
+    if (dtype_in == YTHIP_F32 && dtype_out == YTHIP_F32) YTHIP_GEMM(F32, F32);
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_BF16) YTHIP_GEMM(BF16, BF16);
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_F32) YTHIP_GEMM(BF16, F32);
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F16) YTHIP_GEMM(F16, F16);
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F32) YTHIP_GEMM(F16, F32);
+#undef YTHIP_GEMM
+    return fail(YTHIP_EUNSUPPORTED, "ythip_gemm: unsupported dtype_in/dtype_out combination %d/%d", dtype_in,
+                dtype_out);
+}
+
+}  // namespace ythip
