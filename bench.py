@@ -1,0 +1,313 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X hot path (libythip.so) on one GPU.
+
+Headline (`value`): bf16 GEMM C[M,N] = A[M,K] . B[K,N] at M=N=K=4096 with fp32
+accumulation and bf16 output (its MFMA-bound shape),
+in TFLOP/s of algorithmic work (2*M*N*K per step). One step = one GEMM launch
+through the C ABI (ythip_gemm); inputs are resident in HBM before timing.
+
+Also reported in the same JSON line (each timed with HIP events on the stream
+the kernels are launched on):
+  gemm_sweep      the other configs[1] shapes (NN and the W^T "linear" layout)
+  gemm_fp32       configs[0] (fp32 1024^3)
+  attn_prefill    configs[2] causal flash prefill S = 512/2048/8192 (TFLOP/s)
+  attn_decode     configs[3] decode attention (GB/s of K/V read)
+  rmsnorm_rope    fused RMSNorm+RoPE on configs[2] shapes at S=8192 (GB/s)
+  roofline        the headline kernel against MI355X dense bf16 MFMA peak
+  cpu_baseline    YTensor's own CPU sgemm (compiled reference when present,
+                  else the oracle restatement) on the host cores, same shape
+Synthetic data: torch.randn with fixed seeds, N(0,1) activations and
+N(0,0.02) weights (the configs' distributions). The parity tests use YTensor's
+own seeded generator; the benchmark only needs the shapes and magnitudes.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 matrix
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_bf16_4096_traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline only (no sweep, no CPU baseline)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", help="comma list of sections to run (gemm,sweep,fp32,prefill,decode,norm)")
+    ap.add_argument("--calib", action="store_true",
+                    help="first run a plain conversion-copy kernel of known size (HBM counter calibration)")
+    return ap.parse_args()
+
+
+def time_launches(fn, steps: int, warmup: int, torch) -> float:
+    """Average milliseconds per launch of fn(), HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def rotating(n_bufs: int, make):
+    bufs = [make(i) for i in range(n_bufs)]
+    state = {"i": 0}
+
+    def nxt():
+        b = bufs[state["i"] % n_bufs]
+        state["i"] += 1
+        return b
+    return nxt
+
+
+def host_info() -> dict:
+    info = {"host_cpu": platform.processor() or "", "logical_cpus": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "Thread(s) per core", "Core(s) per socket", "Socket(s)"):
+                info[k.strip()] = v.strip()
+    except Exception:
+        pass
+    return info
+
+
+def cpu_baseline(M: int, N: int, K: int, budget_s: float = 20.0) -> dict:
+    """YTensor's CPU path for the headline shape: the bf16 inputs are up-converted
+    and multiplied by the fp32 sgemm (src/ytensor_base_math.inl:689-700), with
+    the reference default of a single-threaded GEMM (g_num_threads = 0,
+    include/kernel/avx2/gemm_utils.hpp:64). Uses the compiled reference
+    (oracle/_ref) when it was built, else the oracle's restatement."""
+    import numpy as np
+    import oracle
+    path = oracle.reference()
+    kind = "reference"
+    if path is None:
+        path = oracle.oracle()
+        path.set_num_threads(1)
+        kind = "port"
+    rng = np.random.default_rng(0)
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    B = (rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    A = oracle.oracle().bf16_to_f32(oracle.oracle().bf16_round(A))
+    B = oracle.oracle().bf16_to_f32(oracle.oracle().bf16_round(B))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        path.sgemm(A, B)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    return {"value": round(2.0 * M * N * K / t / 1e12, 4), "unit": "TFLOP/s", "cores": 1, "kind": kind,
+            "sample": f"full {M}x{N}x{K} fp32 sgemm on bf16-rounded inputs, median of {len(times)} run(s), "
+                      f"{t:.2f} s each, single thread (reference default g_num_threads=0)",
+            "host": host_info()}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU; --gpus > 1 is not supported (the multi-GPU "
+                                   "sharding is design-only, see DESIGN.md)", "n_gpus": args.gpus}))
+        return 2
+    import torch
+    import ytensor_amd as yt
+    from ytensor_amd import ops
+    yt.load()
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    only = set(filter(None, args.only.split(",")))
+
+    def want(x):
+        return (not only) or (x in only)
+
+    out: dict = {}
+    sections: dict = {}
+
+    if args.calib:
+        # 256 Mi fp32 elements read (1 GiB), written as bf16 (512 MiB): one elementwise kernel.
+        src = torch.randn(256 * 1024 * 1024, device=dev)
+        dst = torch.empty(src.shape, device=dev, dtype=torch.bfloat16)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
+
+    # ---- headline: bf16 GEMM 4096^3, NN (A [M,K] activations, B [K,N] weights) ----
+    M = N = K = 4096
+    A = torch.randn(M, K, device=dev).to(torch.bfloat16)
+    B = (torch.randn(K, N, device=dev) * 0.02).to(torch.bfloat16)
+    C = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    flops = 2.0 * M * N * K
+    ms = time_launches(lambda: ops.gemm(A, B, C), args.steps, args.warmup, torch)
+    tflops = flops / (ms * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        try:
+            traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                "kernel": "gemm_mfma_kernel<BF16,BF16,256,256,2,4,NN>",
+                "algorithmic_flops_per_launch": flops, "avg_launch_ms": round(ms, 5)}
+
+    if want("gemm") and not args.quick:
+        Wt = (torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16)
+        ms_nt = time_launches(lambda: ops.gemm(A, Wt.t(), C), args.steps, args.warmup, torch)
+        ms_torch = time_launches(lambda: torch.matmul(A, B, out=C), args.steps, args.warmup, torch)
+        sections["gemm_4096_bf16"] = {"NN_tflops": round(tflops, 2), "NT_tflops": round(flops / ms_nt / 1e9, 2),
+                                      "torch_hipblaslt_NN_tflops": round(flops / ms_torch / 1e9, 2)}
+        del Wt
+
+    if want("sweep") and not args.quick:
+        sweep = []
+        for (m, n, k) in [(1, 3072, 1024), (128, 3072, 1024), (2048, 151936, 1024)]:
+            for layout in ("NN", "NT"):
+                fl = 2.0 * m * n * k
+                byts = 2.0 * (m * k + k * n + m * n)
+                nb = 1 if byts > 600e6 else max(2, int(math.ceil(600e6 / byts)))  # rotate past the 256 MB MALL
+                nb = min(nb, 64)
+                mk = lambda i: (torch.randn(m, k, device=dev).to(torch.bfloat16),
+                                (torch.randn(k, n, device=dev) * 0.02).to(torch.bfloat16) if layout == "NN"
+                                else (torch.randn(n, k, device=dev) * 0.02).to(torch.bfloat16).t(),
+                                torch.empty(m, n, device=dev, dtype=torch.bfloat16))
+                nxt = rotating(nb, mk)
+
+                def run():
+                    a_, b_, c_ = nxt()
+                    ops.gemm(a_, b_, c_)
+                st = max(args.steps, 20)
+                t = time_launches(run, st, args.warmup, torch)
+                sweep.append({"M": m, "N": n, "K": k, "layout": layout, "ms": round(t, 5),
+                              "tflops": round(fl / t / 1e9, 2), "gbs": round(byts / t / 1e6, 1),
+                              "rotating_buffers": nb})
+                del nxt
+                torch.cuda.empty_cache()
+        sections["gemm_sweep_bf16"] = sweep
+
+    if want("fp32") and not args.quick:
+        a32 = torch.randn(1024, 1024, device=dev)
+        b32 = torch.randn(1024, 1024, device=dev)
+        c32 = torch.empty(1024, 1024, device=dev)
+        t = time_launches(lambda: ops.gemm(a32, b32, c32), args.steps, args.warmup, torch)
+        fl = 2.0 * 1024 ** 3
+        sections["gemm_fp32_1024"] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                                      "frac_fp32_peak": round(fl / t / 1e9 / PEAK_FP32_TFLOPS, 4)}
+
+    if want("prefill") and not args.quick:
+        pre = []
+        for S in (512, 2048, 8192):
+            q = torch.randn(1, 16, S, 128, device=dev).to(torch.bfloat16)
+            k = torch.randn(1, 8, S, 128, device=dev).to(torch.bfloat16)
+            v = torch.randn(1, 8, S, 128, device=dev).to(torch.bfloat16)
+            o = torch.empty_like(q)
+            fl = 4.0 * 1 * 16 * 128 * S * (S + 1) / 2
+            t = time_launches(lambda: ops.scaled_dot_product_attention(q, k, v, 1 / math.sqrt(128), "causal", out=o),
+                              max(args.steps // 2, 10), args.warmup, torch)
+            pre.append({"S": S, "ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                        "frac_bf16_peak": round(fl / t / 1e9 / PEAK_BF16_TFLOPS, 4)})
+        sections["attn_prefill_causal_bf16"] = pre
+
+    if want("decode") and not args.quick:
+        dec = []
+        for (Bq, ctx) in [(1, 1024), (1, 8192), (16, 1024), (16, 8192)]:
+            byts = 2.0 * Bq * 8 * ctx * 128 * 2
+            nb = min(64, max(1, int(math.ceil(600e6 / byts))))
+            mk = lambda i: (torch.randn(Bq, 16, 128, device=dev).to(torch.bfloat16),
+                            torch.randn(Bq, 8, ctx, 128, device=dev).to(torch.bfloat16),
+                            torch.randn(Bq, 8, ctx, 128, device=dev).to(torch.bfloat16),
+                            torch.empty(Bq, 16, 128, device=dev, dtype=torch.bfloat16))
+            nxt = rotating(nb, mk)
+            ws = torch.empty(ops.decode_workspace_bytes(Bq, 16, ctx, 128), dtype=torch.uint8, device=dev)
+
+            def run():
+                q_, k_, v_, o_ = nxt()
+                ops.decode_attention(q_, k_, v_, out=o_, workspace=ws)
+            t = time_launches(run, max(args.steps, 20), args.warmup, torch)
+            dec.append({"B": Bq, "ctx": ctx, "ms": round(t, 5), "gbs": round(byts / t / 1e6, 1),
+                        "frac_hbm": round(byts / t / 1e6 / PEAK_HBM_GBS, 4), "rotating_buffers": nb})
+            del nxt
+            torch.cuda.empty_cache()
+        sections["attn_decode_bf16"] = dec
+
+    if want("norm") and not args.quick:
+        S = 8192
+        qkv = torch.randn(1, S, 32 * 128, device=dev).to(torch.bfloat16)
+        wq = torch.randn(128, device=dev) * 0.02
+        wk = torch.randn(128, device=dev) * 0.02
+        ang = torch.arange(S, device=dev)[:, None] * torch.rand(1, 128, device=dev)
+        cos, sin = torch.cos(ang).contiguous(), torch.sin(ang).contiguous()
+        qo = torch.empty(1, 16, S, 128, device=dev, dtype=torch.bfloat16)
+        ko = torch.empty(1, 8, S, 128, device=dev, dtype=torch.bfloat16)
+        vo = torch.empty(1, 8, S, 128, device=dev, dtype=torch.bfloat16)
+        byts = 2.0 * 32 * 128 * S * 2 + 2.0 * S * 128 * 4
+        t = time_launches(lambda: ops.rms_norm_rope(qkv, 16, 8, 128, wq, wk, 1e-6, cos, sin, 0, qo, ko, vo),
+                          args.steps, args.warmup, torch)
+        sections["rmsnorm_rope_bf16_S8192"] = {"ms": round(t, 5), "gbs": round(byts / t / 1e6, 1),
+                                               "frac_hbm": round(byts / t / 1e6 / PEAK_HBM_GBS, 4)}
+
+    # ---- the timed headline region: exactly K steps, synchronised both sides ----
+    for _ in range(args.warmup):
+        ops.gemm(A, B, C)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ops.gemm(A, B, C)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    value = flops / (ms_step * 1e-3) / 1e12
+
+    cpu = None
+    if not args.quick and not args.no_cpu:
+        try:
+            cpu = cpu_baseline(M, N, K)
+        except Exception as exc:  # the baseline is reported, never required
+            cpu = {"error": repr(exc)}
+
+    out = {
+        "metric": "bf16 GEMM & flash-attn TFLOP/s (% MFMA peak); decode tok/s at Qwen3-0.6B shape",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (torch.randn, seed 0: A ~ N(0,1), B ~ N(0,0.02), bf16)",
+        "config": {"workload": "bf16 GEMM M=N=K=4096, A [M,K] x B [K,N] row-major, fp32 accumulate, bf16 out "
+                               "(configs[1])", "M": M, "N": N, "K": K, "layout": "NN"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        **sections,
+    }
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
