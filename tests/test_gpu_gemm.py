@@ -71,7 +71,7 @@ def test_config2_bf16_sweep(orc, yt, shape, layout):
 
 
 SMALL = [(7, 13, 5), (37, 41, 1001), (64, 64, 64), (130, 260, 96), (1, 33, 72), (5, 1, 40), (256, 512, 128),
-         (300, 200, 64), (2, 2, 2), (17, 520, 1024)]
+         (300, 200, 64), (2, 2, 2), (17, 520, 1024), (100, 272, 128), (1, 4096, 512), (513, 1040, 192), (16, 200, 256), (9, 3000, 3072)]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])

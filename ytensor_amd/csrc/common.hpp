@@ -98,6 +98,34 @@ __device__ __forceinline__ f32x4 mfma_chunk(F32, u32x4 a, u32x4 b, f32x4 c) {
     return c;
 }
 
+// gfx950 LDS data movers. The builtins exist only for the device target; the
+// host compilation pass of a kernel that names them directly drops the kernel's
+// launch stub, so they are wrapped here and compiled in the device pass only.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// global -> LDS DMA of 16 bytes per lane: lane i's 16 bytes land at
+// lds_wave_base + 16*i (lds_wave_base is wave-uniform).
+__device__ __forceinline__ void dma16(const void* gsrc, void* lds_wave_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(gsrc, lds_wave_base, 16, 0, 0);
+#endif
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j supplies the LDS byte
+// address of 4 consecutive 16-bit values R[j][0..3]; lane i receives
+// { R[4t + i/4][i%4] : t = 0..3 }.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* lds, int byte_off) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+    typedef __attribute__((address_space(3))) char lds_char_t;
+    const v4i16 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((lds_char_t*)lds + byte_off));
+    return __builtin_bit_cast(u32x2, t);
+#else
+    (void)lds; (void)byte_off;
+    return u32x2{0u, 0u};
+#endif
+}
+
 // Elements per 16-byte chunk.
 template <class T> struct Vec { static constexpr int n = 16 / sizeof(typename T::raw); };
 

@@ -260,6 +260,302 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// DMA-staged variant (the fast path). Tiles go global -> LDS with
+// global_load_lds (16 bytes per lane, no VGPR staging); the XOR swizzle is
+// applied on the global-address side because the DMA writes 64 consecutive
+// 16-byte LDS slots per wave. While the matrix cores work on one LDS stage the
+// DMA fills the other; fragments for the second 32-wide k step are read from
+// LDS before the first step's MFMAs, and a scheduling pattern interleaves the
+// LDS reads with the MFMAs.
+//   NN (B row-major [k][n], 16-bit): the B tile stays [k][n] in LDS (rows of
+//   BN elements, 32-byte blocks XOR-swizzled by row) and is read with
+//   ds_read_b64_tr_b16: within each 16-lane group, lane j addresses the 4
+//   columns 4*(j%4).. of k-row j/4 and lane i receives column i of those 4
+//   k-rows -- exactly the MFMA B operand (two reads per 16x32 fragment).
+// Requirements (checked on the host): k % BK == 0, 16-byte aligned rows, and
+// for NN: n % 16 == 0. Rows past M / N are clamped (their outputs are never
+// stored); K has no tail.
+// ---------------------------------------------------------------------------
+template <class T, class TO, int BM, int BN, int WM, int WN, bool NN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a) {
+    using raw = typename T::raw;
+    constexpr int THREADS = 64 * WM * WN;
+    constexpr int VEC = 16 / sizeof(raw);
+    constexpr int BK = 8 * VEC;
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int FM = WTM / 16, FN = WTN / 16;
+    constexpr int A_PT = BM * 8 / THREADS, B_PT = BN * 8 / THREADS;
+    static_assert(A_PT * THREADS == BM * 8 && B_PT * THREADS == BN * 8, "tile/thread mismatch");
+    static_assert(!NN || sizeof(raw) == 2, "the transposing LDS read is 16-bit");
+    constexpr int STA = BM * 8, STB = BN * 8;             // 16-byte slots per stage
+    constexpr int NBLK = BN / 16;                          // NN: 32-byte blocks per k-row
+    constexpr int BLK_MASK = (NBLK < 8 ? NBLK : 8) - 1;
+    constexpr int MF_PER_CHUNK = sizeof(raw) == 2 ? 1 : 4;
+
+    __shared__ u32x4 sbuf[2 * (STA + STB)];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int lrow = lane & 15, lgrp = lane >> 4;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int bz = blockIdx.y;
+    const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
+    const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b;
+    const int KT = a.k / BK;
+
+    auto issue = [&](int kt, u32x4* sA, u32x4* sB) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i) {
+            const int slot = i * THREADS + wave * 64 + lane;
+            const int r = slot >> 3;
+            const int c = swz(r, slot & 7);  // the swizzle is an involution on the chunk index
+            const int row = min(m0 + r, a.m - 1);
+            dma16(Ap + (int64_t)row * a.rsa + k0 + c * VEC, &sA[i * THREADS + wave * 64]);
+        }
+#pragma unroll
+        for (int i = 0; i < B_PT; ++i) {
+            const int slot = i * THREADS + wave * 64 + lane;
+            const raw* g;
+            if constexpr (!NN) {
+                const int r = slot >> 3;
+                const int c = swz(r, slot & 7);
+                const int row = min(n0 + r, a.n - 1);
+                g = Bp + (int64_t)row * a.csb + k0 + c * VEC;
+            } else {
+                const int r = slot / (2 * NBLK), ps = slot % (2 * NBLK);
+                const int lb = (ps >> 1) ^ (r & BLK_MASK);
+                g = Bp + (int64_t)(k0 + r) * a.rsb + min(n0 + lb * 16, a.n - 16) + (ps & 1) * 8;
+            }
+            dma16(g, &sB[i * THREADS + wave * 64]);
+        }
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const u32x4* sA, const u32x4* sB) {
+        u32x4 fa[2][FM], fb[2][FN];
+        auto ld = [&](int ks, int buf) {
+            const int chunk = ks * 4 + lgrp;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int r = wm * WTM + i * 16 + lrow;
+                fa[buf][i] = sA[r * 8 + swz(r, chunk)];
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                if constexpr (!NN) {
+                    const int r = wn * WTN + j * 16 + lrow;
+                    fb[buf][j] = sB[r * 8 + swz(r, chunk)];
+                } else {
+                    const int nb = (wn * WTN + j * 16) >> 4;
+                    u32x4 v;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int r = ks * 32 + 8 * lgrp + 4 * h + (lrow >> 2);
+                        const int byte = r * (BN * 2) + ((nb ^ (r & BLK_MASK)) << 5) + 8 * (lrow & 3);
+                        const u32x2 w = lds_read_tr16(sB, byte);
+                        v[2 * h] = w[0];
+                        v[2 * h + 1] = w[1];
+                    }
+                    fb[buf][j] = v;
+                }
+            }
+        };
+        ld(0, 0);
+        ld(1, 1);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma_chunk(T{}, fb[ks][j], fa[ks][i], acc[i][j]);
+#pragma unroll
+            for (int q = 0; q < FM * FN / 2; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF_PER_CHUNK, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                 // LDS read
+            }
+        }
+    };
+
+    u32x4* sA = sbuf;
+    u32x4* sB = sbuf + 2 * STA;
+    issue(0, sA, sB);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) issue(kt + 1, sA + (cur ^ 1) * STA, sB + (cur ^ 1) * STB);
+        compute(sA + cur * STA, sB + cur * STB);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA for the next stage has landed
+        __syncthreads();
+    }
+
+    using oraw = typename TO::raw;
+    oraw* Cp = static_cast<oraw*>(a.C) + bz * a.sc_b;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * WTM + i * 16 + lrow;
+        if (m >= a.m) continue;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = n0 + wn * WTN + j * 16 + lgrp * 4;
+            if (n >= a.n) continue;
+            oraw* crow = Cp + (int64_t)m * a.rsc;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = a.alpha * acc[i][j][r];
+            if (a.beta != 0.0f) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (n + r < a.n) v[r] += a.beta * load_as_f32<TO>(crow, n + r);
+            }
+            if (a.c_vec_ok && n + 3 < a.n) {
+                if constexpr (sizeof(oraw) == 2) {
+                    *reinterpret_cast<u32x2*>(crow + n) = u32x2{pack2<TO>(v[0], v[1]), pack2<TO>(v[2], v[3])};
+                } else {
+                    *reinterpret_cast<f32x4*>(crow + n) = f32x4{v[0], v[1], v[2], v[3]};
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (n + r < a.n) store_from_f32<TO>(crow, n + r, v[r]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny GEMM, M <= 16 (the decode GEMVs: x [1..16, K] . W^T). HBM-bound on
+// the weight stream, so the design goal is bytes in flight, not MFMA reuse.
+//   NT: one workgroup per 16 output columns; its 8 waves split K; each lane
+//   streams 16-byte chunks of W rows, UNR chunks in flight, into a
+//   v_mfma_f32_16x16x32 with the (zero-padded) M rows of A; the 8 partial
+//   16x16 tiles are summed through LDS. The MFMA is used as a 16-lane dot-
+//   product reducer here, its flops are free against the byte stream.
+//   NN (B [K][N] row-major): VALU; lane = one output column, coalesced 2-byte
+//   row loads, 8 waves split K, LDS reduction.
+// ---------------------------------------------------------------------------
+constexpr int SKINNY_M = 16;
+constexpr int SKINNY_WAVES = 8;
+
+template <class T, class TO>
+__global__ __launch_bounds__(64 * SKINNY_WAVES) void gemm_skinny_nt_kernel(GemmArgs a) {
+    using raw = typename T::raw;
+    constexpr int VEC = 16 / sizeof(raw);
+    constexpr int KSTEP = 4 * VEC;  // k covered by one MFMA chunk across the 4 lane groups
+    constexpr int UNR = 4;
+    constexpr int MF_PER_CHUNK = sizeof(raw) == 2 ? 1 : 4;
+    (void)MF_PER_CHUNK;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int bz = blockIdx.y;
+    const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
+    const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b;
+    const int nsteps = (a.k + KSTEP - 1) / KSTEP;
+    const int per_wave = (nsteps + SKINNY_WAVES - 1) / SKINNY_WAVES;
+    const int s_begin = wave * per_wave, s_end = min(nsteps, s_begin + per_wave);
+    const bool arow = r < a.m, brow = n0 + r < a.n;
+    const raw* arp = Ap + (int64_t)(arow ? r : 0) * a.rsa + g * VEC;
+    const raw* brp = Bp + (int64_t)(brow ? n0 + r : 0) * a.csb + g * VEC;
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s = s_begin; s < s_end; s += UNR) {
+        u32x4 fb[UNR], fa[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int k = (s + u) * KSTEP + g * VEC;
+            const bool ok = (s + u < s_end) && k < a.k;
+            fb[u] = (ok && brow) ? *reinterpret_cast<const u32x4*>(brp + (int64_t)(s + u) * KSTEP) : u32x4{0, 0, 0, 0};
+            fa[u] = (ok && arow) ? *reinterpret_cast<const u32x4*>(arp + (int64_t)(s + u) * KSTEP) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) acc = mfma_chunk(T{}, fb[u], fa[u], acc);
+    }
+    // acc: lane holds C[m = r][n0 + 4g + j]; sum the 8 waves' tiles.
+    __shared__ f32x4 red[SKINNY_WAVES][64];
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4 t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < SKINNY_WAVES; ++w) t += red[w][lane];
+    if (r >= a.m) return;
+    using oraw = typename TO::raw;
+    oraw* crow = static_cast<oraw*>(a.C) + bz * a.sc_b + (int64_t)r * a.rsc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 4 * g + j;
+        if (n >= a.n) continue;
+        float v = a.alpha * t[j];
+        if (a.beta != 0.0f) v += a.beta * load_as_f32<TO>(crow, n);
+        store_from_f32<TO>(crow, n, v);
+    }
+}
+
+template <class T, class TO>
+__global__ __launch_bounds__(64 * SKINNY_WAVES) void gemm_skinny_nn_kernel(GemmArgs a) {
+    using raw = typename T::raw;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = blockIdx.x * 64 + lane;
+    const int bz = blockIdx.y;
+    const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
+    const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b;
+    const int per_wave = (a.k + SKINNY_WAVES - 1) / SKINNY_WAVES;
+    const int k_begin = wave * per_wave, k_end = min(a.k, k_begin + per_wave);
+    float acc[SKINNY_M];
+#pragma unroll
+    for (int i = 0; i < SKINNY_M; ++i) acc[i] = 0.f;
+    const bool col = n < a.n;
+    const raw* bp = Bp + (col ? n : 0);
+    constexpr int UNR = 8;
+    int k = k_begin;
+    for (; k + UNR <= k_end; k += UNR) {
+        float b[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) b[u] = col ? load_as_f32<T>(bp, (int64_t)(k + u) * a.rsb) : 0.f;
+#pragma unroll
+        for (int i = 0; i < SKINNY_M; ++i) {
+            if (i < a.m) {
+#pragma unroll
+                for (int u = 0; u < UNR; ++u) acc[i] = fmaf(load_as_f32<T>(Ap, (int64_t)i * a.rsa + k + u), b[u], acc[i]);
+            }
+        }
+    }
+    for (; k < k_end; ++k) {
+        const float b = col ? load_as_f32<T>(bp, (int64_t)k * a.rsb) : 0.f;
+#pragma unroll
+        for (int i = 0; i < SKINNY_M; ++i)
+            if (i < a.m) acc[i] = fmaf(load_as_f32<T>(Ap, (int64_t)i * a.rsa + k), b, acc[i]);
+    }
+    __shared__ float red[SKINNY_WAVES][SKINNY_M][64];
+#pragma unroll
+    for (int i = 0; i < SKINNY_M; ++i) red[wave][i][lane] = acc[i];
+    __syncthreads();
+    if (wave != 0 || !col) return;
+    using oraw = typename TO::raw;
+    for (int i = 0; i < a.m; ++i) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < SKINNY_WAVES; ++w) t += red[w][i][lane];
+        oraw* crow = static_cast<oraw*>(a.C) + bz * a.sc_b + (int64_t)i * a.rsc;
+        float v = a.alpha * t;
+        if (a.beta != 0.0f) v += a.beta * load_as_f32<TO>(crow, n);
+        store_from_f32<TO>(crow, n, v);
+    }
+}
+
 // Any-stride fallback: one output per thread, fp32 accumulation in k order.
 struct GenericArgs {
     const void* A;
@@ -317,6 +613,33 @@ hipError_t launch_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <class T, class TO, int BM, int BN, int WM, int WN>
+hipError_t launch_dma_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s) {
+    GemmArgs a = a0;
+    a.tiles_m = (a.m + BM - 1) / BM;
+    a.tiles_n = (a.n + BN - 1) / BN;
+    dim3 grid(a.tiles_m * a.tiles_n, batch);
+    dim3 block(64 * WM * WN);
+    if constexpr (sizeof(typename T::raw) == 2) {
+        if (nn) {
+            gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, true><<<grid, block, 0, s>>>(a);
+            return hipGetLastError();
+        }
+    }
+    gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, false><<<grid, block, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+template <class T, class TO>
+hipError_t launch_dma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
+    auto tiles = [&](int bm, int bn) {
+        return (int64_t)((a.m + bm - 1) / bm) * ((a.n + bn - 1) / bn) * batch;
+    };
+    if (tiles(256, 256) >= 160) return launch_dma_tile<T, TO, 256, 256, 2, 4>(a, nn, batch, s);
+    if (tiles(128, 128) >= 96) return launch_dma_tile<T, TO, 128, 128, 2, 2>(a, nn, batch, s);
+    return launch_dma_tile<T, TO, 64, 64, 2, 2>(a, nn, batch, s);
+}
+
 template <class T, class TO>
 hipError_t launch_mfma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
     auto tiles = [&](int bm, int bn) {
@@ -366,6 +689,21 @@ int gemm_typed(int batch, int m, int n, int k, const void* A, int64_t sa_b, int6
         g.sa_b = sa_b; g.sb_b = sb_b; g.sc_b = sc_b;
         g.alpha = alpha; g.beta = beta;
         g.c_vec_ok = (rsc % 4 == 0) && (sc_b % 4 == 0) && aligned(C, 4 * sizeof(oraw));
+        if (m <= SKINNY_M) {
+            dim3 block(64 * SKINNY_WAVES);
+            if (nt) {
+                gemm_skinny_nt_kernel<T, TO><<<dim3((n + 15) / 16, batch), block, 0, s>>>(g);
+            } else {
+                gemm_skinny_nn_kernel<T, TO><<<dim3((n + 63) / 64, batch), block, 0, s>>>(g);
+            }
+            return status_of(hipGetLastError());
+        }
+        // DMA-staged fast path: whole k steps, 16-byte aligned rows everywhere.
+        const bool dma_k = (k % (8 * VEC)) == 0;
+        const bool dma_nt = nt;
+        const bool dma_nn = nn && es == 2 && (rsb % VEC) == 0 && (sb_b % VEC) == 0 && (n % 16) == 0 &&
+                            aligned(B, 16);
+        if (dma_k && (dma_nt || dma_nn)) return status_of(launch_dma<T, TO>(g, nn, batch, s));
         return status_of(launch_mfma<T, TO>(g, nn, batch, s));
     }
     GenericArgs g{A, B, C, m, n, k, rsa, csa, rsb, csb, rsc, csc, sa_b, sb_b, sc_b, alpha, beta};
