@@ -52,28 +52,55 @@ struct AttnArgs {
     int nqb;
 };
 
-__device__ __forceinline__ uint32_t half_of(u32x4 v, int i) { return (v[i >> 1] >> (16 * (i & 1))) & 0xffffu; }
-
 // MODE 0: no mask; 1: causal; 2: byte mask and/or bias read per element.
-template <class T, int D, int MODE>
-__global__ __launch_bounds__(256, 2) void attn_fwd_mfma(AttnArgs a) {
+// GH query heads of one GQA group share a workgroup (4 waves per head, 32
+// queries per wave), so each K/V tile is staged once for GH*128 queries.
+// K and V tiles reach LDS by DMA (global_load_lds, 16 bytes per lane), both
+// kept in their natural [key][d] layout:
+//   K rows: 16-byte chunk c stored at c ^ (key & 7) -> the S^T operand is one
+//           conflict-free ds_read_b128 per lane.
+//   V rows: 32-byte block b stored at b ^ (key & BMASK) and read transposed by
+//           ds_read_b64_tr_b16: lane j of a 16-lane group addresses 4 d-values
+//           of key (kt*16 + 4*grp + j/4); lane i receives d = i of 4 keys,
+//           i.e. the V^T operand in the key order P was packed in.
+// Workgroup order: the hardware deals workgroups to the 8 XCDs round-robin;
+// the linear id is remapped so each XCD walks a contiguous range of
+// (kv head, query block) pairs -- one KV head's K/V stays in one XCD's L2 --
+// and, for causal masks, the longest query blocks start first.
+template <class T, int D, int MODE, int GH>
+__global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     using raw = typename T::raw;
+    constexpr int THREADS = 256 * GH;
     constexpr int BQ = 128, BKV = 64, WQ = 32;
-    constexpr int KCH = D / 8;   // 16-byte chunks per K row
-    constexpr int DT = D / 16;   // output d tiles
-    constexpr int KS = D / 32;   // d steps of the score MFMA
-    constexpr int K_PT = BKV * KCH / 256;
-    constexpr int V_GROUPS = (BKV / 4) * (D / 8);  // 4 keys x 8 d per group
+    constexpr int KCH = D / 8;    // 16-byte chunks per K/V row
+    constexpr int DT = D / 16;    // output d tiles
+    constexpr int KS = D / 32;    // d steps of the score MFMA
+    constexpr int PT = BKV * KCH / THREADS;
+    static_assert(PT * THREADS == BKV * KCH, "tile / thread mismatch");
+    constexpr int NB = D / 16;    // 32-byte blocks per V row
+    constexpr int BMASK = (NB < 8 ? NB : 8) - 1;
+    constexpr int STG = BKV * KCH;  // u32x4 slots per tile
 
-    __shared__ u32x4 sK[2][BKV * KCH];
-    __shared__ u32x2 sV[2][D * (BKV / 4)];
+    __shared__ u32x4 sK[2 * STG];
+    __shared__ u32x4 sV[2 * STG];
 
-    const int qb = (MODE == 1) ? (a.nqb - 1 - (int)blockIdx.x) : (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
-    const int kvh = h / (a.Hq / a.Hkv);
+    // (batch, kv head or head pair, query block) from the XCD-remapped id.
+    const int G = a.Hq / a.Hkv;
+    const int hgroups = G / GH;                 // head groups per kv head
+    const int units = a.B * a.Hkv * hgroups;    // (b, kvh, head group) units
+    const int total = units * a.nqb;
+    int w = blockIdx.x;
+    if ((total & 7) == 0) w = (w & 7) * (total >> 3) + (w >> 3);
+    const int unit = w / a.nqb;
+    const int qi = w % a.nqb;
+    const int qb = (MODE == 1) ? (a.nqb - 1 - qi) : qi;
+    const int b = unit / (a.Hkv * hgroups);
+    const int rem = unit % (a.Hkv * hgroups);
+    const int kvh = rem / hgroups;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = kvh * G + (rem % hgroups) * GH + (wave >> 2);
     const int l16 = lane & 15, g = lane >> 4;
-    const int q0 = qb * BQ + wave * WQ;
+    const int q0 = qb * BQ + (wave & 3) * WQ;
 
     const raw* Qp = static_cast<const raw*>(a.Q) + b * a.qs0 + h * a.qs1;
     const raw* Kp = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1;
@@ -95,64 +122,38 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(AttnArgs a) {
     int kv_end = a.Skv;
     if (MODE == 1) kv_end = min(a.Skv, qb * BQ + BQ + off);
     const int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;
+    const float c = a.scale_log2;
 
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};  // m in raw score units
     f32x4 o[2][DT];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 rk[K_PT];
-    u32x4 rv[4];
-    const int v_kq = tid & 15, v_dc = tid >> 4;  // V group: keys 4*v_kq.., d 8*v_dc..
-
-    auto load_kv = [&](int kb) {
+    auto issue = [&](int kb, int st) {
         const int k0 = kb * BKV;
 #pragma unroll
-        for (int i = 0; i < K_PT; ++i) {
-            const int id = tid + i * 256;
-            const int key = id / KCH, c = id % KCH;
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (k0 + key < a.Skv) v = *reinterpret_cast<const u32x4*>(Kp + (int64_t)(k0 + key) * a.ks2 + c * 8);
-            rk[i] = v;
-        }
-        if (V_GROUPS == 256 || tid < V_GROUPS) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = k0 + v_kq * 4 + r;
-                u32x4 v = {0u, 0u, 0u, 0u};
-                if (key < a.Skv) v = *reinterpret_cast<const u32x4*>(Vp + (int64_t)key * a.vs2 + v_dc * 8);
-                rv[r] = v;
-            }
-        }
-    };
-    auto store_kv = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < K_PT; ++i) {
-            const int id = tid + i * 256;
-            const int key = id / KCH, c = id % KCH;
-            sK[st][key * KCH + (c ^ (key & 7))] = rk[i];
-        }
-        if (V_GROUPS == 256 || tid < V_GROUPS) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int row = v_dc * 8 + i;
-                u32x2 w = {half_of(rv[0], i) | (half_of(rv[1], i) << 16), half_of(rv[2], i) | (half_of(rv[3], i) << 16)};
-                sV[st][row * 16 + (v_kq ^ (row & 15))] = w;
-            }
+        for (int i = 0; i < PT; ++i) {
+            const int slot = i * THREADS + wave * 64 + lane;
+            const int row = slot / KCH, ps = slot % KCH;
+            const int64_t key = min(k0 + row, a.Skv - 1);
+            const int kc = ps ^ (row & 7);
+            dma16(Kp + key * a.ks2 + kc * 8, &sK[st * STG + i * THREADS + wave * 64]);
+            const int vb = (ps >> 1) ^ (row & BMASK);
+            dma16(Vp + key * a.vs2 + vb * 16 + (ps & 1) * 8, &sV[st * STG + i * THREADS + wave * 64]);
         }
     };
 
-    if (nkb > 0) {
-        load_kv(0);
-        store_kv(0);
-    }
+    if (nkb > 0) issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     for (int kb = 0; kb < nkb; ++kb) {
         const int cur = kb & 1;
-        if (kb + 1 < nkb) load_kv(kb + 1);
+        if (kb + 1 < nkb) issue(kb + 1, cur ^ 1);
+        const u32x4* cK = sK + cur * STG;
+        const u32x4* cV = sV + cur * STG;
         const int k0 = kb * BKV;
         // Wave-uniform: does this block hold any key visible to this wave's queries?
         const bool active = (MODE != 1) || (k0 <= q0 + WQ - 1 + off);
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(AttnArgs a) {
 #pragma unroll
                 for (int kt = 0; kt < 4; ++kt) {
                     const int key = kt * 16 + l16;
-                    const u32x4 kf = sK[cur][key * KCH + ((ks * 4 + g) ^ (key & 7))];
+                    const u32x4 kf = cK[key * KCH + ((ks * 4 + g) ^ (key & 7))];
 #pragma unroll
                     for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma_chunk(T{}, kf, qf[qt][ks], s[qt][kt]);
                 }
@@ -175,47 +176,55 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(AttnArgs a) {
             const bool need_mask = (MODE == 2) || (k0 + BKV > a.Skv) ||
                                    (MODE == 1 && k0 + BKV - 1 > q0 + off);
             u32x4 pk[2][2];
+            bool rescale = false;
+            float alpha[2];
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
                 const int qa = q0 + qt * 16 + l16;
                 float v[4][4];
-                float mx = -INFINITY;
+                if (need_mask) {
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
+                    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        float x = s[qt][kt][r] * a.scale_log2;
-                        if (need_mask) {
+                        for (int r = 0; r < 4; ++r) {
+                            float x = s[qt][kt][r];
                             const int key = k0 + kt * 16 + g * 4 + r;
                             bool vis = key < a.Skv;
                             if (MODE == 1) vis = vis && (key <= qa + off);
                             if (MODE == 2 && vis && qa < a.Sq) {
                                 if (a.mask != nullptr) vis = a.mask[(int64_t)qa * a.mask_ld + key] != 0;
+                                // bias is added after scaling: fold it into raw units
                                 if (vis && a.bias != nullptr)
-                                    x += a.bias[(int64_t)qa * a.brs + (int64_t)key * a.bcs] * LOG2E;
+                                    x += a.bias[(int64_t)qa * a.brs + (int64_t)key * a.bcs] * LOG2E / c;
                             }
-                            x = vis ? x : -INFINITY;
+                            v[kt][r] = vis ? x : -INFINITY;
                         }
-                        v[kt][r] = x;
-                        mx = fmaxf(mx, x);
-                    }
+                } else {
+#pragma unroll
+                    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) v[kt][r] = s[qt][kt][r];
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+                    mx = fmaxf(mx, fmaxf(fmaxf(v[kt][0], v[kt][1]), fmaxf(v[kt][2], v[kt][3])));
                 mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
                 mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
                 const float m_new = fmaxf(m[qt], mx);
-                const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-                const float alpha = exp2f(m[qt] - m_use);
+                const float mc = (m_new == -INFINITY) ? 0.f : m_new * c;
+                alpha[qt] = __builtin_amdgcn_exp2f(m[qt] * c - mc);
+                rescale |= (m_new != m[qt]);
                 float sum = 0.f;
 #pragma unroll
                 for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        v[kt][r] = exp2f(v[kt][r] - m_use);
+                        v[kt][r] = __builtin_amdgcn_exp2f(fmaf(v[kt][r], c, -mc));
                         sum += v[kt][r];
                     }
-                l[qt] = l[qt] * alpha + sum;
+                l[qt] = fmaf(l[qt], alpha[qt], sum);
                 m[qt] = m_new;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha;
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     pk[qt][kk] = u32x4{pack2<T>(v[2 * kk][0], v[2 * kk][1]), pack2<T>(v[2 * kk][2], v[2 * kk][3]),
@@ -223,21 +232,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma(AttnArgs a) {
                                        pack2<T>(v[2 * kk + 1][2], v[2 * kk + 1][3])};
                 }
             }
+            // O *= alpha only when some lane's running max moved in this block.
+            if (__ballot(rescale) != 0) {
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha[qt];
+            }
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
-                    const int row = dt * 16 + l16;
-                    const int qa_ = 8 * kk + g, qb_ = 8 * kk + 4 + g;
-                    const u32x2 va = sV[cur][row * 16 + (qa_ ^ (row & 15))];
-                    const u32x2 vb = sV[cur][row * 16 + (qb_ ^ (row & 15))];
-                    const u32x4 vf = {va[0], va[1], vb[0], vb[1]};
+                    u32x4 vf;
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int key = (2 * kk + hh) * 16 + g * 4 + (l16 >> 2);
+                        const int byte = key * (D * 2) + ((dt ^ (key & BMASK)) << 5) + 8 * (l16 & 3);
+                        const u32x2 w2 = lds_read_tr16(cV, byte);
+                        vf[2 * hh] = w2[0];
+                        vf[2 * hh + 1] = w2[1];
+                    }
 #pragma unroll
                     for (int qt = 0; qt < 2; ++qt) o[qt][dt] = mfma_chunk(T{}, vf, pk[qt][kk], o[qt][dt]);
                 }
             }
         }
-        if (kb + 1 < nkb) store_kv(cur ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 
@@ -486,14 +506,23 @@ namespace {
 
 bool al(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
+template <class T, int D, int GH>
+hipError_t launch_prefill_gh(AttnArgs a, int mode, hipStream_t s) {
+    a.nqb = (a.Sq + 127) / 128;
+    dim3 grid(a.nqb * a.B * a.Hq / GH);
+    if (mode == 0) attn_fwd_mfma<T, D, 0, GH><<<grid, 256 * GH, 0, s>>>(a);
+    else if (mode == 1) attn_fwd_mfma<T, D, 1, GH><<<grid, 256 * GH, 0, s>>>(a);
+    else attn_fwd_mfma<T, D, 2, GH><<<grid, 256 * GH, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 template <class T, int D>
 hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
-    a.nqb = (a.Sq + 127) / 128;
-    dim3 grid(a.nqb, a.Hq, a.B);
-    if (mode == 0) attn_fwd_mfma<T, D, 0><<<grid, 256, 0, s>>>(a);
-    else if (mode == 1) attn_fwd_mfma<T, D, 1><<<grid, 256, 0, s>>>(a);
-    else attn_fwd_mfma<T, D, 2><<<grid, 256, 0, s>>>(a);
-    return hipGetLastError();
+    // Two query heads per workgroup (K/V staged once for both) when the GQA
+    // group size is even and the paired grid still covers the 256 CUs twice.
+    const int64_t paired = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq / 2;
+    if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) return launch_prefill_gh<T, D, 2>(a, mode, s);
+    return launch_prefill_gh<T, D, 1>(a, mode, s);
 }
 
 template <class T>
@@ -509,6 +538,7 @@ int prefill_typed(AttnArgs a, hipStream_t s) {
     const bool simple_mask = a.mask == nullptr && a.bias == nullptr;
     const int mode = a.causal ? 1 : (simple_mask ? 0 : 2);
     const bool mfma_ok = es == 2 && (a.D == 64 || a.D == 128) && a.Dv == a.D && !(a.causal && !simple_mask) &&
+                         a.scale_log2 > 0.f &&
                          al(a.Q, 16) && al(a.K, 16) && al(a.V, 16) && al(a.O, 8) &&
                          a.qs0 % 8 == 0 && a.qs1 % 8 == 0 && a.qs2 % 8 == 0 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
                          a.ks2 % 8 == 0 && a.vs0 % 8 == 0 && a.vs1 % 8 == 0 && a.vs2 % 8 == 0 &&

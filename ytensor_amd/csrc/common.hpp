@@ -25,11 +25,14 @@ struct F32 { using raw = float; static constexpr int code = YTHIP_F32; };
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// fp32 -> bf16, IEEE round-to-nearest-even; NaN stays NaN.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 with the gfx950 converter (v_cvt_pk_bf16_f32): IEEE
+// round-to-nearest-even, NaN stays NaN.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -64,11 +67,12 @@ template <> __device__ __forceinline__ void store_from_f32<F16>(void* p, int64_t
 }
 
 template <class T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+// Two fp32 -> one packed 16-bit pair (low half = a), one conversion instruction.
 template <> __device__ __forceinline__ uint32_t pack2<BF16>(float a, float b) {
-    return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2_t));
 }
 template <> __device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
-    return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), f16x2_t));
 }
 
 __device__ __forceinline__ float lo_as_f32(BF16, uint32_t w) { return bf16_bits_to_f32(w & 0xffffu); }
