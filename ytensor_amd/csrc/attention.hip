@@ -358,7 +358,7 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
     using raw = typename T::raw;
     constexpr int LPK = D / 8;          // lanes per key
     constexpr int SLOTS = 256 / LPK;    // keys in flight per workgroup
-    constexpr int UNR = 2;
+    constexpr int UNR = 4;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int slot = tid / LPK, part = tid % LPK;
@@ -392,52 +392,64 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
         for (int u = 0; u < UNR; ++u) {
             const int key = k0 + u * SLOTS;
             ok[u] = key < kend;
+            const int kk = ok[u] ? key : kbeg;  // clamped: loaded but never used
+            const raw* kp = Kb + (int64_t)kk * a.ks2;
+            const raw* vp = Vb + (int64_t)kk * a.ks2;
+            if constexpr (sizeof(raw) == 2) {
+                const u32x4 kw = *reinterpret_cast<const u32x4*>(kp);
+                const u32x4 vw = *reinterpret_cast<const u32x4*>(vp);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) { kx[u][e] = 0.f; vx[u][e] = 0.f; }
-            if (ok[u]) {
-                const raw* kp = Kb + (int64_t)key * a.ks2;
-                const raw* vp = Vb + (int64_t)key * a.ks2;
-                if constexpr (sizeof(raw) == 2) {
-                    const u32x4 kw = *reinterpret_cast<const u32x4*>(kp);
-                    const u32x4 vw = *reinterpret_cast<const u32x4*>(vp);
+                for (int e = 0; e < 4; ++e) {
+                    kx[u][2 * e] = lo_as_f32(T{}, kw[e]);
+                    kx[u][2 * e + 1] = hi_as_f32(T{}, kw[e]);
+                    vx[u][2 * e] = lo_as_f32(T{}, vw[e]);
+                    vx[u][2 * e + 1] = hi_as_f32(T{}, vw[e]);
+                }
+            } else {
+                const f32x4 k_lo = *reinterpret_cast<const f32x4*>(kp);
+                const f32x4 k_hi = *reinterpret_cast<const f32x4*>(kp + 4);
+                const f32x4 v_lo = *reinterpret_cast<const f32x4*>(vp);
+                const f32x4 v_hi = *reinterpret_cast<const f32x4*>(vp + 4);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        kx[u][2 * e] = lo_as_f32(T{}, kw[e]);
-                        kx[u][2 * e + 1] = hi_as_f32(T{}, kw[e]);
-                        vx[u][2 * e] = lo_as_f32(T{}, vw[e]);
-                        vx[u][2 * e + 1] = hi_as_f32(T{}, vw[e]);
-                    }
-                } else {
-                    const f32x4 k_lo = *reinterpret_cast<const f32x4*>(kp);
-                    const f32x4 k_hi = *reinterpret_cast<const f32x4*>(kp + 4);
-                    const f32x4 v_lo = *reinterpret_cast<const f32x4*>(vp);
-                    const f32x4 v_hi = *reinterpret_cast<const f32x4*>(vp + 4);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        kx[u][e] = k_lo[e]; kx[u][e + 4] = k_hi[e];
-                        vx[u][e] = v_lo[e]; vx[u][e + 4] = v_hi[e];
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    kx[u][e] = k_lo[e]; kx[u][e + 4] = k_hi[e];
+                    vx[u][e] = v_lo[e]; vx[u][e + 4] = v_hi[e];
                 }
             }
         }
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
+        for (int gi = 0; gi < G; ++gi) {
+            float sc[UNR];
+            float mx = m[gi];
 #pragma unroll
-            for (int gi = 0; gi < G; ++gi) {
-                float s = 0.f;
+            for (int u = 0; u < UNR; ++u) {
+                float sv = 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) s = fmaf(q[gi][e], kx[u][e], s);
+                for (int e = 0; e < 8; ++e) sv = fmaf(q[gi][e], kx[u][e], sv);
 #pragma unroll
-                for (int w = LPK / 2; w >= 1; w >>= 1) s += __shfl_xor(s, w, LPK);
-                if (!ok[u]) continue;
-                const float m_new = fmaxf(m[gi], s);
-                const float corr = exp2f(m[gi] - m_new);
-                const float p = exp2f(s - m_new);
-                l[gi] = fmaf(l[gi], corr, p);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[gi][e] = fmaf(o[gi][e], corr, p * vx[u][e]);
-                m[gi] = m_new;
+                for (int w = LPK / 2; w >= 1; w >>= 1) sv += __shfl_xor(sv, w, LPK);
+                sc[u] = ok[u] ? sv : -INFINITY;
+                mx = fmaxf(mx, sc[u]);
             }
+            // One correction per UNR keys; the running max stays finite once any key was seen.
+            const float m_use = (mx == -INFINITY) ? 0.f : mx;
+            const float corr = __builtin_amdgcn_exp2f(m[gi] - m_use);
+            float psum = 0.f;
+            float p[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                p[u] = __builtin_amdgcn_exp2f(sc[u] - m_use);
+                psum += p[u];
+            }
+            l[gi] = fmaf(l[gi], corr, psum);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float acc = o[gi][e] * corr;
+#pragma unroll
+                for (int u = 0; u < UNR; ++u) acc = fmaf(p[u], vx[u][e], acc);
+                o[gi][e] = acc;
+            }
+            m[gi] = mx;
         }
     }
 
@@ -464,7 +476,7 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
             for (int sl = 0; sl < SLOTS; ++sl) {
                 const float ms = s_ml[sl][gi][0];
                 if (ms == -INFINITY) continue;
-                const float w = exp2f(ms - M);
+                const float w = __builtin_amdgcn_exp2f(ms - M);
                 L = fmaf(s_ml[sl][gi][1], w, L);
                 acc = fmaf(s_o[sl][gi][d], w, acc);
             }

@@ -277,7 +277,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs a) {
 // for NN: n % 16 == 0. Rows past M / N are clamped (their outputs are never
 // stored); K has no tail.
 // ---------------------------------------------------------------------------
-template <class T, class TO, int BM, int BN, int WM, int WN, bool NN>
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
+// left at their "no wait" maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <class T, class TO, int BM, int BN, int WM, int WN, bool NN, int STAGES>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a) {
     using raw = typename T::raw;
     constexpr int THREADS = 64 * WM * WN;
@@ -293,7 +302,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
     constexpr int BLK_MASK = (NBLK < 8 ? NBLK : 8) - 1;
     constexpr int MF_PER_CHUNK = sizeof(raw) == 2 ? 1 : 4;
 
-    __shared__ u32x4 sbuf[2 * (STA + STB)];
+    constexpr int PER = A_PT + B_PT;  // DMA instructions per thread per stage
+    static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 2) * PER < 64, "pipeline depth");
+
+    __shared__ u32x4 sbuf[STAGES * (STA + STB)];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -389,16 +401,35 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
     };
 
     u32x4* sA = sbuf;
-    u32x4* sB = sbuf + 2 * STA;
-    issue(0, sA, sB);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) issue(kt + 1, sA + (cur ^ 1) * STA, sB + (cur ^ 1) * STB);
-        compute(sA + cur * STA, sB + cur * STB);
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA for the next stage has landed
+    u32x4* sB = sbuf + STAGES * STA;
+    if constexpr (STAGES == 2) {
+        // Double buffer: DMA of step kt+1 overlaps the MFMAs of step kt.
+        issue(0, sA, sB);
+        wait_vmcnt<0>();
         __syncthreads();
+        for (int kt = 0; kt < KT; ++kt) {
+            const int cur = kt & 1;
+            if (kt + 1 < KT) issue(kt + 1, sA + (cur ^ 1) * STA, sB + (cur ^ 1) * STB);
+            compute(sA + cur * STA, sB + cur * STB);
+            wait_vmcnt<0>();  // this wave's DMA for the next step has landed
+            __syncthreads();
+        }
+    } else {
+    // STAGES-deep ring: STAGES-1 k steps are in flight while one is computed.
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < KT) issue(st, sA + st * STA, sB + st * STB);
+    for (int kt = 0; kt < KT; ++kt) {
+        // Stage kt has landed for this wave once at most `ahead` later stages are outstanding.
+        const int ahead = min(STAGES - 2, KT - 1 - kt);
+        if (STAGES > 2 && ahead >= 2) wait_vmcnt<(STAGES > 2 ? 2 : 0) * PER>();
+        else if (STAGES > 2 && ahead == 1) wait_vmcnt<PER>();
+        else wait_vmcnt<0>();
+        __syncthreads();  // every wave's share of stage kt is in LDS; stage kt-1 is consumed
+        const int nxt = kt + STAGES - 1;
+        if (nxt < KT) issue(nxt, sA + (nxt % STAGES) * STA, sB + (nxt % STAGES) * STB);
+        compute(sA + (kt % STAGES) * STA, sB + (kt % STAGES) * STB);
+    }
     }
 
     using oraw = typename TO::raw;
@@ -613,7 +644,7 @@ hipError_t launch_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <class T, class TO, int BM, int BN, int WM, int WN>
+template <class T, class TO, int BM, int BN, int WM, int WN, int STAGES>
 hipError_t launch_dma_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s) {
     GemmArgs a = a0;
     a.tiles_m = (a.m + BM - 1) / BM;
@@ -622,11 +653,11 @@ hipError_t launch_dma_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s
     dim3 block(64 * WM * WN);
     if constexpr (sizeof(typename T::raw) == 2) {
         if (nn) {
-            gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, true><<<grid, block, 0, s>>>(a);
+            gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, true, STAGES><<<grid, block, 0, s>>>(a);
             return hipGetLastError();
         }
     }
-    gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, false><<<grid, block, 0, s>>>(a);
+    gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, false, STAGES><<<grid, block, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -635,9 +666,9 @@ hipError_t launch_dma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
     auto tiles = [&](int bm, int bn) {
         return (int64_t)((a.m + bm - 1) / bm) * ((a.n + bn - 1) / bn) * batch;
     };
-    if (tiles(256, 256) >= 160) return launch_dma_tile<T, TO, 256, 256, 2, 4>(a, nn, batch, s);
-    if (tiles(128, 128) >= 96) return launch_dma_tile<T, TO, 128, 128, 2, 2>(a, nn, batch, s);
-    return launch_dma_tile<T, TO, 64, 64, 2, 2>(a, nn, batch, s);
+    if (tiles(256, 256) >= 160) return launch_dma_tile<T, TO, 256, 256, 2, 4, 2>(a, nn, batch, s);
+    if (tiles(128, 128) >= 96) return launch_dma_tile<T, TO, 128, 128, 2, 2, 4>(a, nn, batch, s);
+    return launch_dma_tile<T, TO, 64, 64, 2, 2, 4>(a, nn, batch, s);
 }
 
 template <class T, class TO>
