@@ -119,6 +119,8 @@ int ythip_attn_decode(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
  * wq / wk (fp32 [d]) may be NULL to skip that norm; cos/sin (fp32 [*, ld_tab],
  * from RoPECache::precompute, qwen3.cpp:161-175) may be NULL to skip RoPE.
  * Output strides are (batch, head, row); d is contiguous. K/V outputs may be NULL.
+ * dev_pos: optional device int32; when given, pos0 and cache_pos are both read
+ * from it when the kernel runs (a decode step captured once in a HIP graph).
  */
 int ythip_rmsnorm_rope(int dtype, int B, int S, int Hq, int Hkv, int d,
                        const void* qkv, int64_t ld_qkv,
@@ -127,15 +129,50 @@ int ythip_rmsnorm_rope(int dtype, int B, int S, int Hq, int Hkv, int d,
                        void* Qout, const int64_t q_str[3],
                        void* Kout, const int64_t k_str[3],
                        void* Vout, const int64_t v_str[3],
-                       int cache_pos, void* stream);
+                       int cache_pos, const int32_t* dev_pos, void* stream);
 
 /*
  * RMSNorm over the last axis of [rows, n] (the hidden-state norms of the Qwen3
  * layers, src/function/normalization.inl:256-267): y = x / sqrt(mean(x^2)+eps) * w.
- * x/y rows at stride ld_x / ld_y (in place allowed); w fp32 [n].
+ * x/y rows at stride ld_x / ld_y (in place allowed when the dtypes match);
+ * w fp32 [n]. dtype_in/dtype_out may differ (fp32 residual -> bf16 GEMM input).
  */
-int ythip_rms_norm(int dtype, int rows, int n, const void* x, int64_t ld_x,
+int ythip_rms_norm(int dtype_in, int dtype_out, int rows, int n, const void* x, int64_t ld_x,
                    const float* w, float eps, void* y, int64_t ld_y, void* stream);
+
+/*
+ * SwiGLU over a fused gate_up projection (Qwen3MLP::forward,
+ * example/qwen3/src/qwen3.cpp:193-200): for each row r and j < n,
+ *   out[r][j] = swish(gu[r][j]) * gu[r][n + j],  swish(a) = a * sigmoid(a)
+ * with the stable sigmoid of src/ytensor_function.inl:43-52.
+ */
+int ythip_silu_mul(int dtype_in, int dtype_out, int rows, int n, const void* gate_up, int64_t ld_gu,
+                   void* out, int64_t ld_out, void* stream);
+
+/*
+ * Embedding gather (Qwen3Model::forward, example/qwen3/src/qwen3.cpp:378-385):
+ *   out[r][:] = table[ids[r]][:]   (table [V, n], ids device int32[rows])
+ */
+int ythip_embedding(int dtype_table, int dtype_out, int rows, int n, const void* table,
+                    const int32_t* ids, void* out, int64_t ld_out, void* stream);
+
+/*
+ * Greedy token selection over fp32 logits [n]: *token = first index of the
+ * maximum. If state (device int32[3] = {generated, position, kv_len}) is given:
+ * history[state[0]] = token (history may be NULL), then state[0] += 1,
+ * state[1] += 1, state[2] = state[1] + 1 -- the counters the next decode step's
+ * ythip_rmsnorm_rope (dev_pos = &state[1]) and ythip_attn_decode
+ * (kv_len = &state[2]) read. Replaces the example's top-20 sampling
+ * (qwen3.cpp:465-486) by argmax, as configs[4] specifies.
+ */
+int ythip_argmax_step(int n, const float* logits, int32_t* token, int32_t* history,
+                      int32_t* state, void* stream);
+
+/*
+ * RoPE tables on the HOST, as RoPECache::precompute builds them
+ * (example/qwen3/src/qwen3.cpp:161-175): cosv/sinv [max_len][dim] (host memory).
+ */
+int ythip_rope_tables(int dim, int max_len, float theta, float* cosv, float* sinv);
 
 #ifdef __cplusplus
 }

@@ -148,3 +148,73 @@ REXPORT void ref_rope(float* x, int B, int H, int L, int D, const float* cosv, c
     qwen3::ops::rope_k(k, c, s);
     std::memcpy(x, k.data(), sizeof(float) * k.size());
 }
+
+// The reference's own Qwen3ForCausalLM (example/qwen3/src/qwen3.cpp), weights
+// filled from the same flat fp32 buffer the oracle takes (layout documented in
+// ytoracle.cpp), driven greedily: forward(prompt, chat_only=true), then
+// forward(token, false) per step, argmax on the returned logits.
+REXPORT int ref_qwen3_generate(const int* cfg_i, const float* cfg_f, const float* W, const int* prompt,
+                               int prompt_len, int n_steps, int* out_tokens, float* out_margins, float* logits0) {
+    qwen3::Qwen3Config cfg;
+    cfg.hidden_size = cfg_i[0];
+    cfg.num_hidden_layers = cfg_i[1];
+    cfg.vocab_size = cfg_i[2];
+    cfg.intermediate_size = cfg_i[3];
+    cfg.num_attention_heads = cfg_i[4];
+    cfg.num_key_value_heads = cfg_i[5];
+    cfg.head_dim = cfg_i[6];
+    cfg.max_position_embeddings = cfg_i[7];
+    cfg.rms_norm_eps = cfg_f[0];
+    cfg.rope_theta = cfg_f[1];
+    auto* lm = new qwen3::Qwen3ForCausalLM();
+    lm->init(cfg);
+    const int H = cfg.hidden_size, V = cfg.vocab_size, I = cfg.intermediate_size, hd = cfg.head_dim;
+    const int nh = cfg.num_attention_heads, nkv = cfg.num_key_value_heads;
+    const float* p = W;
+    auto take2 = [&](int r, int c) {
+        yt::YTensor<float, 2> t(r, c);
+        std::memcpy(t.data(), p, sizeof(float) * static_cast<size_t>(r) * c);
+        p += static_cast<size_t>(r) * c;
+        return t;
+    };
+    auto take1 = [&](int n) {
+        yt::YTensor<float, 1> t(n);
+        std::memcpy(t.data(), p, sizeof(float) * n);
+        p += n;
+        return t;
+    };
+    lm->model.embed = take2(V, H);
+    for (int i = 0; i < cfg.num_hidden_layers; ++i) {
+        auto& L = lm->model.layers[i];
+        L.attn.qkv_proj = take2((nh + 2 * nkv) * hd, H);
+        L.attn.o_proj = take2(H, nh * hd);
+        L.attn.q_norm.weight = take1(hd);
+        L.attn.k_norm.weight = take1(hd);
+        L.mlp.gate_up = take2(2 * I, H);
+        L.mlp.down = take2(H, I);
+        L.norm1.weight = take1(H);
+        L.norm2.weight = take1(H);
+    }
+    lm->model.norm.weight = take1(H);
+    yt::YTensor<int, 2> ids(1, prompt_len);
+    std::memcpy(ids.data(), prompt, sizeof(int) * prompt_len);
+    auto logits = lm->forward(ids, true);
+    for (int step = 0; step < n_steps; ++step) {
+        auto lc = logits.contiguous();
+        const float* lg = lc.data();
+        if (step == 0 && logits0) std::memcpy(logits0, lg, sizeof(float) * V);
+        int best = 0;
+        for (int j = 1; j < V; ++j) if (lg[j] > lg[best]) best = j;
+        float second = -INFINITY;
+        for (int j = 0; j < V; ++j) if (j != best && lg[j] > second) second = lg[j];
+        out_tokens[step] = best;
+        out_margins[step] = lg[best] - second;
+        if (step + 1 < n_steps) {
+            yt::YTensor<int, 2> nid(1, 1);
+            nid.at(0, 0) = best;
+            logits = lm->forward(nid, false);
+        }
+    }
+    delete lm;
+    return 0;
+}

@@ -210,6 +210,7 @@ void gemv_row(const float* A, const float* B, float* C, int n, int k, float alph
         // gemv_row_colmajor_kernel<4> (sgemv.inl:379-425): full groups of 4
         // columns use gemv_dot_ncols<4>; leftover columns use sdot_contiguous.
         const int full = (n / 4) * 4;
+#pragma omp parallel for schedule(static) if (n >= 1024)
         for (int j = 0; j < n; ++j) {
             const float* bcol = B + static_cast<int64_t>(j) * csb;
             float s = (j < full) ? dot_2x8(A, bcol, k) : dot_4x8(A, bcol, k);
@@ -622,4 +623,253 @@ OEXPORT void oracle_set_num_threads(int t) {
 #else
     (void)t;
 #endif
+}
+
+// ===========================================================================
+// Qwen3 decoder (example/qwen3/src/qwen3.cpp:193-516), fp32, batch 1, greedy.
+// Composition of the functions above exactly as the example composes
+// yt::function::linear / rmsNorm_ / scaledDotProductAttention(FLASH_AVX2) /
+// swish_ and the example's rope, KV cache and chat_only last layer.
+//
+// Weight buffer layout (fp32, in the configs' fill order): embed [V,H]; per
+// layer: q [nh*hd,H], k [nkv*hd,H], v [nkv*hd,H] (= the fused qkv_proj,
+// qwen3.cpp:326-338), o [H,nh*hd], q_norm [hd], k_norm [hd], gate [I,H],
+// up [I,H] (= gate_up, 339-349), down [H,I], norm1 [H], norm2 [H]; final norm [H].
+// ===========================================================================
+namespace {
+
+struct Q3Cfg { int H, L, V, I, nh, nkv, hd, max_pos; float eps, theta; };
+
+struct Q3Layer {
+    const float *qkv, *o, *qn, *kn, *gu, *down, *n1, *n2;
+};
+
+struct Q3Cache {  // KVCache (qwen3.cpp:57-126), batch 1
+    std::vector<float> k, v;  // [nkv][max_len][hd]
+    int cur_len = 0, write_pos = 0, total = 0, max_len = 0, nkv = 0, hd = 0;
+    void init(int ml, int kvh, int d) {
+        max_len = ml; nkv = kvh; hd = d;
+        k.assign(static_cast<size_t>(kvh) * ml * d, 0.0f);
+        v.assign(static_cast<size_t>(kvh) * ml * d, 0.0f);
+    }
+    // new_k/new_v: [nkv][l][hd]
+    void append(const float* nk, const float* nv, int l) {
+        for (int t = 0; t < l; ++t) {
+            for (int h = 0; h < nkv; ++h) {
+                std::memcpy(&k[(static_cast<size_t>(h) * max_len + write_pos) * hd], nk + (static_cast<size_t>(h) * l + t) * hd, hd * 4);
+                std::memcpy(&v[(static_cast<size_t>(h) * max_len + write_pos) * hd], nv + (static_cast<size_t>(h) * l + t) * hd, hd * 4);
+            }
+            write_pos = (write_pos + 1) % max_len;
+            total++;
+            if (cur_len < max_len) cur_len++;
+        }
+    }
+    // get_mask (104-126): [q_len, cur_len]
+    std::vector<uint8_t> mask(int q_len) const {
+        const int kv_len = cur_len;
+        std::vector<uint8_t> m(static_cast<size_t>(q_len) * kv_len);
+        const int start = kv_len - q_len;
+        const bool full = cur_len >= max_len;
+        for (int qi = 0; qi < q_len; ++qi)
+            for (int ki = 0; ki < kv_len; ++ki) {
+                bool vis;
+                if (!full) vis = ki <= start + qi;
+                else vis = ((ki - write_pos + max_len) % max_len) <= start + qi;
+                m[static_cast<size_t>(qi) * kv_len + ki] = vis ? 1 : 0;
+            }
+        return m;
+    }
+};
+
+struct Q3Model {
+    Q3Cfg c;
+    const float* embed;
+    const float* fnorm;
+    std::vector<Q3Layer> layers;
+    std::vector<Q3Cache> caches;
+    std::vector<float> cosv, sinv;
+
+    // yt::function::linear: x [l, in] . W[out, in]^T
+    static void linear(const float* x, const float* W, float* y, int l, int in, int out) {
+        sgemm_full(x, W, y, l, out, in, 1.0f, 0.0f, in, 1, 1, in, out, 1);
+    }
+    void rms(float* x, const float* w, int rows, int n) const { oracle_rms_norm(x, w, rows, n, c.eps); }
+
+    // ops::rope / rope_k on [heads][l][hd] with table rows [start, start+l)
+    void rope(float* x, int heads, int l, int start) const {
+        oracle_rope(x, 1, heads, l, c.hd, &cosv[static_cast<size_t>(start) * c.hd], &sinv[static_cast<size_t>(start) * c.hd]);
+    }
+
+    // qkv projection + per-head norms + RoPE, then cache append (the parts of
+    // Qwen3Attention::forward / prefill_kv_only, qwen3.cpp:203-247).
+    void qkv_rope_append(const Q3Layer& W, Q3Cache& cache, const float* h, int l, int start, std::vector<float>* q_out) {
+        const int qs = c.nh * c.hd, ks = c.nkv * c.hd, tot = qs + 2 * ks;
+        std::vector<float> qkv(static_cast<size_t>(l) * tot);
+        linear(h, W.qkv, qkv.data(), l, c.H, tot);
+        std::vector<float> k(static_cast<size_t>(c.nkv) * l * c.hd), v(k.size());
+        for (int t = 0; t < l; ++t)
+            for (int hh = 0; hh < c.nkv; ++hh)
+                for (int d = 0; d < c.hd; ++d) {
+                    k[(static_cast<size_t>(hh) * l + t) * c.hd + d] = qkv[static_cast<size_t>(t) * tot + qs + hh * c.hd + d];
+                    v[(static_cast<size_t>(hh) * l + t) * c.hd + d] = qkv[static_cast<size_t>(t) * tot + qs + ks + hh * c.hd + d];
+                }
+        if (q_out) {
+            q_out->assign(static_cast<size_t>(c.nh) * l * c.hd, 0.0f);
+            for (int t = 0; t < l; ++t)
+                for (int hh = 0; hh < c.nh; ++hh)
+                    std::memcpy(&(*q_out)[(static_cast<size_t>(hh) * l + t) * c.hd], &qkv[static_cast<size_t>(t) * tot + hh * c.hd], c.hd * 4);
+            rms(q_out->data(), W.qn, c.nh * l, c.hd);
+        }
+        rms(k.data(), W.kn, c.nkv * l, c.hd);
+        if (q_out) rope(q_out->data(), c.nh, l, start);
+        rope(k.data(), c.nkv, l, start);
+        cache.append(k.data(), v.data(), l);
+    }
+
+    // Qwen3Attention::forward (224-269): returns o_proj output [l, H]
+    std::vector<float> attention(const Q3Layer& W, Q3Cache& cache, const float* h, int l, int start) {
+        std::vector<float> q;
+        qkv_rope_append(W, cache, h, l, start, &q);
+        const int kv_len = cache.cur_len, G = c.nh / c.nkv;
+        std::vector<uint8_t> m = cache.mask(l);
+        std::vector<float> att(static_cast<size_t>(l) * c.nh * c.hd);
+        const float scale = 1.0f / std::sqrt(static_cast<float>(c.hd));
+#pragma omp parallel for schedule(dynamic, 1)
+        for (int hh = 0; hh < c.nh; ++hh) {
+            const int kh = hh / G;
+            std::vector<float> o(static_cast<size_t>(l) * c.hd);
+            oracle_flash_attention(&q[static_cast<size_t>(hh) * l * c.hd], &cache.k[static_cast<size_t>(kh) * cache.max_len * c.hd],
+                                   &cache.v[static_cast<size_t>(kh) * cache.max_len * c.hd], o.data(), l, kv_len, c.hd, c.hd,
+                                   scale, c.hd, 1, c.hd, 1, c.hd, 1, c.hd, 1, m.data(), kv_len, nullptr, 0, 0);
+            for (int t = 0; t < l; ++t)
+                std::memcpy(&att[(static_cast<size_t>(t) * c.nh + hh) * c.hd], &o[static_cast<size_t>(t) * c.hd], c.hd * 4);
+        }
+        std::vector<float> out(static_cast<size_t>(l) * c.H);
+        linear(att.data(), W.o, out.data(), l, c.nh * c.hd, c.H);
+        return out;
+    }
+
+    // Qwen3MLP::forward (193-200) with swish_ (activation.inl:631-647,
+    // _stableSigmoid ytensor_function.inl:43-52)
+    std::vector<float> mlp(const Q3Layer& W, const float* h, int l) const {
+        std::vector<float> gu(static_cast<size_t>(l) * 2 * c.I);
+        linear(h, W.gu, gu.data(), l, c.H, 2 * c.I);
+        std::vector<float> act(static_cast<size_t>(l) * c.I);
+        for (int t = 0; t < l; ++t)
+            for (int j = 0; j < c.I; ++j) {
+                const float a = gu[static_cast<size_t>(t) * 2 * c.I + j];
+                float sig;
+                if (a >= 0.0f) { const float z = std::exp(-a); sig = 1.0f / (1.0f + z); }
+                else { const float z = std::exp(a); sig = z / (1.0f + z); }
+                act[static_cast<size_t>(t) * c.I + j] = (a * sig) * gu[static_cast<size_t>(t) * 2 * c.I + c.I + j];
+            }
+        std::vector<float> out(static_cast<size_t>(l) * c.H);
+        linear(act.data(), W.down, out.data(), l, c.I, c.H);
+        return out;
+    }
+
+    // Qwen3DecoderLayer::forward (271-283), in place on x [l, H]
+    void layer(int i, std::vector<float>& x, int l, int start) {
+        const Q3Layer& W = layers[i];
+        std::vector<float> h1(x);
+        rms(h1.data(), W.n1, l, c.H);
+        std::vector<float> x2 = attention(W, caches[i], h1.data(), l, start);
+        for (size_t e = 0; e < x2.size(); ++e) x2[e] += x[e];
+        std::vector<float> h2(x2);
+        rms(h2.data(), W.n2, l, c.H);
+        std::vector<float> mo = mlp(W, h2.data(), l);
+        for (size_t e = 0; e < x2.size(); ++e) x2[e] += mo[e];
+        x.swap(x2);
+    }
+
+    // Qwen3Model::forward (365-413) + Qwen3ForCausalLM::forward (449-457): logits of the last token
+    std::vector<float> forward(const int* ids, int l, bool chat_only) {
+        int start = caches[0].cur_len > 0 ? caches[0].total : 0;
+        if (start + l > c.max_pos) {
+            start = caches[0].cur_len;
+            if (start + l > c.max_pos) start = 0;
+        }
+        std::vector<float> x(static_cast<size_t>(l) * c.H);
+        for (int t = 0; t < l; ++t) std::memcpy(&x[static_cast<size_t>(t) * c.H], embed + static_cast<size_t>(ids[t]) * c.H, c.H * 4);
+        std::vector<float> last(c.H);
+        bool done = false;
+        for (int i = 0; i < c.L; ++i) {
+            if (chat_only && l > 1 && i == c.L - 1) {
+                const Q3Layer& W = layers[i];
+                std::vector<float> h1(x);
+                rms(h1.data(), W.n1, l, c.H);
+                qkv_rope_append(W, caches[i], h1.data(), l - 1, start, nullptr);  // prefill_kv_only
+                std::vector<float> x2 = attention(W, caches[i], &h1[static_cast<size_t>(l - 1) * c.H], 1, start + l - 1);
+                for (int e = 0; e < c.H; ++e) x2[e] += x[static_cast<size_t>(l - 1) * c.H + e];
+                std::vector<float> h2(x2);
+                rms(h2.data(), W.n2, 1, c.H);
+                std::vector<float> mo = mlp(W, h2.data(), 1);
+                for (int e = 0; e < c.H; ++e) x2[e] += mo[e];
+                rms(x2.data(), fnorm, 1, c.H);
+                last = x2;
+                done = true;
+                break;
+            }
+            layer(i, x, l, start);
+        }
+        if (!done) {
+            rms(x.data(), fnorm, l, c.H);
+            std::memcpy(last.data(), &x[static_cast<size_t>(l - 1) * c.H], c.H * 4);
+        }
+        // last.matmul(embed^T): a 1 x V GEMV with B = embed^T (col-major view)
+        std::vector<float> logits(c.V);
+        sgemm_full(last.data(), embed, logits.data(), 1, c.V, c.H, 1.0f, 0.0f, c.H, 1, 1, c.H, c.V, 1);
+        return logits;
+    }
+};
+
+}  // namespace
+
+// cfg_i: H, L, V, I, nh, nkv, hd, max_pos ; cfg_f: eps, theta
+// Greedy generation: prompt forward with chat_only = true, then n_steps - 1
+// single-token steps (Qwen3ForCausalLM::generate, 506-516, with argmax in
+// place of the example's top-20 sampling). out_tokens[n_steps]; margins =
+// top1 - top2 logit per step; logits0 (optional [V]) = first step's logits.
+OEXPORT int oracle_qwen3_generate(const int* cfg_i, const float* cfg_f, const float* W, const int* prompt,
+                                  int prompt_len, int n_steps, int* out_tokens, float* out_margins,
+                                  float* logits0) {
+    Q3Model m;
+    m.c = {cfg_i[0], cfg_i[1], cfg_i[2], cfg_i[3], cfg_i[4], cfg_i[5], cfg_i[6], cfg_i[7], cfg_f[0], cfg_f[1]};
+    const Q3Cfg& c = m.c;
+    if (prompt_len <= 0 || prompt_len + n_steps > c.max_pos) return -1;
+    const float* p = W;
+    m.embed = p;
+    p += static_cast<size_t>(c.V) * c.H;
+    const size_t qkv_rows = static_cast<size_t>(c.nh + 2 * c.nkv) * c.hd;
+    for (int i = 0; i < c.L; ++i) {
+        Q3Layer L{};
+        L.qkv = p; p += qkv_rows * c.H;
+        L.o = p; p += static_cast<size_t>(c.H) * c.nh * c.hd;
+        L.qn = p; p += c.hd;
+        L.kn = p; p += c.hd;
+        L.gu = p; p += static_cast<size_t>(2) * c.I * c.H;
+        L.down = p; p += static_cast<size_t>(c.H) * c.I;
+        L.n1 = p; p += c.H;
+        L.n2 = p; p += c.H;
+        m.layers.push_back(L);
+    }
+    m.fnorm = p;
+    m.caches.resize(c.L);
+    for (auto& ch : m.caches) ch.init(c.max_pos, c.nkv, c.hd);
+    m.cosv.resize(static_cast<size_t>(c.max_pos) * c.hd);
+    m.sinv.resize(m.cosv.size());
+    oracle_rope_precompute(c.hd, c.max_pos, c.theta, m.cosv.data(), m.sinv.data());
+    std::vector<int> ids(prompt, prompt + prompt_len);
+    for (int step = 0; step < n_steps; ++step) {
+        std::vector<float> lg = m.forward(ids.data(), static_cast<int>(ids.size()), step == 0);
+        if (step == 0 && logits0) std::memcpy(logits0, lg.data(), sizeof(float) * c.V);
+        int best = 0;
+        for (int j = 1; j < c.V; ++j) if (lg[j] > lg[best]) best = j;
+        float second = -std::numeric_limits<float>::infinity();
+        for (int j = 0; j < c.V; ++j) if (j != best && lg[j] > second) second = lg[j];
+        out_tokens[step] = best;
+        out_margins[step] = lg[best] - second;
+        ids.assign(1, best);
+    }
+    return 0;
 }

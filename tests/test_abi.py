@@ -47,5 +47,5 @@ def test_abi_version_and_argument_errors():
     # m == 0: a no-op that succeeds (src/kernel/avx2/sgemm.inl:594)
     assert lib.ythip_gemm(0, 0, 1, 0, 2, 2, None, 0, 2, 1, None, 0, 2, 1, None, 0, 2, 1, 1.0, 0.0, None) == 0
     st = lib.ythip_rmsnorm_rope(2, 1, 1, 1, 1, 96, None, 0, None, None, 1e-6, None, None, 0, 0,
-                                None, None, None, None, None, None, 0, None)
+                                None, None, None, None, None, None, 0, None, None)
     assert st == -2  # head dim 96 unsupported

@@ -42,6 +42,7 @@ struct NormRopeArgs {
     int64_t qs0, qs1, qs2, ks0, ks1, ks2, vs0, vs1, vs2;
     int B, S, Hq, Hkv;
     int cache_pos;
+    const int32_t* dev_pos;  // when set: pos0 = cache_pos = *dev_pos (graph-replayable decode)
 };
 
 // One wave per (token, head) with d = 2 * HALF; HALF <= 64 (d <= 128).
@@ -57,6 +58,8 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
     const int s = tok % a.S;
     const int b = tok / a.S;
     constexpr int D = 2 * HALF;
+    const int pos0 = a.dev_pos ? a.dev_pos[0] : a.pos0;
+    const int cache_pos = a.dev_pos ? a.dev_pos[0] : a.cache_pos;
     const bool active = lane < HALF;
 
     const auto* src = static_cast<const typename T::raw*>(a.qkv) + tok * a.ld_qkv + (int64_t)h * D;
@@ -74,11 +77,11 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
         w = a.wq;
     } else if (h < a.Hq + a.Hkv) {
         dst = a.k;
-        off = b * a.ks0 + (h - a.Hq) * a.ks1 + (int64_t)(a.cache_pos + s) * a.ks2;
+        off = b * a.ks0 + (h - a.Hq) * a.ks1 + (int64_t)(cache_pos + s) * a.ks2;
         w = a.wk;
     } else {
         dst = a.v;
-        off = b * a.vs0 + (h - a.Hq - a.Hkv) * a.vs1 + (int64_t)(a.cache_pos + s) * a.vs2;
+        off = b * a.vs0 + (h - a.Hq - a.Hkv) * a.vs1 + (int64_t)(cache_pos + s) * a.vs2;
         if (dst != nullptr && active) {
             store_from_f32<T>(dst, off + lane, x1);
             store_from_f32<T>(dst, off + lane + HALF, x2);
@@ -95,7 +98,7 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
         }
     }
     if (a.cos_tab != nullptr && active) {
-        const int64_t t = (int64_t)(a.pos0 + s) * a.ld_tab;
+        const int64_t t = (int64_t)(pos0 + s) * a.ld_tab;
         const float c = a.cos_tab[t + lane], sn = a.sin_tab[t + lane];
         const float y1 = fmaf(x1, c, -(x2 * sn));
         const float y2 = fmaf(x2, c, x1 * sn);
@@ -109,12 +112,12 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
 }
 
 // Row RMSNorm for wide rows (hidden size): one 256-thread block per row.
-template <class T>
+template <class T, class TO>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const void* x, int64_t ldx, const float* w, float eps,
                                                        void* y, int64_t ldy, int n) {
     const int64_t row = blockIdx.x;
     const auto* xr = static_cast<const typename T::raw*>(x) + row * ldx;
-    auto* yr = static_cast<typename T::raw*>(y) + row * ldy;
+    auto* yr = static_cast<typename TO::raw*>(y) + row * ldy;
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += 256) {
         const float v = load_as_f32<T>(xr, i);
@@ -126,7 +129,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void* x, int64_t ld
     __syncthreads();
     const float tot = (part[0] + part[1]) + (part[2] + part[3]);
     const float den = sqrtf(tot / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += 256) store_from_f32<T>(yr, i, (load_as_f32<T>(xr, i) / den) * w[i]);
+    for (int i = threadIdx.x; i < n; i += 256) store_from_f32<TO>(yr, i, (load_as_f32<T>(xr, i) / den) * w[i]);
 }
 
 namespace {
@@ -143,10 +146,10 @@ hipError_t launch_norm_rope(const NormRopeArgs& a, int d, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <class T>
+template <class T, class TO>
 hipError_t launch_rms(int rows, int n, const void* x, int64_t ldx, const float* w, float eps, void* y, int64_t ldy,
                       hipStream_t s) {
-    rms_norm_kernel<T><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
+    rms_norm_kernel<T, TO><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
     return hipGetLastError();
 }
 
@@ -162,7 +165,7 @@ __attribute__((visibility("default"))) int ythip_rmsnorm_rope(
     int dtype, int B, int S, int Hq, int Hkv, int d, const void* qkv, int64_t ld_qkv, const float* wq,
     const float* wk, float eps, const float* cos_tab, const float* sin_tab, int64_t ld_tab, int pos0, void* Qout,
     const int64_t q_str[3], void* Kout, const int64_t k_str[3], void* Vout, const int64_t v_str[3], int cache_pos,
-    void* stream) {
+    const int32_t* dev_pos, void* stream) {
     if (B < 0 || S < 0 || Hq < 0 || Hkv < 0) return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: negative size");
     if (d != 64 && d != 128) return fail(YTHIP_EUNSUPPORTED, "ythip_rmsnorm_rope: head dim %d (supported: 64, 128)", d);
     if ((int64_t)B * S * (Hq + 2 * Hkv) == 0) return 0;
@@ -180,7 +183,7 @@ __attribute__((visibility("default"))) int ythip_rmsnorm_rope(
     a.qs0 = q_str[0]; a.qs1 = q_str[1]; a.qs2 = q_str[2];
     if (k_str) { a.ks0 = k_str[0]; a.ks1 = k_str[1]; a.ks2 = k_str[2]; }
     if (v_str) { a.vs0 = v_str[0]; a.vs1 = v_str[1]; a.vs2 = v_str[2]; }
-    a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.cache_pos = cache_pos;
+    a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.cache_pos = cache_pos; a.dev_pos = dev_pos;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (dtype) {
         case YTHIP_F32: return status_of(launch_norm_rope<F32>(a, d, s));
@@ -190,20 +193,25 @@ __attribute__((visibility("default"))) int ythip_rmsnorm_rope(
     }
 }
 
-__attribute__((visibility("default"))) int ythip_rms_norm(int dtype, int rows, int n, const void* x, int64_t ld_x,
-                                                          const float* w, float eps, void* y, int64_t ld_y,
-                                                          void* stream) {
+__attribute__((visibility("default"))) int ythip_rms_norm(int dtype_in, int dtype_out, int rows, int n,
+                                                          const void* x, int64_t ld_x, const float* w, float eps,
+                                                          void* y, int64_t ld_y, void* stream) {
     if (rows < 0 || n < 0) return fail(YTHIP_EINVAL, "ythip_rms_norm: negative size");
     if (rows == 0 || n == 0) return 0;
     if (x == nullptr || y == nullptr || w == nullptr) return fail(YTHIP_EINVAL, "ythip_rms_norm: NULL pointer");
     if (ld_x < n || ld_y < n) return fail(YTHIP_EINVAL, "ythip_rms_norm: leading dimension smaller than n");
+    if (x == y && dtype_in != dtype_out) return fail(YTHIP_EINVAL, "ythip_rms_norm: in place needs one dtype");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    switch (dtype) {
-        case YTHIP_F32: return status_of(launch_rms<F32>(rows, n, x, ld_x, w, eps, y, ld_y, s));
-        case YTHIP_F16: return status_of(launch_rms<F16>(rows, n, x, ld_x, w, eps, y, ld_y, s));
-        case YTHIP_BF16: return status_of(launch_rms<BF16>(rows, n, x, ld_x, w, eps, y, ld_y, s));
-        default: return fail(YTHIP_EINVAL, "ythip_rms_norm: invalid dtype %d", dtype);
-    }
+#define YTHIP_RMS(TI, TOUT) return status_of(launch_rms<TI, TOUT>(rows, n, x, ld_x, w, eps, y, ld_y, s))
+    if (dtype_in == YTHIP_F32 && dtype_out == YTHIP_F32) YTHIP_RMS(F32, F32);
+    if (dtype_in == YTHIP_F32 && dtype_out == YTHIP_BF16) YTHIP_RMS(F32, BF16);
+    if (dtype_in == YTHIP_F32 && dtype_out == YTHIP_F16) YTHIP_RMS(F32, F16);
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_BF16) YTHIP_RMS(BF16, BF16);
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_F32) YTHIP_RMS(BF16, F32);
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F16) YTHIP_RMS(F16, F16);
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F32) YTHIP_RMS(F16, F32);
+#undef YTHIP_RMS
+    return fail(YTHIP_EINVAL, "ythip_rms_norm: invalid dtype pair %d/%d", dtype_in, dtype_out);
 }
 
 }  // extern "C"

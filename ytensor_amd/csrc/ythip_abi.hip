@@ -4,6 +4,7 @@
 // L3/L4 checks (src/function/ops.inl:123-128, 382-387; src/ytensor_math.inl:290-292)
 // but as status codes plus a thread-local message instead of exceptions.
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 
@@ -55,6 +56,25 @@ __attribute__((visibility("default"))) int ythip_gemm(int dtype_in, int dtype_ou
         return fail(YTHIP_EINVAL, "ythip_gemm: A or B is NULL");
     return gemm_dispatch(dtype_in, dtype_out, batch, m, n, k, A, sa_b, rsa, csa, B, sb_b, rsb, csb, C, sc_b, rsc,
                          csc, alpha, beta, static_cast<hipStream_t>(stream));
+}
+
+// Host-side RoPE tables, computed as RoPECache::precompute does
+// (example/qwen3/src/qwen3.cpp:161-175): float freq = 1/powf(theta, 2i/dim),
+// angle = t*freq, cos/sin duplicated into both halves. HOST pointers,
+// cosv/sinv [max_len][dim].
+__attribute__((visibility("default"))) int ythip_rope_tables(int dim, int max_len, float theta, float* cosv,
+                                                             float* sinv) {
+    if (dim <= 0 || (dim & 1) || max_len < 0 || !cosv || !sinv)
+        return fail(YTHIP_EINVAL, "ythip_rope_tables: bad arguments");
+    const int half = dim / 2;
+    for (int t = 0; t < max_len; ++t)
+        for (int i = 0; i < half; ++i) {
+            const float freq = 1.0f / std::pow(theta, 2.0f * i / dim);
+            const float angle = t * freq;
+            cosv[(size_t)t * dim + i] = cosv[(size_t)t * dim + i + half] = std::cos(angle);
+            sinv[(size_t)t * dim + i] = sinv[(size_t)t * dim + i + half] = std::sin(angle);
+        }
+    return 0;
 }
 
 }  // extern "C"

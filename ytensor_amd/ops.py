@@ -214,7 +214,8 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
              out: torch.Tensor | None = None) -> torch.Tensor:
-    """yt::function::rmsNorm over the last axis; weight float32 [n]."""
+    """yt::function::rmsNorm over the last axis; weight float32 [n]; `out` may
+    have another dtype than x (e.g. fp32 residual in, bf16 out)."""
     _dev(x, weight)
     n = x.shape[-1]
     x2 = x.reshape(-1, n)
@@ -224,7 +225,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
         out = torch.empty_like(x)
     o2 = out.reshape(-1, n)
     w = weight.to(torch.float32).contiguous()
-    st = _lib.lib().ythip_rms_norm(_code(x), x2.shape[0], n, x2.data_ptr(), x2.stride(0), w.data_ptr(),
+    st = _lib.lib().ythip_rms_norm(_code(x), _code(out), x2.shape[0], n, x2.data_ptr(), x2.stride(0), w.data_ptr(),
                                    float(eps), o2.data_ptr(), o2.stride(0), _stream())
     check(st, "ythip_rms_norm")
     return out
@@ -233,7 +234,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
 def rms_norm_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torch.Tensor | None, wk: torch.Tensor | None,
                   eps: float, cos: torch.Tensor | None, sin: torch.Tensor | None, pos0: int = 0,
                   q_out: torch.Tensor | None = None, k_out: torch.Tensor | None = None,
-                  v_out: torch.Tensor | None = None, cache_pos: int = 0):
+                  v_out: torch.Tensor | None = None, cache_pos: int = 0, dev_pos: torch.Tensor | None = None):
     """Fused per-head RMSNorm + RoPE on qkv [B, S, (Hq+2*Hkv)*d].
 
     Returns (q [B,Hq,S,d], k, v) where k/v are written to rows
@@ -254,12 +255,12 @@ def rms_norm_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torch.Tensor
     if v_out is None:
         v_out = torch.empty((B, Hkv, S, d), dtype=dt, device=dev)
     for name, t, h in (("q_out", q_out, Hq), ("k_out", k_out, Hkv), ("v_out", v_out, Hkv)):
-        rows_needed = S if name == "q_out" else cache_pos + S
+        rows_needed = S if (name == "q_out" or dev_pos is not None) else cache_pos + S
         if t.dim() != 4 or t.shape[0] != B or t.shape[1] != h or t.shape[3] != d or t.shape[2] < rows_needed:
             raise ValueError(f"{name} has shape {tuple(t.shape)}; needs [{B}, {h}, >={rows_needed}, {d}]")
         if t.stride(3) != 1 or t.dtype != dt:
             raise ValueError(f"{name} must have a contiguous last dim and dtype {dt}")
-    if cos is not None and (cos.shape[0] < pos0 + S or cos.shape[1] < d):
+    if cos is not None and dev_pos is None and (cos.shape[0] < pos0 + S or cos.shape[1] < d):
         raise ValueError(f"RoPE tables {tuple(cos.shape)} too small for positions {pos0}..{pos0 + S - 1}")
     keep = []
 
@@ -279,9 +280,44 @@ def rms_norm_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torch.Tensor
         q_out.data_ptr(), i64array(q_out.stride()[:3]),
         k_out.data_ptr(), i64array(k_out.stride()[:3]),
         v_out.data_ptr(), i64array(v_out.stride()[:3]),
-        int(cache_pos), _stream())
+        int(cache_pos), None if dev_pos is None else dev_pos.data_ptr(), _stream())
     check(st, "ythip_rmsnorm_rope")
     return q_out, k_out, v_out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """SwiGLU on a fused [rows, 2n] gate_up projection -> [rows, n]."""
+    _dev(gate_up)
+    g2 = gate_up.reshape(-1, gate_up.shape[-1])
+    n = g2.shape[1] // 2
+    if out is None:
+        out = torch.empty((*gate_up.shape[:-1], n), dtype=gate_up.dtype, device=gate_up.device)
+    o2 = out.reshape(-1, n)
+    check(_lib.lib().ythip_silu_mul(_code(gate_up), _code(out), g2.shape[0], n, g2.data_ptr(), g2.stride(0),
+                                    o2.data_ptr(), o2.stride(0), _stream()), "ythip_silu_mul")
+    return out
+
+
+def embedding(table: torch.Tensor, ids: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[r] = table[ids[r]] with ids an int32 device tensor."""
+    _dev(table, ids, out)
+    if ids.dtype != torch.int32:
+        raise ValueError("ids must be int32")
+    check(_lib.lib().ythip_embedding(_code(table), _code(out), ids.numel(), table.shape[1], table.data_ptr(),
+                                     ids.data_ptr(), out.data_ptr(), out.stride(0), _stream()), "ythip_embedding")
+    return out
+
+
+def argmax_step(logits: torch.Tensor, token: torch.Tensor, history: torch.Tensor | None = None,
+                state: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy token (first max index) into token[0]; optionally history/state updates."""
+    _dev(logits, token)
+    if logits.dtype != torch.float32:
+        raise ValueError("logits must be float32")
+    check(_lib.lib().ythip_argmax_step(logits.numel(), logits.data_ptr(), token.data_ptr(),
+                                       None if history is None else history.data_ptr(),
+                                       None if state is None else state.data_ptr(), _stream()), "ythip_argmax_step")
+    return token
 
 
 def default_scale(d: int) -> float:

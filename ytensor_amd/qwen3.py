@@ -1,0 +1,218 @@
+"""Device-resident Qwen3 decoder on libythip.so (the caller of the hot path).
+
+Mirrors the reference's Qwen3 example (example/qwen3/src/qwen3.cpp:193-516):
+per layer RMSNorm -> fused qkv projection -> per-head q/k RMSNorm + RoPE with
+the K/V append into the cache -> GQA causal attention -> o projection +
+residual -> RMSNorm -> fused gate_up -> SwiGLU -> down projection + residual,
+then the final norm and the tied LM head, greedy selection.
+
+MI355X layout and execution:
+  * weights bf16 in HBM (qkv and gate_up fused as in the example's load(),
+    qwen3.cpp:326-349), norms fp32, embedding bf16 and reused as the LM head;
+  * residual stream fp32; GEMM inputs bf16; the o/down projections write
+    fp32 straight into the residual with beta = 1 (residual add fused into
+    the GEMM epilogue); logits fp32;
+  * KV cache bf16 [layers][1, kv_heads, ctx, head_dim];
+  * a decode step is ~10 launches per layer with no host-side value that
+    changes between steps (token id and positions live in device memory), so
+    it is captured once as a HIP graph and replayed per token.
+Every arithmetic operation runs in libythip.so; torch only allocates device
+memory and provides the stream / graph capture.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib, ops
+
+
+class Qwen3Config:
+    """Qwen3Config defaults (example/qwen3/include/qwen3.hpp:46-60)."""
+
+    def __init__(self, hidden=1024, layers=28, vocab=151936, inter=3072, n_heads=16, n_kv=8, head_dim=128,
+                 max_pos=4096, eps=1e-6, theta=1e6):
+        self.hidden, self.layers, self.vocab, self.inter = hidden, layers, vocab, inter
+        self.n_heads, self.n_kv, self.head_dim, self.max_pos = n_heads, n_kv, head_dim, max_pos
+        self.eps, self.theta = eps, theta
+
+
+def weight_layout(cfg) -> list[tuple[str, tuple[int, ...]]]:
+    """(name, shape) of the flat weight buffer: embed, then per layer q, k, v,
+    o, q_norm, k_norm, gate, up, down, norm1, norm2, then the final norm."""
+    H, I, hd = cfg.hidden, cfg.inter, cfg.head_dim
+    out = [("embed", (cfg.vocab, H))]
+    for i in range(cfg.layers):
+        out += [(f"{i}.q", (cfg.n_heads * hd, H)), (f"{i}.k", (cfg.n_kv * hd, H)), (f"{i}.v", (cfg.n_kv * hd, H)),
+                (f"{i}.o", (H, cfg.n_heads * hd)), (f"{i}.q_norm", (hd,)), (f"{i}.k_norm", (hd,)),
+                (f"{i}.gate", (I, H)), (f"{i}.up", (I, H)), (f"{i}.down", (H, I)),
+                (f"{i}.norm1", (H,)), (f"{i}.norm2", (H,))]
+    out.append(("norm", (H,)))
+    return out
+
+
+def rope_tables(dim: int, max_len: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
+    """RoPECache::precompute tables built by libythip on the host."""
+    c = np.empty((max_len, dim), np.float32)
+    s = np.empty((max_len, dim), np.float32)
+    _lib.check(_lib.lib().ythip_rope_tables(dim, max_len, float(theta), c.ctypes.data, s.ctypes.data),
+               "ythip_rope_tables")
+    return c, s
+
+
+class Qwen3:
+    """Greedy batch-1 generation on one GPU."""
+
+    def __init__(self, cfg: Qwen3Config, weights, device="cuda", max_ctx: int | None = None,
+                 max_prompt: int = 512):
+        self.cfg = cfg
+        self.dev = torch.device(device)
+        self.max_ctx = min(cfg.max_pos, max_ctx or cfg.max_pos)
+        self.max_prompt = max_prompt
+        self._upload(weights)
+        self._alloc()
+        self.graph = None
+
+    # ---------------------------------------------------------------- weights
+    def _upload(self, weights) -> None:
+        """weights: flat fp32 array (numpy or torch) in weight_layout order, or a
+        dict name -> tensor. Matrices become bf16, norms stay fp32."""
+        cfg, dev = self.cfg, self.dev
+        lay = weight_layout(cfg)
+        if isinstance(weights, dict):
+            get = lambda name, shp: torch.as_tensor(weights[name]).reshape(shp)
+        else:
+            flat = torch.as_tensor(weights)
+            offs = {}
+            o = 0
+            for name, shp in lay:
+                n = int(np.prod(shp))
+                offs[name] = (o, n)
+                o += n
+            if flat.numel() != o:
+                raise ValueError(f"weight buffer has {flat.numel()} values, the layout needs {o}")
+            get = lambda name, shp: flat[offs[name][0]:offs[name][0] + offs[name][1]].reshape(shp)
+        bf = lambda t: t.to(device=dev, dtype=torch.bfloat16).contiguous()
+        f32 = lambda t: t.to(device=dev, dtype=torch.float32).contiguous()
+        self.embed = bf(get("embed", (cfg.vocab, cfg.hidden)))
+        self.layers = []
+        for i in range(cfg.layers):
+            shp = dict(lay)
+            qkv = torch.cat([get(f"{i}.q", shp[f"{i}.q"]), get(f"{i}.k", shp[f"{i}.k"]),
+                             get(f"{i}.v", shp[f"{i}.v"])], 0)
+            gu = torch.cat([get(f"{i}.gate", shp[f"{i}.gate"]), get(f"{i}.up", shp[f"{i}.up"])], 0)
+            self.layers.append(dict(
+                qkv=bf(qkv), o=bf(get(f"{i}.o", shp[f"{i}.o"])), gu=bf(gu), down=bf(get(f"{i}.down", shp[f"{i}.down"])),
+                qn=f32(get(f"{i}.q_norm", shp[f"{i}.q_norm"])), kn=f32(get(f"{i}.k_norm", shp[f"{i}.k_norm"])),
+                n1=f32(get(f"{i}.norm1", shp[f"{i}.norm1"])), n2=f32(get(f"{i}.norm2", shp[f"{i}.norm2"]))))
+        self.fnorm = f32(get("norm", (cfg.hidden,)))
+        c, s = rope_tables(cfg.head_dim, cfg.max_pos, cfg.theta)
+        self.cos = torch.from_numpy(c).to(dev)
+        self.sin = torch.from_numpy(s).to(dev)
+
+    def _alloc(self) -> None:
+        cfg, dev, P = self.cfg, self.dev, self.max_prompt
+        H, nh, nkv, hd, I = cfg.hidden, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
+        bf, f32 = torch.bfloat16, torch.float32
+        self.x = torch.empty((P, H), dtype=f32, device=dev)
+        self.h = torch.empty((P, H), dtype=bf, device=dev)
+        self.qkv = torch.empty((P, (nh + 2 * nkv) * hd), dtype=bf, device=dev)
+        self.q = torch.empty((1, nh, P, hd), dtype=bf, device=dev)
+        self.attn = torch.empty((P, nh * hd), dtype=bf, device=dev)
+        self.gu = torch.empty((P, 2 * I), dtype=bf, device=dev)
+        self.act = torch.empty((P, I), dtype=bf, device=dev)
+        self.kc = torch.zeros((cfg.layers, 1, nkv, self.max_ctx, hd), dtype=bf, device=dev)
+        self.vc = torch.zeros_like(self.kc)
+        self.hf = torch.empty((1, H), dtype=bf, device=dev)
+        self.logits = torch.empty((1, cfg.vocab), dtype=f32, device=dev)
+        self.ids = torch.zeros((P,), dtype=torch.int32, device=dev)
+        self.token = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.history = torch.zeros((self.max_ctx,), dtype=torch.int32, device=dev)
+        self.state = torch.zeros((3,), dtype=torch.int32, device=dev)  # generated, position, kv_len
+        self.ws = torch.empty((ops.decode_workspace_bytes(1, nh, self.max_ctx, hd),), dtype=torch.uint8, device=dev)
+        self.qd = torch.empty((1, nh, 1, hd), dtype=bf, device=dev)  # decode query
+
+    # ------------------------------------------------------------------ steps
+    def _attn_view(self, S: int) -> torch.Tensor:
+        """[1, nh, S, hd] view whose memory is attn[S, nh*hd] (no permute copy)."""
+        nh, hd = self.cfg.n_heads, self.cfg.head_dim
+        return self.attn[:S].view(S, nh, hd).permute(1, 0, 2).unsqueeze(0)
+
+    def _layer(self, i: int, S: int, pos0: int, decode: bool) -> None:
+        cfg, L = self.cfg, self.layers[i]
+        nh, nkv, hd = cfg.n_heads, cfg.n_kv, cfg.head_dim
+        x, h = self.x[:S], self.h[:S]
+        ops.rms_norm(x, L["n1"], cfg.eps, out=h)
+        ops.gemm(h, L["qkv"].t(), self.qkv[:S])
+        kc, vc = self.kc[i], self.vc[i]
+        if decode:
+            qv = self.qd
+            ops.rms_norm_rope(self.qkv[:S].view(1, S, -1), nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
+                              q_out=qv, k_out=kc, v_out=vc, dev_pos=self.state[1:2])
+            ops.decode_attention(qv.view(1, nh, hd), kc, vc, kv_len=self.state[2:3],
+                                 out=self.attn[:1].view(1, nh, hd), workspace=self.ws)
+        else:
+            qv = self.q[:, :, :S, :]
+            ops.rms_norm_rope(self.qkv[:S].view(1, S, -1), nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
+                              pos0=pos0, q_out=qv, k_out=kc, v_out=vc, cache_pos=pos0)
+            ops.scaled_dot_product_attention(qv, kc[:, :, :pos0 + S], vc[:, :, :pos0 + S], 0.0, mask="causal",
+                                             out=self._attn_view(S))
+        ops.gemm(self.attn[:S], L["o"].t(), x, beta=1.0)          # x += attn . Wo^T
+        ops.rms_norm(x, L["n2"], cfg.eps, out=h)
+        ops.gemm(h, L["gu"].t(), self.gu[:S])
+        ops.silu_mul(self.gu[:S], out=self.act[:S])
+        ops.gemm(self.act[:S], L["down"].t(), x, beta=1.0)        # x += act . Wdown^T
+
+    def _head(self, S: int) -> None:
+        ops.rms_norm(self.x[S - 1:S], self.fnorm, self.cfg.eps, out=self.hf)
+        ops.gemm(self.hf, self.embed.t(), self.logits)             # tied LM head, fp32 logits
+        ops.argmax_step(self.logits, self.token, self.history, self.state)
+
+    def prefill(self, prompt) -> None:
+        """Run the prompt; the first generated token lands in history[0]."""
+        P = len(prompt)
+        if P > self.max_prompt or P >= self.max_ctx:
+            raise ValueError(f"prompt of {P} tokens exceeds max_prompt={self.max_prompt} / max_ctx={self.max_ctx}")
+        self.ids[:P].copy_(torch.as_tensor(np.asarray(prompt, dtype=np.int32)))
+        # state after the head's argmax: generated = 1, position = P, kv_len = P + 1
+        self.state.copy_(torch.tensor([0, P - 1, P], dtype=torch.int32))
+        ops.embedding(self.embed, self.ids[:P], self.x[:P])
+        for i in range(self.cfg.layers):
+            self._layer(i, P, 0, decode=False)
+        self._head(P)
+        self.prompt_len = P
+
+    def _decode_step(self) -> None:
+        ops.embedding(self.embed, self.token, self.x[:1])
+        for i in range(self.cfg.layers):
+            self._layer(i, 1, 0, decode=True)
+        self._head(1)
+
+    def capture(self) -> None:
+        """Capture one decode step as a HIP graph (replayed per token)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                self._decode_step()
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = g
+
+    def generate(self, prompt, n_tokens: int, use_graph: bool = True) -> np.ndarray:
+        """Greedy: prompt forward, then n_tokens - 1 decode steps. Returns the tokens."""
+        self.prefill(prompt)
+        if len(prompt) + n_tokens > self.max_ctx:
+            raise ValueError("max_ctx too small for prompt + generated tokens")
+        if use_graph and self.graph is None:
+            # capturing does not execute the step; state is untouched
+            self.capture()
+        for _ in range(n_tokens - 1):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self._decode_step()
+        torch.cuda.synchronize()
+        return self.history[:n_tokens].cpu().numpy()
