@@ -13,6 +13,7 @@ the kernels are launched on):
   attn_prefill    configs[2] causal flash prefill S = 512/2048/8192 (TFLOP/s)
   attn_decode     configs[3] decode attention (GB/s of K/V read)
   rmsnorm_rope    fused RMSNorm+RoPE on configs[2] shapes at S=8192 (GB/s)
+  qwen3_0p6b      configs[4] shape: 512-token prefill + greedy decode tok/s
   roofline        the headline kernel against MI355X dense bf16 MFMA peak
   cpu_baseline    YTensor's own CPU sgemm (compiled reference when present,
                   else the oracle restatement) on the host cores, same shape
@@ -47,7 +48,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no sweep, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list of sections to run (gemm,sweep,fp32,prefill,decode,norm)")
+    ap.add_argument("--only", default="", help="comma list of sections to run "
+                                               "(gemm,sweep,fp32,prefill,decode,norm,qwen3)")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain conversion-copy kernel of known size (HBM counter calibration)")
     return ap.parse_args()
@@ -144,6 +146,54 @@ def cpu_baseline(M: int, N: int, K: int, budget_s: float = 20.0) -> dict:
             "sample": f"full {M}x{N}x{K} fp32 sgemm on bf16-rounded inputs, median of {len(times)} run(s), "
                       f"{t:.2f} s each, single thread (reference default g_num_threads=0)",
             "host": host_info()}
+
+
+def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256) -> dict:
+    """configs[4] shape: random-init Qwen3-0.6B (synthetic N(0, 0.02) weights,
+    bf16 matrices, fp32 norms), 512-token prompt, then greedy decode with each
+    step replayed from one captured HIP graph. tok/s counts the decode steps."""
+    import numpy as np
+    from ytensor_amd.qwen3 import Qwen3, Qwen3Config, weight_layout
+    cfg = Qwen3Config()
+    total = sum(int(np.prod(s)) for _, s in weight_layout(cfg))
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    W = torch.randn(total, device=dev, generator=g) * 0.02
+    m = Qwen3(cfg, W, max_ctx=prompt_len + n_tokens + 64, max_prompt=prompt_len)
+    del W
+    torch.cuda.empty_cache()
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, cfg.vocab, prompt_len).astype(np.int32)
+    m.prefill(prompt)  # warm-up (kernels, allocator)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    m.prefill(prompt)
+    e.record()
+    torch.cuda.synchronize()
+    prefill_ms = s.elapsed_time(e)
+    m.capture()
+    steps = n_tokens - 1
+    s.record()
+    for _ in range(steps):
+        m.graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    dec_ms = s.elapsed_time(e)
+    toks = m.history[:n_tokens].cpu().numpy()
+    per_tok_ms = dec_ms / steps
+    # HBM bytes per decode token: every bf16 weight matrix once (tied LM head
+    # included) + the K/V rows attended (mean context over the run).
+    w_bytes = 2.0 * sum(int(np.prod(s)) for n, s in weight_layout(cfg) if "norm" not in n)
+    mean_ctx = prompt_len + n_tokens / 2.0
+    kv_bytes = cfg.layers * 2 * cfg.n_kv * cfg.head_dim * 2 * mean_ctx
+    gbs = (w_bytes + kv_bytes) / (per_tok_ms * 1e-3) / 1e9
+    return {"decode_tok_s": round(1e3 / per_tok_ms, 1), "ms_per_token": round(per_tok_ms, 4),
+            "prefill_ms_512": round(prefill_ms, 3), "prefill_tok_s": round(prompt_len / prefill_ms * 1e3, 1),
+            "bytes_per_token": w_bytes + kv_bytes, "hbm_gbs": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "tokens_generated": int(n_tokens),
+            "distinct_tokens": int(len(set(toks.tolist()))),
+            "note": "batch 1, greedy, decode step = one HIP graph replay of ~290 kernels"}
 
 
 def main() -> int:
@@ -289,6 +339,9 @@ def main() -> int:
                           args.steps, args.warmup, torch)
         sections["rmsnorm_rope_bf16_S8192"] = {"ms": round(t, 5), "gbs": round(byts / t / 1e6, 1),
                                                "frac_hbm": round(byts / t / 1e6 / PEAK_HBM_GBS, 4)}
+
+    if want("qwen3") and not args.quick:
+        sections["qwen3_0p6b_decode"] = bench_qwen3(torch, dev)
 
     # ---- the timed headline region: exactly K steps, synchronised both sides ----
     for _ in range(args.warmup):
