@@ -49,3 +49,21 @@ def test_abi_version_and_argument_errors():
     st = lib.ythip_rmsnorm_rope(2, 1, 1, 1, 1, 96, None, 0, None, None, 1e-6, None, None, 0, 0,
                                 None, None, None, None, None, None, 0, None, None)
     assert st == -2  # head dim 96 unsupported
+
+
+def test_cpp_mirror_compiles_and_reports_errors(tmp_path):
+    """include/ythip.hpp (yt::kernel::hip) builds with the host C++ compiler
+    against libythip.so and maps argument errors to exceptions."""
+    import shutil
+    import subprocess
+    from ytensor_amd import _lib
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path / "abi_errors"
+    lib_dir = os.path.dirname(_lib.LIB_PATH)
+    subprocess.check_call([gxx, "-std=c++17", "-O1", os.path.join(ROOT, "tests", "cpp", "abi_errors.cpp"),
+                           "-o", str(exe), f"-L{lib_dir}", "-lythip", f"-Wl,-rpath,{lib_dir}"])
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "ok:" in out.stdout
