@@ -261,6 +261,13 @@ def main() -> int:
     B = (torch.randn(K, N, device=dev) * 0.02).to(torch.bfloat16)
     C = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     flops = 2.0 * M * N * K
+    # An idle MI355X needs a few hundred milliseconds of load before its clocks
+    # settle; without this the first section would be timed on a cold GPU.
+    t_end = time.perf_counter() + 0.5
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            ops.gemm(A, B, C)
+        torch.cuda.synchronize()
     ms = time_launches(lambda: ops.gemm(A, B, C), args.steps, args.warmup, torch)
     tflops = flops / (ms * 1e-3) / 1e12
     traffic = read_traffic(TRAFFIC_FILE)

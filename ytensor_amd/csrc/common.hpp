@@ -115,6 +115,23 @@ __device__ __forceinline__ void dma16(const void* gsrc, void* lds_wave_base) {
 #endif
 }
 
+// The same DMA issued through inline asm. The compiler does not model an asm
+// DMA, so it keeps using partial lgkmcnt waits for the ds_reads that follow
+// (with the builtin it falls back to lgkmcnt(0) after every read, which
+// serialises the LDS fragment loads with the MFMAs). Callers order the DMA with
+// explicit vmcnt waits and barriers.
+__device__ __forceinline__ void dma16_async(const void* gsrc, void* lds_wave_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t l = (uint32_t)(uintptr_t)lds_wave_base;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gsrc), "s"(__builtin_amdgcn_readfirstlane(l))
+                 : "memory", "m0");
+#else
+    (void)gsrc; (void)lds_wave_base;
+#endif
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane j supplies the LDS byte
 // address of 4 consecutive 16-bit values R[j][0..3]; lane i receives
 // { R[4t + i/4][i%4] : t = 0..3 }.
@@ -128,6 +145,15 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* lds, int byte_off) {
     (void)lds; (void)byte_off;
     return u32x2{0u, 0u};
 #endif
+}
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i in [B, E).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
 }
 
 // Elements per 16-byte chunk.

@@ -4,22 +4,27 @@
 //
 // Design (MI355X-first, not a translation of the CPU Goto loop):
 //  * Block tile BM x BN, k step of 128 bytes per row (64 bf16/fp16 or 32 fp32).
-//    Both operands are staged in LDS K-contiguous, [rows][8 chunks of 16 B],
-//    so every MFMA operand is one ds_read_b128 per lane.
-//  * LDS chunk swizzle: chunk c of row r lives at c ^ ((r ^ (r >> 3)) & 7).
-//    16 consecutive rows reading the same logical chunk hit 8 distinct 16-byte
-//    slots per 8-lane group, and the NN transposing writes (rows 4 apart) also
-//    spread over all 8 slots.
-//  * Two LDS stages; the next k step is fetched into registers while the
-//    current one runs on the matrix cores; one barrier per k step.
-//  * A row-major B ("NN", B[k][n]) is transposed in registers on its way to
-//    LDS (8 k-rows x 4 columns per thread, v_perm-style half-word shuffles), so
-//    the compute loop is the same for NN and NT ("linear": B = W^T).
+//    Both operands live in LDS K-contiguous, [rows][8 chunks of 16 B], so an
+//    MFMA operand fragment is one ds_read_b128 per lane. A row-major B ("NN",
+//    B[k][n]) stays [k][n] in LDS and its fragments are read with the gfx950
+//    transposing read ds_read_b64_tr_b16, so nothing is transposed in registers.
+//  * Tiles move global -> LDS by direct-to-LDS DMA (global_load_lds_dwordx4):
+//    no VGPR staging. Two stages for the 256 x 256 tile (one k step in flight),
+//    a 4-deep ring for the smaller tiles. The bytes each CU can pull through its
+//    vector-memory path (~28 B/clk) are close to what 256 x 256 MFMA work
+//    consumes, so the 256 x 256 tile is the only one that keeps up at 4096^3.
+//  * LDS swizzles were chosen by measuring gfx950's LDS read rate per pattern
+//    (see swz_dma / nn_blk): fragment reads are bank-conflict free.
+//  * Inside a k step the A fragments stream through a 3-register ring read two
+//    MFMA groups ahead, pinned by schedule barriers, so LDS latency overlaps
+//    the matrix cores.
 //  * MFMA operands are swapped (src0 = B rows, src1 = A rows): each lane then
 //    holds 4 consecutive output columns of one row, stored as one vector.
 //  * Tiles are assigned XCD-aware: the hardware places workgroup w on XCD
 //    w % 8; each XCD receives a contiguous, M-grouped range of tiles so its
 //    32 CUs share A and B panels in their own L2.
+//  * The register-staged kernel (gemm_mfma_kernel) serves layouts the DMA path
+//    cannot take (k not a multiple of the k step, 4-byte-aligned NN rows).
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -39,6 +44,18 @@ struct GemmArgs {
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
+
+// Swizzles of the DMA-staged kernel, chosen by measuring gfx950's LDS read rate
+// per access pattern (64 banks; ds_read_b128 and ds_read_b64_tr_b16):
+//  * K-major tiles [row][8 x 16 B]: chunk c of row r at c ^ ((r >> 1) & 7). Rows
+//    r and r+1 share one 256-byte bank window and take the same XOR, so a
+//    fragment read (16 rows, one logical chunk) covers all 64 banks without
+//    conflict; the previous row-XOR swizzle ran at ~60% of that rate.
+//  * NN B tiles [k][n] in 32-byte column blocks: block b of k-row r at
+//    b ^ h(r), h(r) = (r ^ ((r >> 3) << 2)) & mask, so the transposing reads of
+//    k-rows r and r + 8 (served together) land in different blocks.
+__device__ __forceinline__ int swz_dma(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int nn_blk(int row, int blk, int mask) { return blk ^ ((row ^ ((row >> 3) << 2)) & mask); }
 
 __device__ __forceinline__ void tile_coords(int w, int tiles_m, int tiles_n, int& tm, int& tn) {
     const int T = tiles_m * tiles_n;
@@ -327,9 +344,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
         for (int i = 0; i < A_PT; ++i) {
             const int slot = i * THREADS + wave * 64 + lane;
             const int r = slot >> 3;
-            const int c = swz(r, slot & 7);  // the swizzle is an involution on the chunk index
+            const int c = swz_dma(r, slot & 7);  // the swizzle is an involution on the chunk index
             const int row = min(m0 + r, a.m - 1);
-            dma16(Ap + (int64_t)row * a.rsa + k0 + c * VEC, &sA[i * THREADS + wave * 64]);
+            dma16_async(Ap + (int64_t)row * a.rsa + k0 + c * VEC, &sA[i * THREADS + wave * 64]);
         }
 #pragma unroll
         for (int i = 0; i < B_PT; ++i) {
@@ -337,15 +354,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
             const raw* g;
             if constexpr (!NN) {
                 const int r = slot >> 3;
-                const int c = swz(r, slot & 7);
+                const int c = swz_dma(r, slot & 7);
                 const int row = min(n0 + r, a.n - 1);
                 g = Bp + (int64_t)row * a.csb + k0 + c * VEC;
             } else {
                 const int r = slot / (2 * NBLK), ps = slot % (2 * NBLK);
-                const int lb = (ps >> 1) ^ (r & BLK_MASK);
+                const int lb = nn_blk(r, ps >> 1, BLK_MASK);
                 g = Bp + (int64_t)(k0 + r) * a.rsb + min(n0 + lb * 16, a.n - 16) + (ps & 1) * 8;
             }
-            dma16(g, &sB[i * THREADS + wave * 64]);
+            dma16_async(g, &sB[i * THREADS + wave * 64]);
         }
     };
 
@@ -355,49 +372,59 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](const u32x4* sA, const u32x4* sB) {
-        u32x4 fa[2][FM], fb[2][FN];
-        auto ld = [&](int ks, int buf) {
-            const int chunk = ks * 4 + lgrp;
+    // Fragment reads. A fragment (16 rows x one 16-byte chunk) is one ds_read_b128;
+    // a B fragment is one ds_read_b128 (NT) or two transposing reads (NN).
+    auto ldA = [&](const u32x4* sA, int ks, int i) -> u32x4 {
+        const int r = wm * WTM + i * 16 + lrow;
+        return sA[r * 8 + swz_dma(r, ks * 4 + lgrp)];
+    };
+    auto ldB = [&](const u32x4* sB, int ks, int j) -> u32x4 {
+        if constexpr (!NN) {
+            const int r = wn * WTN + j * 16 + lrow;
+            return sB[r * 8 + swz_dma(r, ks * 4 + lgrp)];
+        } else {
+            const int nb = (wn * WTN + j * 16) >> 4;
+            u32x4 v;
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int r = wm * WTM + i * 16 + lrow;
-                fa[buf][i] = sA[r * 8 + swz(r, chunk)];
+            for (int h = 0; h < 2; ++h) {
+                const int r = ks * 32 + 8 * lgrp + 4 * h + (lrow >> 2);
+                const int byte = r * (BN * 2) + (nn_blk(r, nb, BLK_MASK) << 5) + 8 * (lrow & 3);
+                const u32x2 w = lds_read_tr16(sB, byte);
+                v[2 * h] = w[0];
+                v[2 * h + 1] = w[1];
             }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                if constexpr (!NN) {
-                    const int r = wn * WTN + j * 16 + lrow;
-                    fb[buf][j] = sB[r * 8 + swz(r, chunk)];
-                } else {
-                    const int nb = (wn * WTN + j * 16) >> 4;
-                    u32x4 v;
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const int r = ks * 32 + 8 * lgrp + 4 * h + (lrow >> 2);
-                        const int byte = r * (BN * 2) + ((nb ^ (r & BLK_MASK)) << 5) + 8 * (lrow & 3);
-                        const u32x2 w = lds_read_tr16(sB, byte);
-                        v[2 * h] = w[0];
-                        v[2 * h + 1] = w[1];
-                    }
-                    fb[buf][j] = v;
-                }
-            }
-        };
-        ld(0, 0);
-        ld(1, 1);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j) acc[i][j] = mfma_chunk(T{}, fb[ks][j], fa[ks][i], acc[i][j]);
-#pragma unroll
-            for (int q = 0; q < FM * FN / 2; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF_PER_CHUNK, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                 // LDS read
-            }
+            return v;
         }
+    };
+    // One k step = 2 x 32 k = 2*FM A fragments (t = ks*FM + i). A fragments stream
+    // through a ring of 3 registers, read two steps ahead; the B fragments of the
+    // second half are read right after the first step. The schedule barriers pin
+    // the order (reads for t+2, then the FN MFMAs of t), so every wait before an
+    // MFMA is a partial lgkmcnt and the reads overlap the matrix work.
+    constexpr int BR = NN ? 2 : 1;
+    constexpr int NTS = 2 * FM;
+    static_assert(FM >= 2, "the A ring needs at least 4 fragments per k step");
+    auto compute = [&](const u32x4* sA, const u32x4* sB) {
+        u32x4 fb[2][FN], fa[3];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[0][j] = ldB(sB, 0, j);
+        fa[0] = ldA(sA, 0, 0);
+        fa[1] = ldA(sA, 1 / FM, 1 % FM);
+        __builtin_amdgcn_sched_group_barrier(0x100, FN * BR + 2, 0);
+        static_for<0, NTS>([&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            constexpr int ks = t / FM, i = t % FM;
+            constexpr int nrd = (t + 2 < NTS ? 1 : 0) + (t == 1 ? FN * BR : 0);
+            if constexpr (t + 2 < NTS) fa[(t + 2) % 3] = ldA(sA, (t + 2) / FM, (t + 2) % FM);
+            if constexpr (t == 1) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[1][j] = ldB(sB, 1, j);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = mfma_chunk(T{}, fb[ks][j], fa[t % 3], acc[i][j]);
+            if constexpr (nrd > 0) __builtin_amdgcn_sched_group_barrier(0x100, nrd, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, FN * MF_PER_CHUNK, 0);
+        });
     };
 
     u32x4* sA = sbuf;
@@ -666,8 +693,13 @@ hipError_t launch_dma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
     auto tiles = [&](int bm, int bn) {
         return (int64_t)((a.m + bm - 1) / bm) * ((a.n + bn - 1) / bn) * batch;
     };
-    if (tiles(256, 256) >= 160) return launch_dma_tile<T, TO, 256, 256, 2, 4, 2>(a, nn, batch, s);
-    if (tiles(128, 128) >= 96) return launch_dma_tile<T, TO, 128, 128, 2, 2, 4>(a, nn, batch, s);
+    // Chosen from a sweep of M x N x K shapes on MI355X (bf16): the 256 x 256 tile
+    // once it has most of the 256 CUs busy, 128 x 128 (two workgroups per CU) for
+    // mid sizes, 64 x 64 below that; the 64 x 64 ring pays off only while its
+    // grid is short of several workgroups per CU.
+    if (tiles(256, 256) >= 192) return launch_dma_tile<T, TO, 256, 256, 2, 4, 2>(a, nn, batch, s);
+    if (tiles(128, 128) >= 384) return launch_dma_tile<T, TO, 128, 128, 2, 2, 2>(a, nn, batch, s);
+    if (tiles(64, 64) >= 768) return launch_dma_tile<T, TO, 64, 64, 2, 2, 2>(a, nn, batch, s);
     return launch_dma_tile<T, TO, 64, 64, 2, 2, 4>(a, nn, batch, s);
 }
 
