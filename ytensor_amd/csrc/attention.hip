@@ -57,8 +57,8 @@ struct AttnArgs {
 // queries per wave), so each K/V tile is staged once for GH*128 queries.
 // K and V tiles reach LDS by DMA (global_load_lds, 16 bytes per lane), both
 // kept in their natural [key][d] layout:
-//   K rows: 16-byte chunk c stored at c ^ (key & 7) -> the S^T operand is one
-//           conflict-free ds_read_b128 per lane.
+//   K rows: 16-byte chunk c stored at c ^ (key & KMASK) -> the S^T operand is
+//           one conflict-free ds_read_b128 per lane.
 //   V rows: 32-byte block b stored at b ^ (key & BMASK) and read transposed by
 //           ds_read_b64_tr_b16: lane j of a 16-lane group addresses 4 d-values
 //           of key (kt*16 + 4*grp + j/4); lane i receives d = i of 4 keys,
@@ -80,7 +80,10 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     constexpr int NB = D / 16;    // 32-byte blocks per V row
     constexpr int BMASK = (NB < 8 ? NB : 8) - 1;
     constexpr int STG = BKV * KCH;  // u32x4 slots per tile
-
+    // K chunk swizzle: with D = 128 a K row is one full 256-byte bank window, so
+    // 16 consecutive keys XOR their chunk index with key & 15 and a fragment read
+    // (16 keys, one logical chunk) touches all 64 banks once.
+    constexpr int KMASK = KCH - 1 < 15 ? KCH - 1 : 15;
     __shared__ u32x4 sK[2 * STG];
     __shared__ u32x4 sV[2 * STG];
 
@@ -124,138 +127,172 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     const int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;
     const float c = a.scale_log2;
 
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};  // m in raw score units
+    // m is the reference point of the exponentials (raw score units). It moves
+    // only when a block's max exceeds it by more than 2^8 in probability, so the
+    // O rescale is rare; p = 2^((s - m) c) <= 2^8 stays far from any overflow and
+    // the final O / l is independent of m.
+    constexpr float LAZY = 8.0f;
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
     f32x4 o[2][DT];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto issue = [&](int kb, int st) {
-        const int k0 = kb * BKV;
+    // Per-thread DMA offsets (elements) within a block; the block base moves by BKV keys.
+    int koff[PT], voff[PT];  // the host guarantees 64 rows of K and V span < 2^31 elements
+    int krow[PT];
 #pragma unroll
-        for (int i = 0; i < PT; ++i) {
-            const int slot = i * THREADS + wave * 64 + lane;
-            const int row = slot / KCH, ps = slot % KCH;
-            const int64_t key = min(k0 + row, a.Skv - 1);
-            const int kc = ps ^ (row & 7);
-            dma16(Kp + key * a.ks2 + kc * 8, &sK[st * STG + i * THREADS + wave * 64]);
-            const int vb = (ps >> 1) ^ (row & BMASK);
-            dma16(Vp + key * a.vs2 + vb * 16 + (ps & 1) * 8, &sV[st * STG + i * THREADS + wave * 64]);
+    for (int i = 0; i < PT; ++i) {
+        const int slot = i * THREADS + wave * 64 + lane;
+        const int row = slot / KCH, ps = slot % KCH;
+        krow[i] = row;
+        koff[i] = row * (int)a.ks2 + (ps ^ (row & KMASK)) * 8;
+        voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
+    }
+    auto issue = [&](int kb) {
+        const int k0 = kb * BKV;
+        u32x4* dK = sK + (kb & 1) * STG;
+        u32x4* dV = sV + (kb & 1) * STG;
+        const raw* kbase = Kp + (int64_t)k0 * a.ks2;
+        const raw* vbase = Vp + (int64_t)k0 * a.vs2;
+        if (k0 + BKV <= a.Skv) {
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                dma16_async(kbase + koff[i], &dK[i * THREADS + wave * 64]);
+                dma16_async(vbase + voff[i], &dV[i * THREADS + wave * 64]);
+            }
+        } else {
+            // tail block: rows past the end re-read the last key (never used)
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const int sh = min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
+                dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * THREADS + wave * 64]);
+                dma16_async(vbase + voff[i] + sh * (int)a.vs2, &dV[i * THREADS + wave * 64]);
+            }
         }
     };
 
-    if (nkb > 0) issue(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int cur = kb & 1;
-        if (kb + 1 < nkb) issue(kb + 1, cur ^ 1);
-        const u32x4* cK = sK + cur * STG;
-        const u32x4* cV = sV + cur * STG;
-        const int k0 = kb * BKV;
-        // Wave-uniform: does this block hold any key visible to this wave's queries?
-        const bool active = (MODE != 1) || (k0 <= q0 + WQ - 1 + off);
-        if (active) {
-            f32x4 s[2][4];
+    f32x4 s[2][4];
+    // S^T = K . Q^T for block kb (K stage kb & 1).
+    auto qk = [&](int kb) {
+        const u32x4* cK = sK + (kb & 1) * STG;
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt) {
-                    const int key = kt * 16 + l16;
-                    const u32x4 kf = cK[key * KCH + ((ks * 4 + g) ^ (key & 7))];
+            for (int kt = 0; kt < 4; ++kt) {
+                const int key = kt * 16 + l16;
+                const u32x4 kf = cK[key * KCH + ((ks * 4 + g) ^ (key & KMASK))];
 #pragma unroll
-                    for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma_chunk(T{}, kf, qf[qt][ks], s[qt][kt]);
-                }
+                for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma_chunk(T{}, kf, qf[qt][ks], s[qt][kt]);
             }
-            const bool need_mask = (MODE == 2) || (k0 + BKV > a.Skv) ||
-                                   (MODE == 1 && k0 + BKV - 1 > q0 + off);
-            u32x4 pk[2][2];
-            bool rescale = false;
-            float alpha[2];
+        }
+    };
+    // Online softmax of block kb and O += V^T P^T (V stage kb & 1).
+    auto softmax_pv = [&](int kb) {
+        const int k0 = kb * BKV;
+        const bool need_mask = (MODE == 2) || (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off);
+        u32x4 pk[2][2];
+        bool rescale = false;
+        float alpha[2];
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                const int qa = q0 + qt * 16 + l16;
-                float v[4][4];
-                if (need_mask) {
-#pragma unroll
-                    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            float x = s[qt][kt][r];
-                            const int key = k0 + kt * 16 + g * 4 + r;
-                            bool vis = key < a.Skv;
-                            if (MODE == 1) vis = vis && (key <= qa + off);
-                            if (MODE == 2 && vis && qa < a.Sq) {
-                                if (a.mask != nullptr) vis = a.mask[(int64_t)qa * a.mask_ld + key] != 0;
-                                // bias is added after scaling: fold it into raw units
-                                if (vis && a.bias != nullptr)
-                                    x += a.bias[(int64_t)qa * a.brs + (int64_t)key * a.bcs] * LOG2E / c;
-                            }
-                            v[kt][r] = vis ? x : -INFINITY;
-                        }
-                } else {
-#pragma unroll
-                    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) v[kt][r] = s[qt][kt][r];
-                }
-                float mx = -INFINITY;
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
-                    mx = fmaxf(mx, fmaxf(fmaxf(v[kt][0], v[kt][1]), fmaxf(v[kt][2], v[kt][3])));
-                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const float m_new = fmaxf(m[qt], mx);
-                const float mc = (m_new == -INFINITY) ? 0.f : m_new * c;
-                alpha[qt] = __builtin_amdgcn_exp2f(m[qt] * c - mc);
-                rescale |= (m_new != m[qt]);
-                float sum = 0.f;
+        for (int qt = 0; qt < 2; ++qt) {
+            const int qa = q0 + qt * 16 + l16;
+            float v[4][4];
+            if (need_mask) {
 #pragma unroll
                 for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        v[kt][r] = __builtin_amdgcn_exp2f(fmaf(v[kt][r], c, -mc));
-                        sum += v[kt][r];
+                        float x = s[qt][kt][r];
+                        const int key = k0 + kt * 16 + g * 4 + r;
+                        bool vis = key < a.Skv;
+                        if (MODE == 1) vis = vis && (key <= qa + off);
+                        if (MODE == 2 && vis && qa < a.Sq) {
+                            if (a.mask != nullptr) vis = a.mask[(int64_t)qa * a.mask_ld + key] != 0;
+                            // bias is added after scaling: fold it into raw units
+                            if (vis && a.bias != nullptr)
+                                x += a.bias[(int64_t)qa * a.brs + (int64_t)key * a.bcs] * LOG2E / c;
+                        }
+                        v[kt][r] = vis ? x : -INFINITY;
                     }
-                l[qt] = fmaf(l[qt], alpha[qt], sum);
-                m[qt] = m_new;
+            } else {
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    pk[qt][kk] = u32x4{pack2<T>(v[2 * kk][0], v[2 * kk][1]), pack2<T>(v[2 * kk][2], v[2 * kk][3]),
-                                       pack2<T>(v[2 * kk + 1][0], v[2 * kk + 1][1]),
-                                       pack2<T>(v[2 * kk + 1][2], v[2 * kk + 1][3])};
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[kt][r] = s[qt][kt][r];
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+                mx = fmaxf(mx, fmaxf(fmaxf(v[kt][0], v[kt][1]), fmaxf(v[kt][2], v[kt][3])));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            // move the reference point only when the block max is far above it
+            const bool move = (m[qt] == -INFINITY) ? (mx != -INFINITY) : ((mx - m[qt]) * c > LAZY);
+            const float m_new = move ? mx : m[qt];
+            const float mc = (m_new == -INFINITY) ? 0.f : m_new * c;
+            alpha[qt] = move ? __builtin_amdgcn_exp2f(m[qt] * c - mc) : 1.0f;
+            rescale |= move;
+            float sum = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    v[kt][r] = __builtin_amdgcn_exp2f(fmaf(v[kt][r], c, -mc));
+                    sum += v[kt][r];
                 }
-            }
-            // O *= alpha only when some lane's running max moved in this block.
-            if (__ballot(rescale) != 0) {
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-                    for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha[qt];
-            }
+            l[qt] = fmaf(l[qt], alpha[qt], sum);
+            m[qt] = m_new;
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    u32x4 vf;
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const int key = (2 * kk + hh) * 16 + g * 4 + (l16 >> 2);
-                        const int byte = key * (D * 2) + ((dt ^ (key & BMASK)) << 5) + 8 * (l16 & 3);
-                        const u32x2 w2 = lds_read_tr16(cV, byte);
-                        vf[2 * hh] = w2[0];
-                        vf[2 * hh + 1] = w2[1];
-                    }
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt) o[qt][dt] = mfma_chunk(T{}, vf, pk[qt][kk], o[qt][dt]);
-                }
+                pk[qt][kk] = u32x4{pack2<T>(v[2 * kk][0], v[2 * kk][1]), pack2<T>(v[2 * kk][2], v[2 * kk][3]),
+                                   pack2<T>(v[2 * kk + 1][0], v[2 * kk + 1][1]),
+                                   pack2<T>(v[2 * kk + 1][2], v[2 * kk + 1][3])};
             }
+        }
+        // O *= alpha only when some lane's reference point moved in this block.
+        if (__ballot(rescale) != 0) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha[qt];
+        }
+        const u32x4* cV = sV + (kb & 1) * STG;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                u32x4 vf;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int key = (2 * kk + hh) * 16 + g * 4 + (l16 >> 2);
+                    const int byte = key * (D * 2) + ((dt ^ (key & BMASK)) << 5) + 8 * (l16 & 3);
+                    const u32x2 w2 = lds_read_tr16(cV, byte);
+                    vf[2 * hh] = w2[0];
+                    vf[2 * hh + 1] = w2[1];
+                }
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) o[qt][dt] = mfma_chunk(T{}, vf, pk[qt][kk], o[qt][dt]);
+            }
+        }
+    };
+    // Wave-uniform: does block kb hold any key visible to this wave's queries?
+    auto active = [&](int kb) { return (MODE != 1) || (kb * BKV <= q0 + WQ - 1 + off); };
+
+    if (nkb > 0) issue(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        if (kb + 1 < nkb) issue(kb + 1);
+        if (active(kb)) {
+            qk(kb);
+            softmax_pv(kb);
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -396,8 +433,9 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
             const raw* kp = Kb + (int64_t)kk * a.ks2;
             const raw* vp = Vb + (int64_t)kk * a.ks2;
             if constexpr (sizeof(raw) == 2) {
-                const u32x4 kw = *reinterpret_cast<const u32x4*>(kp);
-                const u32x4 vw = *reinterpret_cast<const u32x4*>(vp);
+                // streamed once: non-temporal loads (measured ~10% more HBM read rate)
+                const u32x4 kw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp));
+                const u32x4 vw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp));
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     kx[u][2 * e] = lo_as_f32(T{}, kw[e]);
@@ -554,7 +592,8 @@ int prefill_typed(AttnArgs a, hipStream_t s) {
                          al(a.Q, 16) && al(a.K, 16) && al(a.V, 16) && al(a.O, 8) &&
                          a.qs0 % 8 == 0 && a.qs1 % 8 == 0 && a.qs2 % 8 == 0 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
                          a.ks2 % 8 == 0 && a.vs0 % 8 == 0 && a.vs1 % 8 == 0 && a.vs2 % 8 == 0 &&
-                         a.os0 % 4 == 0 && a.os1 % 4 == 0 && a.os2 % 4 == 0;
+                         a.os0 % 4 == 0 && a.os1 % 4 == 0 && a.os2 % 4 == 0 &&
+                         a.ks2 < (1 << 24) && a.vs2 < (1 << 24) && a.ks2 >= 0 && a.vs2 >= 0;
     if (mfma_ok) {
         if constexpr (es == 2) {
             if (a.D == 128) return status_of(launch_prefill_mfma<T, 128>(a, mode, s));

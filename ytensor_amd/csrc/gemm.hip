@@ -535,7 +535,9 @@ __global__ __launch_bounds__(64 * SKINNY_WAVES) void gemm_skinny_nt_kernel(GemmA
         for (int u = 0; u < UNR; ++u) {
             const int k = (s + u) * KSTEP + g * VEC;
             const bool ok = (s + u < s_end) && k < a.k;
-            fb[u] = (ok && brow) ? *reinterpret_cast<const u32x4*>(brp + (int64_t)(s + u) * KSTEP) : u32x4{0, 0, 0, 0};
+            // the weight stream is read once: non-temporal loads
+            fb[u] = (ok && brow) ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(brp + (int64_t)(s + u) * KSTEP))
+                                 : u32x4{0, 0, 0, 0};
             fa[u] = (ok && arow) ? *reinterpret_cast<const u32x4*>(arp + (int64_t)(s + u) * KSTEP) : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
