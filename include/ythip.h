@@ -169,6 +169,37 @@ int ythip_argmax_step(int n, const float* logits, int32_t* token, int32_t* histo
                       int32_t* state, void* stream);
 
 /*
+ * Decode-time linear with a fused operand prologue, for M <= 16 rows:
+ *   C[m, n] = alpha * A'[m, k] . W[n, k]^T + beta * C
+ * (W row-major [n][k] with row stride ldw -- the weight of `linear`,
+ * src/function/ops.inl:84-91, which the reference runs as gemv_row_simd for
+ * one row, src/kernel/avx2/sgemv.inl:443-717). dtype_in is W's type.
+ *   prologue 0: A' = A (dtype_in, [m][k], row stride lda);
+ *   prologue 1: A' = bf16/fp16-rounded rmsNorm_(A, norm_w, eps) of fp32 rows A
+ *               (src/function/normalization.inl:256-277; the pre-attention,
+ *               pre-MLP and final norms of qwen3.cpp:271-283, 365-413), with the
+ *               same arithmetic as ythip_rms_norm, so bits match the unfused pair;
+ *   prologue 2: A' = rounded swish(gate) * up of dtype_in rows A = [gate | up]
+ *               ([m][2k], qwen3.cpp:193-200), arithmetic of ythip_silu_mul.
+ * argmax_parts (optional, fp32 device buffer of 2 * ceil(n / 16) values): one
+ * (max, index-as-bits) pair of row 0 per 16-column tile, lowest index on ties,
+ * for ythip_argmax_finish. Requires 16-byte aligned A/W rows and k a multiple
+ * of 8 (16-bit) or 4 (fp32); prologues 1 and 2 need 16-bit W.
+ */
+int ythip_gemv_fused(int prologue, int dtype_in, int dtype_out, int m, int n, int k,
+                     const void* A, int64_t lda, const float* norm_w, float eps,
+                     const void* W, int64_t ldw, void* C, int64_t ldc, float alpha,
+                     float beta, float* argmax_parts, void* stream);
+
+/*
+ * Greedy selection from ythip_gemv_fused's per-tile pairs (n_parts tiles):
+ * same result, tie rule and state update as ythip_argmax_step over the full
+ * logits (qwen3.cpp:465-486, argmax as configs[4] specifies).
+ */
+int ythip_argmax_finish(const float* parts, int n_parts, int32_t* token, int32_t* history,
+                        int32_t* state, void* stream);
+
+/*
  * RoPE tables on the HOST, as RoPECache::precompute builds them
  * (example/qwen3/src/qwen3.cpp:161-175): cosv/sinv [max_len][dim] (host memory).
  */

@@ -7,10 +7,12 @@ use and fails loudly when it has not been built: there is no CPU fallback.
 """
 from ._lib import YthipError, lib, LIB_PATH  # noqa: F401
 from .ops import (  # noqa: F401
+    argmax_finish,
     argmax_step,
     decode_attention,
     embedding,
     gemm,
+    gemv_fused,
     linear,
     matmul,
     rms_norm,
@@ -29,4 +31,5 @@ def load():
 __all__ = [
     "YthipError", "lib", "gemm", "matmul", "linear", "scaled_dot_product_attention",
     "decode_attention", "rms_norm", "rms_norm_rope", "silu_mul", "embedding", "argmax_step",
+    "gemv_fused", "argmax_finish",
 ]

@@ -36,6 +36,8 @@ SIGNATURES = {
     "ythip_silu_mul": (_I, [_I, _I, _I, _I, _P, _L, _P, _L, _P]),
     "ythip_embedding": (_I, [_I, _I, _I, _I, _P, _P, _P, _L, _P]),
     "ythip_argmax_step": (_I, [_I, _P, _P, _P, _P, _P]),
+    "ythip_gemv_fused": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _F, _P, _L, _P, _L, _F, _F, _P, _P]),
+    "ythip_argmax_finish": (_I, [_P, _I, _P, _P, _P, _P]),
     "ythip_rope_tables": (_I, [_I, _I, _F, _P, _P]),
 }
 

@@ -147,6 +147,13 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* lds, int byte_off) {
 #endif
 }
 
+// Butterfly sum over the 64 lanes of a wave (every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
 // Compile-time loop: f(std::integral_constant<int, i>) for i in [B, E).
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F&& f) {

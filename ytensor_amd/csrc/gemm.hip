@@ -496,73 +496,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 // ---------------------------------------------------------------------------
 // Skinny GEMM, M <= 16 (the decode GEMVs: x [1..16, K] . W^T). HBM-bound on
 // the weight stream, so the design goal is bytes in flight, not MFMA reuse.
-//   NT: one workgroup per 16 output columns; its 8 waves split K; each lane
-//   streams 16-byte chunks of W rows, UNR chunks in flight, into a
-//   v_mfma_f32_16x16x32 with the (zero-padded) M rows of A; the 8 partial
-//   16x16 tiles are summed through LDS. The MFMA is used as a 16-lane dot-
-//   product reducer here, its flops are free against the byte stream.
+//   NT (W^T, the `linear` layout): gemv_kernel in gemv.hip.
 //   NN (B [K][N] row-major): VALU; lane = one output column, coalesced 2-byte
 //   row loads, 8 waves split K, LDS reduction.
 // ---------------------------------------------------------------------------
 constexpr int SKINNY_M = 16;
 constexpr int SKINNY_WAVES = 8;
-
-template <class T, class TO>
-__global__ __launch_bounds__(64 * SKINNY_WAVES) void gemm_skinny_nt_kernel(GemmArgs a) {
-    using raw = typename T::raw;
-    constexpr int VEC = 16 / sizeof(raw);
-    constexpr int KSTEP = 4 * VEC;  // k covered by one MFMA chunk across the 4 lane groups
-    constexpr int UNR = 4;
-    constexpr int MF_PER_CHUNK = sizeof(raw) == 2 ? 1 : 4;
-    (void)MF_PER_CHUNK;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
-    const int bz = blockIdx.y;
-    const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
-    const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b;
-    const int nsteps = (a.k + KSTEP - 1) / KSTEP;
-    const int per_wave = (nsteps + SKINNY_WAVES - 1) / SKINNY_WAVES;
-    const int s_begin = wave * per_wave, s_end = min(nsteps, s_begin + per_wave);
-    const bool arow = r < a.m, brow = n0 + r < a.n;
-    const raw* arp = Ap + (int64_t)(arow ? r : 0) * a.rsa + g * VEC;
-    const raw* brp = Bp + (int64_t)(brow ? n0 + r : 0) * a.csb + g * VEC;
-
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = s_begin; s < s_end; s += UNR) {
-        u32x4 fb[UNR], fa[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int k = (s + u) * KSTEP + g * VEC;
-            const bool ok = (s + u < s_end) && k < a.k;
-            // the weight stream is read once: non-temporal loads
-            fb[u] = (ok && brow) ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(brp + (int64_t)(s + u) * KSTEP))
-                                 : u32x4{0, 0, 0, 0};
-            fa[u] = (ok && arow) ? *reinterpret_cast<const u32x4*>(arp + (int64_t)(s + u) * KSTEP) : u32x4{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) acc = mfma_chunk(T{}, fb[u], fa[u], acc);
-    }
-    // acc: lane holds C[m = r][n0 + 4g + j]; sum the 8 waves' tiles.
-    __shared__ f32x4 red[SKINNY_WAVES][64];
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave != 0) return;
-    f32x4 t = red[0][lane];
-#pragma unroll
-    for (int w = 1; w < SKINNY_WAVES; ++w) t += red[w][lane];
-    if (r >= a.m) return;
-    using oraw = typename TO::raw;
-    oraw* crow = static_cast<oraw*>(a.C) + bz * a.sc_b + (int64_t)r * a.rsc;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + 4 * g + j;
-        if (n >= a.n) continue;
-        float v = a.alpha * t[j];
-        if (a.beta != 0.0f) v += a.beta * load_as_f32<TO>(crow, n);
-        store_from_f32<TO>(crow, n, v);
-    }
-}
 
 template <class T, class TO>
 __global__ __launch_bounds__(64 * SKINNY_WAVES) void gemm_skinny_nn_kernel(GemmArgs a) {
@@ -755,12 +694,14 @@ int gemm_typed(int batch, int m, int n, int k, const void* A, int64_t sa_b, int6
         g.alpha = alpha; g.beta = beta;
         g.c_vec_ok = (rsc % 4 == 0) && (sc_b % 4 == 0) && aligned(C, 4 * sizeof(oraw));
         if (m <= SKINNY_M) {
-            dim3 block(64 * SKINNY_WAVES);
             if (nt) {
-                gemm_skinny_nt_kernel<T, TO><<<dim3((n + 15) / 16, batch), block, 0, s>>>(g);
-            } else {
-                gemm_skinny_nn_kernel<T, TO><<<dim3((n + 63) / 64, batch), block, 0, s>>>(g);
+                GemvArgs v{};
+                v.A = A; v.lda = rsa; v.W = B; v.ldw = csb; v.C = C; v.ldc = rsc;
+                v.sa_b = sa_b; v.sw_b = sb_b; v.sc_b = sc_b;
+                v.m = m; v.n = n; v.k = k; v.alpha = alpha; v.beta = beta;
+                return gemv_dispatch(0, T::code, TO::code, v, batch, s);
             }
+            gemm_skinny_nn_kernel<T, TO><<<dim3((n + 63) / 64, batch), 64 * SKINNY_WAVES, 0, s>>>(g);
             return status_of(hipGetLastError());
         }
         // DMA-staged fast path: whole k steps, 16-byte aligned rows everywhere.

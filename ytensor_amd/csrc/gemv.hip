@@ -1,0 +1,311 @@
+// gemv.hip — skinny GEMM (M <= 16 rows of activations against a weight
+// W [N, K], i.e. the decode-time `linear`) with optional fused prologues.
+//
+// Reference operations replaced (example/qwen3/src/qwen3.cpp):
+//   * linear(x, W) (src/function/ops.inl:84-91) for M <= 16, which the
+//     reference runs as gemv_row_simd (src/kernel/avx2/sgemv.inl:443-717);
+//   * rmsNorm_(x, w) feeding a linear (qwen3.cpp:271-283, 365-413; the norm is
+//     src/function/normalization.inl:256-277): the normalised, bf16-rounded
+//     activation is built in the GEMV's operand prologue;
+//   * swish(gate) * up feeding the down projection (qwen3.cpp:193-200,
+//     src/ytensor_function.inl:42-52);
+//   * the greedy argmax over the LM-head logits (qwen3.cpp:465-486): the
+//     epilogue leaves one (max, index) pair per 16-column tile and a one-block
+//     kernel reduces them and advances the decode state.
+// The prologues reproduce the standalone kernels' arithmetic exactly
+// (rms_norm_kernel: same per-thread FMA order, wave butterflies and pairwise
+// combination; silu_mul_kernel: same stable sigmoid), so a fused call gives
+// the same bits as the unfused sequence.
+//
+// MI355X design: HBM-bound on the weight stream. One workgroup per 16 output
+// columns; its waves split K and each wave issues all of its 16-byte weight
+// loads for a round (UNR chunks per lane) before consuming any, so a single
+// memory latency covers the wave's share; non-temporal loads for the weights
+// (read once). v_mfma_f32_16x16x32 serves as the 16-lane dot-product reducer
+// (its flops are free against the byte stream); the waves' 16 x 16 partial
+// tiles are summed through LDS. Small N gets 16 waves per column tile so
+// that the chip still has enough loads in flight.
+
+#include <cfloat>
+
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace ythip {
+
+constexpr int GEMV_M = 16;
+constexpr int GEMV_LDS_MAX = 64 * 1024;  // bytes of the staged A' (prologues 1 and 2)
+
+
+// Stable sigmoid of the reference (src/ytensor_function.inl:43-52), as in silu_mul_kernel.
+__device__ __forceinline__ float silu_ref(float a) {
+    float sig;
+    if (a >= 0.0f) {
+        const float z = expf(-a);
+        sig = 1.0f / (1.0f + z);
+    } else {
+        const float z = expf(a);
+        sig = z / (1.0f + z);
+    }
+    return a * sig;
+}
+
+template <class T, class TO, int WAVES, int PRO>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
+    using raw = typename T::raw;
+    constexpr int VEC = 16 / sizeof(raw);
+    constexpr int KSTEP = 4 * VEC;  // k covered by one MFMA chunk across the 4 lane groups
+    constexpr int UNR = 8;
+    static_assert(PRO == 0 || sizeof(raw) == 2, "fused prologues are 16-bit");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int bz = blockIdx.y;
+    const int nsteps = (a.k + KSTEP - 1) / KSTEP;
+    const int per_wave = (nsteps + WAVES - 1) / WAVES;
+    const int s_begin = wave * per_wave, s_end = min(nsteps, s_begin + per_wave);
+    const bool arow = r < a.m, brow = n0 + r < a.n;
+    const raw* __restrict__ wrp =
+        static_cast<const raw*>(a.W) + bz * a.sw_b + (int64_t)(brow ? n0 + r : 0) * a.ldw + g * VEC;
+
+    auto load_w = [&](int s) -> u32x4 {
+        const int k = s * KSTEP + g * VEC;
+        if (s < s_end && k < a.k && brow)
+            return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrp + (int64_t)s * KSTEP));
+        return u32x4{0u, 0u, 0u, 0u};
+    };
+    // The first round of weight loads goes out before the prologue's reduction.
+    u32x4 fb[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) fb[u] = load_w(s_begin + u);
+
+    __shared__ float s_part[GEMV_M][4];
+    __shared__ float s_den[GEMV_M];
+    if constexpr (PRO == 1) {
+        // rms_norm_kernel's reduction, row by row, on the first 256 threads.
+        const float* X = static_cast<const float*>(a.A) + bz * a.sa_b;
+        for (int row = 0; row < a.m; ++row) {
+            if (tid < 256) {
+                float ss = 0.f;
+                for (int i = tid; i < a.k; i += 256) {
+                    const float v = X[(int64_t)row * a.lda + i];
+                    ss = fmaf(v, v, ss);
+                }
+                ss = wave_sum(ss);
+                if (lane == 0) s_part[row][wave] = ss;
+            }
+        }
+        __syncthreads();
+        if (tid < a.m) {
+            const float tot = (s_part[tid][0] + s_part[tid][1]) + (s_part[tid][2] + s_part[tid][3]);
+            s_den[tid] = sqrtf(tot / (float)a.k + a.eps);
+        }
+        __syncthreads();
+    }
+    // Prologues 1 and 2 build A' [m][k] once per workgroup in LDS (every thread
+    // takes whole elements, so no lane idles on the m < 16 padding rows), then the
+    // waves read their operand chunks from there.
+    extern __shared__ u32x4 gemv_lds[];  // dynamic: m * k 16-bit values
+    raw* sAp = reinterpret_cast<raw*>(gemv_lds);
+    if constexpr (PRO != 0) {
+        const int total = a.m * a.k;
+        for (int e = tid; e < total; e += 64 * WAVES) {
+            const int row = e / a.k, col = e - row * a.k;
+            float y;
+            if constexpr (PRO == 1) {
+                const float* xr = static_cast<const float*>(a.A) + bz * a.sa_b + (int64_t)row * a.lda;
+                y = (xr[col] / s_den[row]) * a.nw[col];
+            } else {
+                const raw* gp = static_cast<const raw*>(a.A) + bz * a.sa_b + (int64_t)row * a.lda;
+                y = silu_ref(load_as_f32<T>(gp, col)) * load_as_f32<T>(gp, a.k + col);
+            }
+            sAp[e] = static_cast<raw>(pack2<T>(y, 0.0f) & 0xffffu);
+        }
+        __syncthreads();
+    }
+
+    // A operand chunk s of this lane: 8 (16-bit) or 4 (fp32) k values of row r.
+    auto load_a = [&](int s) -> u32x4 {
+        const int k = s * KSTEP + g * VEC;
+        if (!(s < s_end && k < a.k && arow)) return u32x4{0u, 0u, 0u, 0u};
+        if constexpr (PRO == 0)
+            return *reinterpret_cast<const u32x4*>(static_cast<const raw*>(a.A) + bz * a.sa_b + (int64_t)r * a.lda + k);
+        else
+            return *reinterpret_cast<const u32x4*>(&sAp[r * a.k + k]);
+    };
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s = s_begin; s < s_end; s += UNR) {
+        if (s != s_begin) {
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) fb[u] = load_w(s + u);
+        }
+        u32x4 fa[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) fa[u] = load_a(s + u);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) acc = mfma_chunk(T{}, fb[u], fa[u], acc);
+    }
+    // acc: lane holds C[m = r][n0 + 4g + j] partial over this wave's k range.
+    __shared__ f32x4 red[WAVES][64];
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4 t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) t += red[w][lane];
+    using oraw = typename TO::raw;
+    float v[4];
+    oraw* crow = static_cast<oraw*>(a.C) + bz * a.sc_b + (int64_t)r * a.ldc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 4 * g + j;
+        v[j] = a.alpha * t[j];
+        if (arow && n < a.n) {
+            if (a.beta != 0.0f) v[j] += a.beta * load_as_f32<TO>(crow, n);
+            store_from_f32<TO>(crow, n, v[j]);
+            if constexpr (sizeof(oraw) == 2) v[j] = load_as_f32<TO>(crow, n);  // the value as stored
+        }
+    }
+    if (a.amax != nullptr && bz == 0) {
+        // row 0: lanes 0, 16, 32, 48 hold its 16 columns; lowest index wins ties, NaN never wins
+        float best = -INFINITY;
+        int idx = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 4 * g + j;
+            if (n < a.n && (v[j] > best || (v[j] == best && n < idx))) { best = v[j]; idx = n; }
+        }
+#pragma unroll
+        for (int off = 16; off <= 32; off <<= 1) {
+            const float ob = __shfl_xor(best, off, 64);
+            const int oi = __shfl_xor(idx, off, 64);
+            if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+        }
+        if (lane == 0) {
+            a.amax[2 * blockIdx.x] = best;
+            a.amax[2 * blockIdx.x + 1] = __int_as_float(idx);
+        }
+    }
+}
+
+// Final greedy step over the per-tile (max, index) pairs; same tie rule and
+// state update as argmax_step_kernel.
+__global__ __launch_bounds__(1024) void argmax_finish_kernel(const float* parts, int n_parts, int32_t* token,
+                                                             int32_t* history, int32_t* state) {
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n_parts; i += 1024) {
+        const float v = parts[2 * i];
+        const int id = __float_as_int(parts[2 * i + 1]);
+        if (v > best || (v == best && id < idx)) { best = v; idx = id; }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ob = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    }
+    __shared__ float sb[16];
+    __shared__ int si[16];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) { sb[wave] = best; si[wave] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = sb[0];
+        int id = si[0];
+        for (int w = 1; w < 16; ++w)
+            if (sb[w] > b || (sb[w] == b && si[w] < id)) { b = sb[w]; id = si[w]; }
+        if (id == 0x7fffffff) id = 0;  // all NaN / empty: token 0
+        token[0] = id;
+        if (state != nullptr) {
+            if (history != nullptr) history[state[0]] = id;
+            state[0] += 1;
+            state[1] += 1;
+            state[2] = state[1] + 1;
+        }
+    }
+}
+
+namespace {
+
+template <class T, class TO, int PRO>
+hipError_t launch_gemv_t(const GemvArgs& a, int batch, hipStream_t s) {
+    const int tiles = (a.n + 15) / 16;
+    // fewer than ~2 column tiles per CU: more waves per tile to keep loads in flight
+    const size_t lds = PRO == 0 ? 0 : (size_t)a.m * a.k * sizeof(typename T::raw);
+    if ((int64_t)tiles * batch < 512)
+        gemv_kernel<T, TO, 16, PRO><<<dim3(tiles, batch), 1024, lds, s>>>(a);
+    else
+        gemv_kernel<T, TO, 8, PRO><<<dim3(tiles, batch), 512, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int gemv_dispatch(int prologue, int dtype_in, int dtype_out, const GemvArgs& a, int batch, hipStream_t s) {
+#define YTHIP_GEMV(TI, TOUT)                                                          \
+    do {                                                                              \
+        if (prologue == 0) return status_of(launch_gemv_t<TI, TOUT, 0>(a, batch, s)); \
+        if constexpr (sizeof(typename TI::raw) == 2) {                                \
+            if (prologue == 1) return status_of(launch_gemv_t<TI, TOUT, 1>(a, batch, s)); \
+            if (prologue == 2) return status_of(launch_gemv_t<TI, TOUT, 2>(a, batch, s)); \
+        }                                                                             \
+        return fail(YTHIP_EUNSUPPORTED, "gemv: prologue %d needs 16-bit inputs", prologue); \
+    } while (0)
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_BF16) YTHIP_GEMV(BF16, BF16);
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_F32) YTHIP_GEMV(BF16, F32);
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F16) YTHIP_GEMV(F16, F16);
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F32) YTHIP_GEMV(F16, F32);
+    if (dtype_in == YTHIP_F32 && dtype_out == YTHIP_F32) YTHIP_GEMV(F32, F32);
+#undef YTHIP_GEMV
+    return fail(YTHIP_EUNSUPPORTED, "gemv: unsupported dtype_in/dtype_out combination %d/%d", dtype_in, dtype_out);
+}
+
+}  // namespace ythip
+
+using namespace ythip;
+
+extern "C" {
+
+__attribute__((visibility("default"))) int ythip_gemv_fused(int prologue, int dtype_in, int dtype_out, int m, int n,
+                                                            int k, const void* A, int64_t lda, const float* norm_w,
+                                                            float eps, const void* W, int64_t ldw, void* C,
+                                                            int64_t ldc, float alpha, float beta,
+                                                            float* argmax_parts, void* stream) {
+    if (prologue < 0 || prologue > 2) return fail(YTHIP_EINVAL, "ythip_gemv_fused: prologue %d", prologue);
+    if (m < 0 || n < 0 || k < 0) return fail(YTHIP_EINVAL, "ythip_gemv_fused: negative size");
+    if (m > GEMV_M) return fail(YTHIP_EUNSUPPORTED, "ythip_gemv_fused: m = %d (at most %d rows)", m, GEMV_M);
+    if (m == 0 || n == 0) return 0;
+    if (!A || !W || !C) return fail(YTHIP_EINVAL, "ythip_gemv_fused: NULL A, W or C");
+    if (prologue == 1 && (norm_w == nullptr || dtype_in == YTHIP_F32))
+        return fail(YTHIP_EINVAL, "ythip_gemv_fused: the RMSNorm prologue needs norm_w and 16-bit weights");
+    const int es = dtype_in == YTHIP_F32 ? 4 : 2;
+    const int vec = 16 / es;
+    const int64_t a_cols = prologue == 2 ? 2 * (int64_t)k : k;
+    if (k % vec || ldw % vec || (prologue == 1 ? lda % 4 : lda % vec) || lda < a_cols || ldw < k ||
+        (reinterpret_cast<uintptr_t>(A) % 16) || (reinterpret_cast<uintptr_t>(W) % 16) ||
+        (prologue == 1 && (reinterpret_cast<uintptr_t>(norm_w) % 16)))
+        return fail(YTHIP_EUNSUPPORTED,
+                    "ythip_gemv_fused: rows of A/W must be 16-byte aligned and k a multiple of %d", vec);
+    if (ldc < n) return fail(YTHIP_EINVAL, "ythip_gemv_fused: ldc < n");
+    if (prologue != 0 && (int64_t)m * k * es > GEMV_LDS_MAX)
+        return fail(YTHIP_EUNSUPPORTED, "ythip_gemv_fused: m * k = %lld exceeds the %d-byte operand staging",
+                    (long long)m * k, GEMV_LDS_MAX);
+    GemvArgs a{};
+    a.A = A; a.lda = lda; a.nw = norm_w; a.eps = eps;
+    a.W = W; a.ldw = ldw; a.C = C; a.ldc = ldc;
+    a.m = m; a.n = n; a.k = k; a.alpha = alpha; a.beta = beta;
+    a.amax = argmax_parts;
+    return gemv_dispatch(prologue, dtype_in, dtype_out, a, 1, static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int ythip_argmax_finish(const float* parts, int n_parts, int32_t* token,
+                                                               int32_t* history, int32_t* state, void* stream) {
+    if (n_parts <= 0 || parts == nullptr || token == nullptr)
+        return fail(YTHIP_EINVAL, "ythip_argmax_finish: bad arguments");
+    argmax_finish_kernel<<<1, 1024, 0, static_cast<hipStream_t>(stream)>>>(parts, n_parts, token, history, state);
+    return status_of(hipGetLastError());
+}
+
+}  // extern "C"

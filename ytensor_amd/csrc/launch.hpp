@@ -19,4 +19,24 @@ int gemm_dispatch(int dtype_in, int dtype_out, int batch, int m, int n, int k, c
                   int64_t rsa, int64_t csa, const void* B, int64_t sb_b, int64_t rsb, int64_t csb, void* C,
                   int64_t sc_b, int64_t rsc, int64_t csc, float alpha, float beta, hipStream_t s);
 
+// Skinny GEMM / fused decode GEMV (gemv.hip): C[m, n] = alpha * A' . W^T + beta * C
+// with A' built by the prologue (0: A as is, 1: RMSNorm of fp32 rows, 2: SwiGLU
+// of [gate | up] rows).
+struct GemvArgs {
+    const void* A;  // prologue 0: T [m][k]; 1: fp32 [m][k]; 2: T [m][2k] (gate | up)
+    int64_t lda;
+    const float* nw;  // prologue 1: norm weight [k]
+    float eps;
+    const void* W;  // [n][k] rows, stride ldw
+    int64_t ldw;
+    void* C;
+    int64_t ldc;
+    int64_t sa_b, sw_b, sc_b;  // batch strides (blockIdx.y)
+    int m, n, k;
+    float alpha, beta;
+    float* amax;  // optional: per 16-column tile (max, index) of row 0
+};
+
+int gemv_dispatch(int prologue, int dtype_in, int dtype_out, const GemvArgs& a, int batch, hipStream_t s);
+
 }  // namespace ythip

@@ -20,12 +20,6 @@
 
 namespace ythip {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 struct NormRopeArgs {
     const void* qkv;
     int64_t ld_qkv;

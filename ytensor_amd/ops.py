@@ -320,6 +320,57 @@ def argmax_step(logits: torch.Tensor, token: torch.Tensor, history: torch.Tensor
     return token
 
 
+GEMV_PROLOGUE = {"none": 0, "rmsnorm": 1, "swiglu": 2}
+
+
+def gemv_fused(a: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, prologue: str = "none",
+               norm_weight: torch.Tensor | None = None, eps: float = 1e-6, alpha: float = 1.0, beta: float = 0.0,
+               argmax_parts: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode-time linear for at most 16 rows, out = alpha * A' @ weight.T + beta * out,
+    weight [N, K] (the `linear` layout). prologue "none": A' = a [m, K];
+    "rmsnorm": A' = rms_norm(a fp32 [m, K], norm_weight, eps) rounded to the weight
+    type; "swiglu": A' = silu(gate) * up of a = [m, 2K] (gate | up). argmax_parts
+    (fp32, 2 * ceil(N/16) values) receives per-tile (max, index) pairs of row 0."""
+    _dev(a, weight, out)
+    if prologue not in GEMV_PROLOGUE:
+        raise ValueError(f"prologue must be one of {sorted(GEMV_PROLOGUE)}")
+    pro = GEMV_PROLOGUE[prologue]
+    n, k = weight.shape
+    a2 = a.reshape(-1, a.shape[-1])
+    o2 = out.reshape(-1, out.shape[-1])
+    m = a2.shape[0]
+    if o2.shape != (m, n):
+        raise ValueError(f"out must be [{m}, {n}], got {tuple(o2.shape)}")
+    if weight.stride(1) != 1 or a2.stride(1) != 1 or o2.stride(1) != 1:
+        raise ValueError("gemv_fused needs unit column strides")
+    want_a = torch.float32 if pro == 1 else weight.dtype
+    if a.dtype != want_a:
+        raise ValueError(f"A must be {want_a} for prologue {prologue!r}")
+    if a2.shape[1] != (2 * k if pro == 2 else k):
+        raise ValueError("A's width does not match the weight (2K for swiglu)")
+    if pro == 1 and (norm_weight is None or norm_weight.dtype != torch.float32):
+        raise ValueError("the rmsnorm prologue needs an fp32 norm_weight")
+    if argmax_parts is not None and (argmax_parts.dtype != torch.float32 or argmax_parts.numel() < 2 * ((n + 15) // 16)):
+        raise ValueError("argmax_parts must be fp32 with 2 * ceil(N/16) values")
+    check(_lib.lib().ythip_gemv_fused(pro, _code(weight), _code(out), m, n, k, a2.data_ptr(), a2.stride(0),
+                                      None if norm_weight is None else norm_weight.data_ptr(), float(eps),
+                                      weight.data_ptr(), weight.stride(0), o2.data_ptr(), o2.stride(0),
+                                      float(alpha), float(beta),
+                                      None if argmax_parts is None else argmax_parts.data_ptr(), _stream()),
+          "ythip_gemv_fused")
+    return out
+
+
+def argmax_finish(parts: torch.Tensor, n_parts: int, token: torch.Tensor, history: torch.Tensor | None = None,
+                  state: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy token from gemv_fused's per-tile (max, index) pairs; as argmax_step."""
+    _dev(parts, token)
+    check(_lib.lib().ythip_argmax_finish(parts.data_ptr(), int(n_parts), token.data_ptr(),
+                                         None if history is None else history.data_ptr(),
+                                         None if state is None else state.data_ptr(), _stream()), "ythip_argmax_finish")
+    return token
+
+
 def default_scale(d: int) -> float:
     """scale = 0 -> 1/sqrt(d) (src/function/ops.inl:378-381)."""
     return 1.0 / math.sqrt(d)

@@ -13,9 +13,11 @@ MI355X layout and execution:
     fp32 straight into the residual with beta = 1 (residual add fused into
     the GEMM epilogue); logits fp32;
   * KV cache bf16 [layers][1, kv_heads, ctx, head_dim];
-  * a decode step is ~10 launches per layer with no host-side value that
-    changes between steps (token id and positions live in device memory), so
-    it is captured once as a HIP graph and replayed per token.
+  * a decode step is 7 launches per layer (the RMSNorms ride in the qkv and
+    gate_up GEMV prologues, SwiGLU in the down projection's, the final norm
+    and the argmax in the LM head's) with no host-side value that changes
+    between steps (token id and positions live in device memory), so it is
+    captured once as a HIP graph and replayed per token.
 Every arithmetic operation runs in libythip.so; torch only allocates device
 memory and provides the stream / graph capture.
 """
@@ -66,8 +68,9 @@ class Qwen3:
     """Greedy batch-1 generation on one GPU."""
 
     def __init__(self, cfg: Qwen3Config, weights, device="cuda", max_ctx: int | None = None,
-                 max_prompt: int = 512):
+                 max_prompt: int = 512, fused: bool = True):
         self.cfg = cfg
+        self.fused = fused  # decode step with the fused GEMV prologues (same bits as the unfused path)
         self.dev = torch.device(device)
         self.max_ctx = min(cfg.max_pos, max_ctx or cfg.max_pos)
         self.max_prompt = max_prompt
@@ -133,6 +136,7 @@ class Qwen3:
         self.state = torch.zeros((3,), dtype=torch.int32, device=dev)  # generated, position, kv_len
         self.ws = torch.empty((ops.decode_workspace_bytes(1, nh, self.max_ctx, hd),), dtype=torch.uint8, device=dev)
         self.qd = torch.empty((1, nh, 1, hd), dtype=bf, device=dev)  # decode query
+        self.amax = torch.empty((2 * ((cfg.vocab + 15) // 16),), dtype=f32, device=dev)  # LM-head tile maxima
 
     # ------------------------------------------------------------------ steps
     def _attn_view(self, S: int) -> torch.Tensor:
@@ -144,9 +148,12 @@ class Qwen3:
         cfg, L = self.cfg, self.layers[i]
         nh, nkv, hd = cfg.n_heads, cfg.n_kv, cfg.head_dim
         x, h = self.x[:S], self.h[:S]
+        kc, vc = self.kc[i], self.vc[i]
+        if decode and self.fused:
+            self._layer_decode_fused(i)
+            return
         ops.rms_norm(x, L["n1"], cfg.eps, out=h)
         ops.gemm(h, L["qkv"].t(), self.qkv[:S])
-        kc, vc = self.kc[i], self.vc[i]
         if decode:
             qv = self.qd
             ops.rms_norm_rope(self.qkv[:S].view(1, S, -1), nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
@@ -165,7 +172,29 @@ class Qwen3:
         ops.silu_mul(self.gu[:S], out=self.act[:S])
         ops.gemm(self.act[:S], L["down"].t(), x, beta=1.0)        # x += act . Wdown^T
 
+    def _layer_decode_fused(self, i: int) -> None:
+        """One token through layer i in 7 launches: the RMSNorms ride in the
+        qkv / gate_up GEMV prologues and SwiGLU in the down projection's."""
+        cfg, L = self.cfg, self.layers[i]
+        nh, nkv, hd = cfg.n_heads, cfg.n_kv, cfg.head_dim
+        x = self.x[:1]
+        kc, vc = self.kc[i], self.vc[i]
+        ops.gemv_fused(x, L["qkv"], self.qkv[:1], "rmsnorm", L["n1"], cfg.eps)
+        ops.rms_norm_rope(self.qkv[:1].view(1, 1, -1), nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
+                          q_out=self.qd, k_out=kc, v_out=vc, dev_pos=self.state[1:2])
+        ops.decode_attention(self.qd.view(1, nh, hd), kc, vc, kv_len=self.state[2:3],
+                             out=self.attn[:1].view(1, nh, hd), workspace=self.ws)
+        ops.gemv_fused(self.attn[:1], L["o"], x, beta=1.0)                         # x += attn . Wo^T
+        ops.gemv_fused(x, L["gu"], self.gu[:1], "rmsnorm", L["n2"], cfg.eps)
+        ops.gemv_fused(self.gu[:1], L["down"], x, "swiglu", beta=1.0)             # x += swiglu . Wdown^T
+
     def _head(self, S: int) -> None:
+        if S == 1 and self.fused:
+            # final norm + tied LM head + per-tile argmax in one launch, then the pick
+            ops.gemv_fused(self.x[:1], self.embed, self.logits, "rmsnorm", self.fnorm, self.cfg.eps,
+                           argmax_parts=self.amax)
+            ops.argmax_finish(self.amax, self.amax.numel() // 2, self.token, self.history, self.state)
+            return
         ops.rms_norm(self.x[S - 1:S], self.fnorm, self.cfg.eps, out=self.hf)
         ops.gemm(self.hf, self.embed.t(), self.logits)             # tied LM head, fp32 logits
         ops.argmax_step(self.logits, self.token, self.history, self.state)
