@@ -67,11 +67,11 @@ struct AttnArgs {
 // the linear id is remapped so each XCD walks a contiguous range of
 // (kv head, query block) pairs -- one KV head's K/V stays in one XCD's L2 --
 // and, for causal masks, the longest query blocks start first.
-template <class T, int D, int MODE, int GH>
+template <class T, int D, int MODE, int GH, int QT>
 __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     using raw = typename T::raw;
     constexpr int THREADS = 256 * GH;
-    constexpr int BQ = 128, BKV = 64, WQ = 32;
+    constexpr int WQ = 16 * QT, BQ = 4 * WQ, BKV = 64;  // QT 16-query tiles per wave
     constexpr int KCH = D / 8;    // 16-byte chunks per K/V row
     constexpr int DT = D / 16;    // output d tiles
     constexpr int KS = D / 32;    // d steps of the score MFMA
@@ -109,9 +109,9 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     const raw* Kp = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1;
     const raw* Vp = static_cast<const raw*>(a.V) + b * a.vs0 + kvh * a.vs1;
 
-    u32x4 qf[2][KS];
+    u32x4 qf[QT][KS];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int q = q0 + qt * 16 + l16;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -132,10 +132,15 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     // O rescale is rare; p = 2^((s - m) c) <= 2^8 stays far from any overflow and
     // the final O / l is independent of m.
     constexpr float LAZY = 8.0f;
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-    f32x4 o[2][DT];
+    float m[QT], l[QT];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int qt = 0; qt < QT; ++qt) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.f;
+    }
+    f32x4 o[QT][DT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -173,12 +178,12 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         }
     };
 
-    f32x4 s[2][4];
+    f32x4 s[QT][4];
     // S^T = K . Q^T for block kb (K stage kb & 1).
     auto qk = [&](int kb) {
         const u32x4* cK = sK + (kb & 1) * STG;
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -188,7 +193,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
                 const int key = kt * 16 + l16;
                 const u32x4 kf = cK[key * KCH + ((ks * 4 + g) ^ (key & KMASK))];
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma_chunk(T{}, kf, qf[qt][ks], s[qt][kt]);
+                for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma_chunk(T{}, kf, qf[qt][ks], s[qt][kt]);
             }
         }
     };
@@ -196,11 +201,11 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     auto softmax_pv = [&](int kb) {
         const int k0 = kb * BKV;
         const bool need_mask = (MODE == 2) || (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off);
-        u32x4 pk[2][2];
+        u32x4 pk[QT][2];
         bool rescale = false;
-        float alpha[2];
+        float alpha[QT];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
             const int qa = q0 + qt * 16 + l16;
             float v[4][4];
             if (need_mask) {
@@ -258,7 +263,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         // O *= alpha only when some lane's reference point moved in this block.
         if (__ballot(rescale) != 0) {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+            for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha[qt];
         }
@@ -277,7 +282,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
                     vf[2 * hh + 1] = w2[1];
                 }
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) o[qt][dt] = mfma_chunk(T{}, vf, pk[qt][kk], o[qt][dt]);
+                for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_chunk(T{}, vf, pk[qt][kk], o[qt][dt]);
             }
         }
     };
@@ -300,7 +305,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
 
     raw* Op = static_cast<raw*>(a.O) + b * a.os0 + h * a.os1;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         float L = l[qt];
         L += __shfl_xor(L, 16, 64);
         L += __shfl_xor(L, 32, 64);
@@ -556,13 +561,14 @@ namespace {
 
 bool al(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
-template <class T, int D, int GH>
+template <class T, int D, int GH, int QT>
 hipError_t launch_prefill_gh(AttnArgs a, int mode, hipStream_t s) {
-    a.nqb = (a.Sq + 127) / 128;
+    constexpr int BQ = 64 * QT;
+    a.nqb = (a.Sq + BQ - 1) / BQ;
     dim3 grid(a.nqb * a.B * a.Hq / GH);
-    if (mode == 0) attn_fwd_mfma<T, D, 0, GH><<<grid, 256 * GH, 0, s>>>(a);
-    else if (mode == 1) attn_fwd_mfma<T, D, 1, GH><<<grid, 256 * GH, 0, s>>>(a);
-    else attn_fwd_mfma<T, D, 2, GH><<<grid, 256 * GH, 0, s>>>(a);
+    if (mode == 0) attn_fwd_mfma<T, D, 0, GH, QT><<<grid, 256 * GH, 0, s>>>(a);
+    else if (mode == 1) attn_fwd_mfma<T, D, 1, GH, QT><<<grid, 256 * GH, 0, s>>>(a);
+    else attn_fwd_mfma<T, D, 2, GH, QT><<<grid, 256 * GH, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -571,8 +577,12 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     // Two query heads per workgroup (K/V staged once for both) when the GQA
     // group size is even and the paired grid still covers the 256 CUs twice.
     const int64_t paired = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq / 2;
-    if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) return launch_prefill_gh<T, D, 2>(a, mode, s);
-    return launch_prefill_gh<T, D, 1>(a, mode, s);
+    if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) return launch_prefill_gh<T, D, 2, 2>(a, mode, s);
+    // Short sequences: 16 queries per wave doubles the workgroups (two per CU)
+    // and halves the per-block work on the longest causal row's serial chain.
+    const int64_t wgs = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq;
+    if (wgs < 512) return launch_prefill_gh<T, D, 1, 1>(a, mode, s);
+    return launch_prefill_gh<T, D, 1, 2>(a, mode, s);
 }
 
 template <class T>
