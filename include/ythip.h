@@ -119,6 +119,8 @@ int ythip_attn_decode(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
  * wq / wk (fp32 [d]) may be NULL to skip that norm; cos/sin (fp32 [*, ld_tab],
  * from RoPECache::precompute, qwen3.cpp:161-175) may be NULL to skip RoPE.
  * Output strides are (batch, head, row); d is contiguous. K/V outputs may be NULL.
+ * All tensors, rows, strides and tables must keep 16-byte alignment
+ * (YTHIP_EUNSUPPORTED otherwise).
  * dev_pos: optional device int32; when given, pos0 and cache_pos are both read
  * from it when the kernel runs (a decode step captured once in a HIP graph).
  */

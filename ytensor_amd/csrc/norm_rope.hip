@@ -10,10 +10,10 @@
 //   The tables are the host's RoPECache::precompute output (qwen3.cpp:161-175)
 //   so the angles are bit-identical to the CPU path.
 //
-// Both kernels are HBM-bound elementwise passes: one wave per (token, head)
-// row of d = 128 elements (64 lanes x 2, lane l holds x[l] and x[l + d/2], the
-// two halves RoPE pairs up), a wave-wide DPP/shuffle sum of squares, then one
-// vectorised store.
+// Both kernels are HBM-bound elementwise passes. The fused one gives each
+// (token, head) row d/16 lanes with 8 rotate-half pairs each (16-byte loads and
+// stores, non-temporal reads of the projection output, a shuffle sum of
+// squares over the row's lanes).
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -39,70 +39,108 @@ struct NormRopeArgs {
     const int32_t* dev_pos;  // when set: pos0 = cache_pos = *dev_pos (graph-replayable decode)
 };
 
-// One wave per (token, head) with d = 2 * HALF; HALF <= 64 (d <= 128).
+// LPR lanes per (token, head) row of d = 2 * HALF: lane j of a row holds
+// x[8j .. 8j+7] and x[HALF + 8j .. HALF + 8j+7], i.e. 8 rotate-half pairs, so
+// every global access is 16 bytes (bf16/fp16) and RoPE stays inside the lane.
 template <class T, int HALF>
 __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
-    const int wave = (blockIdx.x * 4) + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
+    using raw = typename T::raw;
+    constexpr int D = 2 * HALF;
+    constexpr int LPR = HALF / 8;            // lanes per row
+    constexpr int RPB = 256 / LPR;           // rows per block
+    const int j = threadIdx.x % LPR;
     const int H = a.Hq + 2 * a.Hkv;
-    const int64_t rows = (int64_t)a.B * a.S * H;
-    if (wave >= rows) return;
-    const int h = wave % H;
-    const int64_t tok = wave / H;
+    const int rows = a.B * a.S * H;          // < 2^31, checked on the host
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    if (row >= rows) return;                 // whole rows leave together (LPR divides 64)
+    const int h = row % H;
+    const int tok = row / H;
     const int s = tok % a.S;
     const int b = tok / a.S;
-    constexpr int D = 2 * HALF;
     const int pos0 = a.dev_pos ? a.dev_pos[0] : a.pos0;
     const int cache_pos = a.dev_pos ? a.dev_pos[0] : a.cache_pos;
-    const bool active = lane < HALF;
 
-    const auto* src = static_cast<const typename T::raw*>(a.qkv) + tok * a.ld_qkv + (int64_t)h * D;
-    float x1 = 0.f, x2 = 0.f;
-    if (active) {
-        x1 = load_as_f32<T>(src, lane);
-        x2 = load_as_f32<T>(src, lane + HALF);
-    }
-    void* dst;
-    int64_t off;
+    const raw* src = static_cast<const raw*>(a.qkv) + (int64_t)tok * a.ld_qkv + (int64_t)h * D + 8 * j;
+    float x1[8], x2[8];
+    auto load8 = [&](const raw* p, float (&x)[8]) {
+        if constexpr (sizeof(raw) == 2) {
+            const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = lo_as_f32(T{}, w[e]);
+                x[2 * e + 1] = hi_as_f32(T{}, w[e]);
+            }
+        } else {
+            const f32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+            const f32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + 1);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = lo[e];
+                x[e + 4] = hi[e];
+            }
+        }
+    };
+    auto store8 = [&](raw* p, const float (&x)[8]) {
+        if constexpr (sizeof(raw) == 2) {
+            *reinterpret_cast<u32x4*>(p) = u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(x[4], x[5]),
+                                                 pack2<T>(x[6], x[7])};
+        } else {
+            reinterpret_cast<f32x4*>(p)[0] = f32x4{x[0], x[1], x[2], x[3]};
+            reinterpret_cast<f32x4*>(p)[1] = f32x4{x[4], x[5], x[6], x[7]};
+        }
+    };
+    load8(src, x1);
+    load8(src + HALF, x2);
+
+    raw* dst;
     const float* w = nullptr;
     if (h < a.Hq) {
-        dst = a.q;
-        off = b * a.qs0 + h * a.qs1 + s * a.qs2;
+        dst = static_cast<raw*>(a.q) + b * a.qs0 + h * a.qs1 + s * a.qs2;
         w = a.wq;
     } else if (h < a.Hq + a.Hkv) {
-        dst = a.k;
-        off = b * a.ks0 + (h - a.Hq) * a.ks1 + (int64_t)(cache_pos + s) * a.ks2;
+        dst = static_cast<raw*>(a.k) + b * a.ks0 + (h - a.Hq) * a.ks1 + (int64_t)(cache_pos + s) * a.ks2;
         w = a.wk;
     } else {
-        dst = a.v;
-        off = b * a.vs0 + (h - a.Hq - a.Hkv) * a.vs1 + (int64_t)(cache_pos + s) * a.vs2;
-        if (dst != nullptr && active) {
-            store_from_f32<T>(dst, off + lane, x1);
-            store_from_f32<T>(dst, off + lane + HALF, x2);
-        }
+        if (a.v == nullptr) return;
+        dst = static_cast<raw*>(a.v) + b * a.vs0 + (h - a.Hq - a.Hkv) * a.vs1 + (int64_t)(cache_pos + s) * a.vs2;
+        store8(dst + 8 * j, x1);
+        store8(dst + HALF + 8 * j, x2);
         return;
     }
-    if (dst == nullptr) return;
+    if (static_cast<void*>(dst) == nullptr) return;
     if (w != nullptr) {
-        const float ss = wave_sum(x1 * x1 + x2 * x2);
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(x2[e], x2[e], fmaf(x1[e], x1[e], ss));
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
         const float den = sqrtf(ss / (float)D + a.eps);
-        if (active) {
-            x1 = (x1 / den) * w[lane];
-            x2 = (x2 / den) * w[lane + HALF];
+        const f32x4* w1 = reinterpret_cast<const f32x4*>(w + 8 * j);
+        const f32x4* w2 = reinterpret_cast<const f32x4*>(w + HALF + 8 * j);
+        const f32x4 wa = w1[0], wb = w1[1], wc = w2[0], wd = w2[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x1[e] = (x1[e] / den) * wa[e];
+            x1[e + 4] = (x1[e + 4] / den) * wb[e];
+            x2[e] = (x2[e] / den) * wc[e];
+            x2[e + 4] = (x2[e + 4] / den) * wd[e];
         }
     }
-    if (a.cos_tab != nullptr && active) {
-        const int64_t t = (int64_t)(pos0 + s) * a.ld_tab;
-        const float c = a.cos_tab[t + lane], sn = a.sin_tab[t + lane];
-        const float y1 = fmaf(x1, c, -(x2 * sn));
-        const float y2 = fmaf(x2, c, x1 * sn);
-        x1 = y1;
-        x2 = y2;
+    if (a.cos_tab != nullptr) {
+        const int64_t t = (int64_t)(pos0 + s) * a.ld_tab + 8 * j;
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(a.cos_tab + t), c1 = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.sin_tab + t), s1 = *reinterpret_cast<const f32x4*>(a.sin_tab + t + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float c = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
+            const float y1 = fmaf(x1[e], c, -(x2[e] * sn));
+            const float y2 = fmaf(x2[e], c, x1[e] * sn);
+            x1[e] = y1;
+            x2[e] = y2;
+        }
     }
-    if (active) {
-        store_from_f32<T>(dst, off + lane, x1);
-        store_from_f32<T>(dst, off + lane + HALF, x2);
-    }
+    store8(dst + 8 * j, x1);
+    store8(dst + HALF + 8 * j, x2);
 }
 
 // Row RMSNorm for wide rows (hidden size): one 256-thread block per row.
@@ -131,10 +169,9 @@ namespace {
 template <class T>
 hipError_t launch_norm_rope(const NormRopeArgs& a, int d, hipStream_t s) {
     const int64_t rows = (int64_t)a.B * a.S * (a.Hq + 2 * a.Hkv);
-    dim3 grid((unsigned)((rows + 3) / 4));
     switch (d) {
-        case 64: norm_rope_kernel<T, 32><<<grid, 256, 0, s>>>(a); break;
-        case 128: norm_rope_kernel<T, 64><<<grid, 256, 0, s>>>(a); break;
+        case 64: norm_rope_kernel<T, 32><<<(unsigned)((rows + 63) / 64), 256, 0, s>>>(a); break;   // 4 lanes, 64 rows / block
+        case 128: norm_rope_kernel<T, 64><<<(unsigned)((rows + 31) / 32), 256, 0, s>>>(a); break;  // 8 lanes, 32 rows / block
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -170,6 +207,24 @@ __attribute__((visibility("default"))) int ythip_rmsnorm_rope(
     if ((Kout != nullptr && k_str == nullptr) || (Vout != nullptr && v_str == nullptr) || cache_pos < 0)
         return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: bad K/V output args");
     if (ld_qkv < (int64_t)(Hq + 2 * Hkv) * d) return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: ld_qkv too small");
+    if ((int64_t)B * S * (Hq + 2 * Hkv) >= (int64_t)1 << 31)
+        return fail(YTHIP_EUNSUPPORTED, "ythip_rmsnorm_rope: more than 2^31 rows");
+    // every access is 16 bytes wide: rows, strides and tables must keep that alignment
+    {
+        const int es = dtype == YTHIP_F32 ? 4 : 2;
+        const int64_t v = 16 / es;  // elements per 16 bytes
+        auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+        bool ok = al16(qkv) && ld_qkv % v == 0 && al16(Qout) && q_str[0] % v == 0 && q_str[1] % v == 0 &&
+                  q_str[2] % v == 0;
+        if (Kout) ok = ok && al16(Kout) && k_str[0] % v == 0 && k_str[1] % v == 0 && k_str[2] % v == 0;
+        if (Vout) ok = ok && al16(Vout) && v_str[0] % v == 0 && v_str[1] % v == 0 && v_str[2] % v == 0;
+        if (wq) ok = ok && al16(wq);
+        if (wk) ok = ok && al16(wk);
+        if (cos_tab) ok = ok && al16(cos_tab) && al16(sin_tab) && ld_tab % 4 == 0;
+        if (!ok)
+            return fail(YTHIP_EUNSUPPORTED,
+                        "ythip_rmsnorm_rope: tensors, strides and tables must be 16-byte aligned");
+    }
     NormRopeArgs a{};
     a.qkv = qkv; a.ld_qkv = ld_qkv; a.wq = wq; a.wk = wk; a.eps = eps;
     a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.ld_tab = ld_tab; a.pos0 = pos0;
