@@ -16,7 +16,9 @@ the kernels are launched on):
   qwen3_0p6b      configs[4] shape: 512-token prefill + greedy decode tok/s
   roofline        the headline kernel against MI355X dense bf16 MFMA peak
   cpu_baseline    YTensor's own CPU sgemm (compiled reference when present,
-                  else the oracle restatement) on the host cores, same shape
+                  else the oracle restatement) on the host cores, same shape;
+                  its "rows" time the same CPU path on the prefill, decode and
+                  RMSNorm+RoPE shapes (single thread, bounded samples)
 Synthetic data: torch.randn with fixed seeds, N(0,1) activations and
 N(0,0.02) weights (the configs' distributions). The parity tests use YTensor's
 own seeded generator; the benchmark only needs the shapes and magnitudes.
@@ -175,6 +177,62 @@ def cpu_baseline(M: int, N: int, K: int, budget_s: float = 12.0) -> dict:
             "all_cores": {"value": round(flops / tn / 1e12, 4), "threads": ncores, "calls": nn,
                           "median_s": round(tn, 3)},
             "host": host_info()}
+
+
+def cpu_rows(path, kind: str) -> dict:
+    """The reference's CPU path timed beside the other GPU rows, with its own
+    threading defaults (the GEMM's thread count left at 1; the attention and
+    normalisation loops' OpenMP pools sized by OMP_NUM_THREADS), on bounded
+    samples of the same shapes (a few seconds in all):
+      prefill   yt::function::scaled_dot_product_attention causal GQA,
+                16 q / 8 kv heads, D=128, S=2048 (src/function/attention.inl:1-200)
+      decode    the same with one query row per batch entry, B=16, ctx=8192
+      norm_rope rmsNorm_ of the q and k heads + RoPE of both, S=8192
+                (src/function/normalization.inl:256-277, example/qwen3/qwen3.cpp:101-133)
+    Inputs are N(0,1) (weights N(0,0.02)) rounded to bf16, as on the GPU."""
+    import numpy as np
+    import oracle
+    o = oracle.oracle()
+    path.set_num_threads(1)
+    rng = np.random.default_rng(1)
+
+    def bf(*shape, scale=1.0):
+        x = rng.standard_normal(shape, dtype=np.float32) * np.float32(scale)
+        return o.bf16_to_f32(o.bf16_round(x))
+
+    def med(fn, n):
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
+    rows = {"kind": kind, "threads": "reference defaults: GEMM 1 thread, OpenMP loops OMP_NUM_THREADS="
+                                      + os.environ.get("OMP_NUM_THREADS", "unset (all cores)")}
+    S = 2048
+    q, k, v = bf(1, 16, S, 128), bf(1, 8, S, 128), bf(1, 8, S, 128)
+    t = med(lambda: path.sdpa_gqa(q, k, v, 1 / math.sqrt(128), True), 3)
+    rows["attn_prefill_causal_S2048"] = {"s_per_call": round(t, 4),
+                                         "tflops": round(4.0 * 16 * 128 * S * (S + 1) / 2 / t / 1e12, 4)}
+    ctx = 8192
+    q, k, v = bf(16, 16, 1, 128), bf(16, 8, ctx, 128), bf(16, 8, ctx, 128)
+    t = med(lambda: path.sdpa_gqa(q, k, v, 1 / math.sqrt(128), False), 2)
+    rows["attn_decode_B16_ctx8192"] = {"s_per_call": round(t, 4),
+                                       "gbs_bf16_kv": round(2.0 * 16 * 8 * ctx * 128 * 2 / t / 1e9, 3)}
+    del q, k, v
+    S = 8192
+    qk = bf(1, 24, S, 128)
+    w = bf(128, scale=0.02)
+    cos, sin = path.rope_tables(128, S, 1e6)
+
+    def nr():
+        path.rope(path.rms_norm(qk, w, 1e-6), cos, sin)
+    t = med(nr, 3)
+    byts = 2.0 * 32 * 128 * S * 2 + 2.0 * S * 128 * 4
+    rows["rmsnorm_rope_S8192"] = {"s_per_call": round(t, 4), "gbs_bf16_equiv": round(byts / t / 1e9, 3)}
+    del qk
+    return rows
 
 
 def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256) -> dict:
@@ -393,6 +451,13 @@ def main() -> int:
             cpu = cpu_baseline(M, N, K)
         except Exception as exc:  # the baseline is reported, never required
             cpu = {"error": repr(exc)}
+        if not only and "error" not in cpu:
+            try:
+                import oracle
+                ref = oracle.reference()
+                cpu["rows"] = cpu_rows(ref or oracle.oracle(), cpu["kind"])
+            except Exception as exc:
+                cpu["rows"] = {"error": repr(exc)}
 
     out = {
         "metric": "bf16 GEMM & flash-attn TFLOP/s (% MFMA peak); decode tok/s at Qwen3-0.6B shape",
