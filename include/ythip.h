@@ -13,7 +13,8 @@
  *   - Return value: 0 on success, a negative YTHIP_E* code for argument errors
  *     (nothing was launched), or a positive hipError_t from the launch.
  *     ythip_last_error() returns the calling thread's last message.
- *   - No entry point allocates device memory: scratch space is passed in.
+ *   - No entry point allocates device memory: scratch space is passed in
+ *     (the .yt file calls below own pinned HOST staging buffers).
  *   - No C++ exceptions cross this boundary.
  */
 #ifndef YTHIP_H
@@ -33,8 +34,11 @@ enum ythip_dtype { YTHIP_F32 = 0, YTHIP_F16 = 1, YTHIP_BF16 = 2 };
 
 enum ythip_status {
     YTHIP_OK = 0,
-    YTHIP_EINVAL = -1,      /* bad argument (shape, stride, pointer, dtype) */
-    YTHIP_EUNSUPPORTED = -2 /* valid but not implemented combination */
+    YTHIP_EINVAL = -1,       /* bad argument (shape, stride, pointer, dtype) */
+    YTHIP_EUNSUPPORTED = -2, /* valid but not implemented combination */
+    YTHIP_EIO = -3,          /* file could not be opened, read or written */
+    YTHIP_EFORMAT = -4,      /* not a .yt file, or a corrupt / truncated one */
+    YTHIP_ENOTFOUND = -5     /* no tensor of that name */
 };
 
 /* Attention mask kinds. */
@@ -206,6 +210,86 @@ int ythip_argmax_finish(const float* parts, int n_parts, int32_t* token, int32_t
  * (example/qwen3/src/qwen3.cpp:161-175): cosv/sinv [max_len][dim] (host memory).
  */
 int ythip_rope_tables(int dim, int max_len, float theta, float* cosv, float* sinv);
+
+/* ------------------------------------------------------------------------
+ * .yt checkpoint files (yt::io::YTensorIO, include/ytensor_io.hpp:81-180,
+ * src/ytensor_io.inl) read straight into device memory and written from it.
+ * Host-side calls: paths and the info/tensor descriptors are HOST memory,
+ * `dst` / `data` are DEVICE pointers. Loads are queued on `stream` through two
+ * pinned staging buffers owned by the handle; the destination is complete once
+ * the stream reaches the call's last copy (or after ythip_yt_sync).
+ * ---------------------------------------------------------------------- */
+
+/* dtype for ythip_yt_load / ythip_yt_tensor: copy the stored bytes unchanged
+ * (any dense element type, e.g. int32 or float64). */
+#define YTHIP_YT_RAW (-1)
+
+typedef struct ythip_yt_file ythip_yt_file; /* opaque handle */
+
+/* One tensor record (TensorInfo, include/ytensor_io.hpp:67-78). The strings
+ * and the shape array stay valid until ythip_yt_close. */
+typedef struct ythip_yt_tensor_info {
+    const char* name;
+    const char* dtype;       /* typeName, e.g. "bfloat16", "float32" */
+    const char* tensor_type; /* "dense" (loadable), "map", ... */
+    const char* compress;    /* "" or "zlib" */
+    int32_t type_size;       /* bytes per element */
+    int32_t ndim;
+    const int32_t* shape;    /* ndim dims; ndim == 0 is one element */
+    uint64_t data_offset;    /* payload position in the file */
+    uint64_t compressed_size;
+    uint64_t nbytes;         /* type_size * prod(shape) (uncompressedSize) */
+} ythip_yt_tensor_info;
+
+/* YTensorIO::open(path, yt::io::Read) (src/ytensor_io.inl:256-311) with
+ * readHeader + readIndex (458-559). */
+int ythip_yt_open(const char* path, ythip_yt_file** out);
+/* YTensorIO::close for a read handle; waits for queued copies. */
+int ythip_yt_close(ythip_yt_file* f);
+/* getTensorNames().size() (src/ytensor_io.inl:419-425). */
+int ythip_yt_count(const ythip_yt_file* f);
+/* The header's metadata string (readHeader, src/ytensor_io.inl:482). */
+const char* ythip_yt_metadata(const ythip_yt_file* f);
+/* Index of a tensor by name; "" or NULL is the first one, as getTensorInfo("")
+ * (src/ytensor_io.inl:427-443). Negative status if absent. */
+int ythip_yt_find(const ythip_yt_file* f, const char* name);
+/* getTensorInfo for index (0 <= index < count). */
+int ythip_yt_info(const ythip_yt_file* f, int index, ythip_yt_tensor_info* info);
+/*
+ * YTensorIO::load (src/ytensor_io.inl:785-830) of a dense tensor into device
+ * memory `dst` (dst_bytes available), as dtype F32 / F16 / BF16 or YTHIP_YT_RAW.
+ * A stored float32 / bfloat16 / float16 / float64 / int32 tensor converts with
+ * the reference's casts (the static_casts of toFloat, qwen3.cpp:16-45, and
+ * yt::bfloat16 / yt::float16's conversions); matching types are copied as is.
+ * zlib payloads are inflated on the way. A payload whose size differs from
+ * type_size * prod(shape) is rejected (YTHIP_EFORMAT).
+ */
+int ythip_yt_load(ythip_yt_file* f, int index, void* dst, int dtype, uint64_t dst_bytes, void* stream);
+/* Waits until every copy queued by this handle has completed. */
+int ythip_yt_sync(ythip_yt_file* f);
+
+/* A device tensor to save (dense, row-major). */
+typedef struct ythip_yt_tensor {
+    const char* name;        /* "" = numbered by position, as save() (src/ytensor_io.inl:712) */
+    int dtype;               /* F32 / F16 / BF16, or YTHIP_YT_RAW with dtype_name + type_size */
+    const char* dtype_name;  /* typeName written for YTHIP_YT_RAW (e.g. "int32") */
+    int32_t type_size;       /* bytes per element for YTHIP_YT_RAW */
+    int32_t ndim;
+    const int32_t* shape;
+    const void* data;        /* device pointer */
+} ythip_yt_tensor;
+
+/*
+ * YTensorIO::open(path, Write or Append) + save(t_i, name_i) for each tensor +
+ * close() (src/ytensor_io.inl:256-417, 703-783): byte-for-byte the file the
+ * reference writes for the same tensors. compress "zlib" deflates each payload
+ * as compressData does (templates.inl:17-46); anything else stores it raw.
+ * append = 0 (Write): tensors of an existing file that are not saved again are
+ * dropped; append = 1 (Append): they are kept. A name already present is
+ * replaced in place. The file is written to a temporary name and renamed.
+ */
+int ythip_yt_save(const char* path, int n, const ythip_yt_tensor* tensors, const char* compress, int append,
+                  void* stream);
 
 #ifdef __cplusplus
 }

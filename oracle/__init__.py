@@ -54,6 +54,9 @@ def _bind(lib: ctypes.CDLL, prefix: str) -> ctypes.CDLL:
         "rope_precompute": (None, [_I, _I, _F, _P, _P]),
         "rope": (None, [_P, _I, _I, _I, _I, _P, _P]),
         "qwen3_generate": (_I, [_P, _P, _P, _P, _I, _I, _P, _P, _P]),
+        "yt_save": (_I, [ctypes.c_char_p, _I, _P, _P, _P, _P, _P, ctypes.c_char_p, _I]),
+        "yt_names": (_I, [ctypes.c_char_p, _P, _L]),
+        "yt_load": (_I, [ctypes.c_char_p, ctypes.c_char_p, _P, _L, _P, _P, _I, _P, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, f"{prefix}_{name}", None)
@@ -203,6 +206,43 @@ class CpuPath:
         if st != 0:
             raise ValueError(f"qwen3_generate failed ({st})")
         return toks, marg, lg0
+
+    # --- .yt files (the compiled reference's yt::io::YTensorIO only) ----------
+    def yt_save(self, path: str, tensors, compress: str = "", mode: int = 2) -> None:
+        """tensors: [(name, typeName, shape, numpy payload)]; mode 2 = Write, 3 = Append."""
+        n = len(tensors)
+        names = (ctypes.c_char_p * max(1, n))(*[t[0].encode() for t in tensors])
+        dts = (ctypes.c_char_p * max(1, n))(*[t[1].encode() for t in tensors])
+        nd = (ctypes.c_int * max(1, n))(*[len(t[2]) for t in tensors])
+        dims = [int(d) for t in tensors for d in t[2]]
+        sh = (ctypes.c_int * max(1, len(dims)))(*dims)
+        arrs = [np.ascontiguousarray(t[3]) for t in tensors]
+        ptrs = (ctypes.c_void_p * max(1, n))(*[a.ctypes.data for a in arrs])
+        st = self._fn("yt_save")(path.encode(), n, ctypes.cast(names, _P), ctypes.cast(dts, _P),
+                                 ctypes.cast(nd, _P), ctypes.cast(sh, _P), ctypes.cast(ptrs, _P),
+                                 compress.encode(), mode)
+        if st != 0:
+            raise ValueError(f"reference save failed ({st})")
+
+    def yt_names(self, path: str) -> list[str]:
+        buf = ctypes.create_string_buffer(1 << 16)
+        n = self._fn("yt_names")(path.encode(), ctypes.cast(buf, _P), len(buf))
+        if n < 0:
+            raise ValueError("reference open failed")
+        return buf.value.decode().split("\n")[:n]
+
+    def yt_load(self, path: str, name: str = "", cap: int = 1 << 26):
+        """-> (typeName, shape, bytes) as YTensorIO::load returns them."""
+        out = np.empty(cap, np.uint8)
+        nb = ctypes.c_int64()
+        dt = ctypes.create_string_buffer(64)
+        nd = ctypes.c_int()
+        shape = (ctypes.c_int * 16)()
+        st = self._fn("yt_load")(path.encode(), name.encode(), _ptr(out), cap, ctypes.byref(nb),
+                                 ctypes.cast(dt, _P), 64, ctypes.byref(nd), ctypes.cast(shape, _P))
+        if st != 0:
+            raise ValueError(f"reference load failed ({st})")
+        return dt.value.decode(), [shape[i] for i in range(nd.value)], out[:nb.value].tobytes()
 
     def set_num_threads(self, t: int) -> None:
         fn = getattr(self.lib, f"{self.prefix}_set_num_threads", None)

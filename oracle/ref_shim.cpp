@@ -218,3 +218,63 @@ REXPORT int ref_qwen3_generate(const int* cfg_i, const float* cfg_f, const float
     delete lm;
     return 0;
 }
+
+// ---------------------------------------------------------------------------
+// .yt files through the reference's own yt::io::YTensorIO
+// (include/ytensor_io.hpp, src/ytensor_io.inl, src/ytensor_io_templates.inl).
+// ---------------------------------------------------------------------------
+
+// Writes n dense tensors (YTensorIO::open(path, mode) + save(...) + close()),
+// mode 2 = yt::io::Write, 3 = yt::io::Append. shapes holds the dims of every
+// tensor back to back (ndims[i] each); compress is "" or "zlib"
+// (yt::io::compressMethod).
+REXPORT int ref_yt_save(const char* path, int n, const char* const* names, const char* const* dtypes,
+                        const int* ndims, const int* shapes, const void* const* data, const char* compress,
+                        int mode) {
+    yt::io::compressMethod = compress ? compress : "";
+    yt::io::YTensorIO io;
+    if (!io.open(path, mode == 3 ? yt::io::Append : yt::io::Write)) return 1;
+    int so = 0;
+    for (int i = 0; i < n; ++i) {
+        std::vector<int> shape(shapes + so, shapes + so + ndims[i]);
+        so += ndims[i];
+        yt::YTensorBase t(shape, dtypes[i]);
+        const size_t bytes = t.size() * t.elementSize();
+        if (bytes) std::memcpy(t.data(), data[i], bytes);
+        if (!io.save(t, names[i])) return 2;
+    }
+    io.close();
+    yt::io::compressMethod = "";
+    return 0;
+}
+
+// Tensor names of a file, '\n'-separated; returns the count or -1.
+REXPORT int ref_yt_names(const char* path, char* buf, int64_t cap) {
+    yt::io::YTensorIO io;
+    if (!io.open(path, yt::io::Read)) return -1;
+    std::string all;
+    auto names = io.getTensorNames();
+    for (auto& s : names) all += s + "\n";
+    if (static_cast<int64_t>(all.size()) + 1 > cap) return -1;
+    std::memcpy(buf, all.c_str(), all.size() + 1);
+    return static_cast<int>(names.size());
+}
+
+// YTensorIO::load of one tensor ("" = the first): dtype name, shape and the
+// dense bytes. Returns 0, or 1 (open failed), 2 (load returned false), 3 (cap).
+REXPORT int ref_yt_load(const char* path, const char* name, void* out, int64_t cap, int64_t* nbytes,
+                        char* dtype, int dtype_cap, int* ndim, int* shape) {
+    yt::io::YTensorIO io;
+    if (!io.open(path, yt::io::Read)) return 1;
+    yt::YTensorBase t;
+    if (!io.load(t, name ? name : "")) return 2;
+    const int64_t bytes = static_cast<int64_t>(t.size() * t.elementSize());
+    *nbytes = bytes;
+    if (bytes > cap || static_cast<int>(t.dtype().size()) + 1 > dtype_cap) return 3;
+    if (bytes) std::memcpy(out, t.data(), static_cast<size_t>(bytes));
+    std::memcpy(dtype, t.dtype().c_str(), t.dtype().size() + 1);
+    auto sh = t.shape();
+    *ndim = static_cast<int>(sh.size());
+    for (size_t i = 0; i < sh.size() && i < 16; ++i) shape[i] = sh[i];
+    return 0;
+}

@@ -6,6 +6,7 @@ mirror yt::function (see ops.py). Every operator loads the library on first
 use and fails loudly when it has not been built: there is no CPU fallback.
 """
 from ._lib import YthipError, lib, LIB_PATH  # noqa: F401
+from . import io  # noqa: F401  (yt::io: .yt checkpoints to and from device memory)
 from .ops import (  # noqa: F401
     argmax_finish,
     argmax_step,
@@ -31,5 +32,5 @@ def load():
 __all__ = [
     "YthipError", "lib", "gemm", "matmul", "linear", "scaled_dot_product_attention",
     "decode_attention", "rms_norm", "rms_norm_rope", "silu_mul", "embedding", "argmax_step",
-    "gemv_fused", "argmax_finish",
+    "gemv_fused", "argmax_finish", "io",
 ]

@@ -20,6 +20,27 @@ _L = ctypes.c_int64
 _F = ctypes.c_float
 _LP = ctypes.POINTER(ctypes.c_int64)
 
+YT_RAW = -1
+YTHIP_EINVAL, YTHIP_EUNSUPPORTED, YTHIP_EIO, YTHIP_EFORMAT, YTHIP_ENOTFOUND = -1, -2, -3, -4, -5
+
+
+class YtTensorInfo(ctypes.Structure):
+    """struct ythip_yt_tensor_info (include/ythip.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_char_p), ("tensor_type", ctypes.c_char_p),
+                ("compress", ctypes.c_char_p), ("type_size", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("shape", ctypes.POINTER(ctypes.c_int32)), ("data_offset", ctypes.c_uint64),
+                ("compressed_size", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
+class YtTensor(ctypes.Structure):
+    """struct ythip_yt_tensor (include/ythip.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int), ("dtype_name", ctypes.c_char_p),
+                ("type_size", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("shape", ctypes.POINTER(ctypes.c_int32)), ("data", ctypes.c_void_p)]
+
+
+_U64 = ctypes.c_uint64
+
 # Every symbol include/ythip.h declares, with its ctypes signature.
 SIGNATURES = {
     "ythip_abi_version": (_I, []),
@@ -39,6 +60,15 @@ SIGNATURES = {
     "ythip_gemv_fused": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _F, _P, _L, _P, _L, _F, _F, _P, _P]),
     "ythip_argmax_finish": (_I, [_P, _I, _P, _P, _P, _P]),
     "ythip_rope_tables": (_I, [_I, _I, _F, _P, _P]),
+    "ythip_yt_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "ythip_yt_close": (_I, [_P]),
+    "ythip_yt_count": (_I, [_P]),
+    "ythip_yt_metadata": (ctypes.c_char_p, [_P]),
+    "ythip_yt_find": (_I, [_P, ctypes.c_char_p]),
+    "ythip_yt_info": (_I, [_P, _I, ctypes.POINTER(YtTensorInfo)]),
+    "ythip_yt_load": (_I, [_P, _I, _P, _I, _U64, _P]),
+    "ythip_yt_sync": (_I, [_P]),
+    "ythip_yt_save": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(YtTensor), ctypes.c_char_p, _I, _P]),
 }
 
 

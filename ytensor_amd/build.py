@@ -53,7 +53,7 @@ def build(resource: bool = False, verbose: bool = False) -> str:
             print(err, file=sys.stderr)
     objs = [o for o, _ in results]
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lz"]
     subprocess.check_call(cmd)
     os.replace(tmp, LIB)
     return LIB

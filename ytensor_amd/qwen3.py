@@ -8,7 +8,9 @@ then the final norm and the tied LM head, greedy selection.
 
 MI355X layout and execution:
   * weights bf16 in HBM (qkv and gate_up fused as in the example's load(),
-    qwen3.cpp:326-349), norms fp32, embedding bf16 and reused as the LM head;
+    qwen3.cpp:326-349), norms fp32, embedding bf16 and reused as the LM head
+    unless the checkpoint has lm_head.weight; a .yt checkpoint loads straight
+    into this layout (Qwen3.from_yt);
   * residual stream fp32; GEMM inputs bf16; the o/down projections write
     fp32 straight into the residual with beta = 1 (residual add fused into
     the GEMM epilogue); logits fp32;
@@ -39,6 +41,35 @@ class Qwen3Config:
         self.hidden, self.layers, self.vocab, self.inter = hidden, layers, vocab, inter
         self.n_heads, self.n_kv, self.head_dim, self.max_pos = n_heads, n_kv, head_dim, max_pos
         self.eps, self.theta = eps, theta
+
+    @classmethod
+    def from_json(cls, path: str) -> "Qwen3Config":
+        """Qwen3Config::init (example/qwen3/src/qwen3.cpp:128-159): the Hugging
+        Face config.json keys, each falling back to the default when absent."""
+        import json
+        with open(path) as f:
+            j = json.load(f)
+        c = cls()
+        for attr, key in (("hidden", "hidden_size"), ("layers", "num_hidden_layers"), ("vocab", "vocab_size"),
+                          ("eps", "rms_norm_eps"), ("theta", "rope_theta"), ("inter", "intermediate_size"),
+                          ("n_heads", "num_attention_heads"), ("n_kv", "num_key_value_heads"),
+                          ("head_dim", "head_dim"), ("max_pos", "max_position_embeddings")):
+            if key in j:
+                setattr(c, attr, type(getattr(c, attr))(j[key]))
+        return c
+
+
+def hf_names(cfg, i: int | None = None) -> dict:
+    """Checkpoint tensor names that Qwen3Model::load reads
+    (example/qwen3/src/qwen3.cpp:318-358): the model-level ones, or layer i's."""
+    if i is None:
+        return {"embed": "model.embed_tokens.weight", "norm": "model.norm.weight", "lm_head": "lm_head.weight"}
+    p = f"model.layers.{i}."
+    return {"q": p + "self_attn.q_proj.weight", "k": p + "self_attn.k_proj.weight",
+            "v": p + "self_attn.v_proj.weight", "o": p + "self_attn.o_proj.weight",
+            "q_norm": p + "self_attn.q_norm.weight", "k_norm": p + "self_attn.k_norm.weight",
+            "gate": p + "mlp.gate_proj.weight", "up": p + "mlp.up_proj.weight", "down": p + "mlp.down_proj.weight",
+            "norm1": p + "input_layernorm.weight", "norm2": p + "post_attention_layernorm.weight"}
 
 
 def weight_layout(cfg) -> list[tuple[str, tuple[int, ...]]]:
@@ -80,9 +111,13 @@ class Qwen3:
 
     # ---------------------------------------------------------------- weights
     def _upload(self, weights) -> None:
-        """weights: flat fp32 array (numpy or torch) in weight_layout order, or a
-        dict name -> tensor. Matrices become bf16, norms stay fp32."""
+        """weights: flat fp32 array (numpy or torch) in weight_layout order, a
+        dict name -> tensor, or the path of a .yt checkpoint (see _load_yt).
+        Matrices become bf16, norms stay fp32."""
         cfg, dev = self.cfg, self.dev
+        if isinstance(weights, (str, bytes)) or hasattr(weights, "__fspath__"):
+            self._load_yt(weights)
+            return
         lay = weight_layout(cfg)
         if isinstance(weights, dict):
             get = lambda name, shp: torch.as_tensor(weights[name]).reshape(shp)
@@ -111,9 +146,83 @@ class Qwen3:
                 qn=f32(get(f"{i}.q_norm", shp[f"{i}.q_norm"])), kn=f32(get(f"{i}.k_norm", shp[f"{i}.k_norm"])),
                 n1=f32(get(f"{i}.norm1", shp[f"{i}.norm1"])), n2=f32(get(f"{i}.norm2", shp[f"{i}.norm2"]))))
         self.fnorm = f32(get("norm", (cfg.hidden,)))
-        c, s = rope_tables(cfg.head_dim, cfg.max_pos, cfg.theta)
-        self.cos = torch.from_numpy(c).to(dev)
-        self.sin = torch.from_numpy(s).to(dev)
+        self.lm_head = self.embed  # tied (Qwen3ForCausalLM::forward, qwen3.cpp:453-456)
+        self._rope()
+
+    def _rope(self) -> None:
+        c, s = rope_tables(self.cfg.head_dim, self.cfg.max_pos, self.cfg.theta)
+        self.cos = torch.from_numpy(c).to(self.dev)
+        self.sin = torch.from_numpy(s).to(self.dev)
+
+    def _load_yt(self, path) -> None:
+        """Qwen3Model::load + Qwen3ForCausalLM::load (example/qwen3/src/qwen3.cpp:
+        304-363, 424-431) from a .yt checkpoint, straight into the device
+        layout: q/k/v land in the row blocks of the fused qkv weight and
+        gate/up in gate_up (the example's concat, 326-349, without a copy);
+        matrices are stored as bf16 (converted with the reference's cast when
+        the file holds another float type), norms as fp32. lm_head.weight is
+        used when present, else the embedding (tied). Unlike the example, a
+        missing tensor is an error rather than an empty weight."""
+        from . import io as ytio
+        cfg, dev = self.cfg, self.dev
+        H, I, hd, nh, nkv = cfg.hidden, cfg.inter, cfg.head_dim, cfg.n_heads, cfg.n_kv
+        f = ytio.YTensorIO()
+        if not f.open(str(path), ytio.Read):
+            raise FileNotFoundError(f"cannot open {path} as a .yt checkpoint")
+        try:
+            names = set(f.getTensorNames())
+            bf, fp = torch.bfloat16, torch.float32
+            top = hf_names(cfg)
+            need = [top["embed"], top["norm"]] + [n for i in range(cfg.layers) for n in hf_names(cfg, i).values()]
+            missing = [n for n in need if n not in names]
+            if missing:
+                raise KeyError(f"{path}: {len(missing)} tensors missing, first {missing[:3]}")
+            plan = []
+            self.embed = torch.empty((cfg.vocab, H), dtype=bf, device=dev)
+            plan.append((top["embed"], self.embed))
+            self.layers = []
+            for i in range(cfg.layers):
+                n = hf_names(cfg, i)
+                L = dict(qkv=torch.empty(((nh + 2 * nkv) * hd, H), dtype=bf, device=dev),
+                         o=torch.empty((H, nh * hd), dtype=bf, device=dev),
+                         gu=torch.empty((2 * I, H), dtype=bf, device=dev),
+                         down=torch.empty((H, I), dtype=bf, device=dev),
+                         qn=torch.empty((hd,), dtype=fp, device=dev), kn=torch.empty((hd,), dtype=fp, device=dev),
+                         n1=torch.empty((H,), dtype=fp, device=dev), n2=torch.empty((H,), dtype=fp, device=dev))
+                plan += [(n["q"], L["qkv"][:nh * hd]), (n["k"], L["qkv"][nh * hd:(nh + nkv) * hd]),
+                         (n["v"], L["qkv"][(nh + nkv) * hd:]), (n["o"], L["o"]),
+                         (n["gate"], L["gu"][:I]), (n["up"], L["gu"][I:]), (n["down"], L["down"]),
+                         (n["q_norm"], L["qn"]), (n["k_norm"], L["kn"]),
+                         (n["norm1"], L["n1"]), (n["norm2"], L["n2"])]
+                self.layers.append(L)
+            self.fnorm = torch.empty((H,), dtype=fp, device=dev)
+            plan.append((top["norm"], self.fnorm))
+            if top["lm_head"] in names:
+                self.lm_head = torch.empty((cfg.vocab, H), dtype=bf, device=dev)
+                plan.append((top["lm_head"], self.lm_head))
+            else:
+                self.lm_head = self.embed
+            for name, dst in plan:
+                shp = f.getTensorInfo(name).shape
+                if int(np.prod(shp)) != dst.numel() or (len(shp) == 2 and tuple(shp) != tuple(dst.shape)):
+                    raise ValueError(f"{path}: '{name}' has shape {shp}, the model expects {tuple(dst.shape)}")
+            f.load_many(plan)
+        finally:
+            f.close()
+        self._rope()
+
+    @classmethod
+    def from_yt(cls, model_dir_or_file: str, cfg: Qwen3Config | None = None, **kw) -> "Qwen3":
+        """Qwen3ForCausalLM::init + load: `cfg` from `<dir>/config.json` when a
+        directory is given (Qwen3Config::init) and the weights from
+        `<dir>/model.yt`, or from the given .yt file with `cfg` (default shape)."""
+        import os
+        path = model_dir_or_file
+        if os.path.isdir(path):
+            if cfg is None and os.path.exists(os.path.join(path, "config.json")):
+                cfg = Qwen3Config.from_json(os.path.join(path, "config.json"))
+            path = os.path.join(path, "model.yt")
+        return cls(cfg or Qwen3Config(), path, **kw)
 
     def _alloc(self) -> None:
         cfg, dev, P = self.cfg, self.dev, self.max_prompt
@@ -191,12 +300,12 @@ class Qwen3:
     def _head(self, S: int) -> None:
         if S == 1 and self.fused:
             # final norm + tied LM head + per-tile argmax in one launch, then the pick
-            ops.gemv_fused(self.x[:1], self.embed, self.logits, "rmsnorm", self.fnorm, self.cfg.eps,
+            ops.gemv_fused(self.x[:1], self.lm_head, self.logits, "rmsnorm", self.fnorm, self.cfg.eps,
                            argmax_parts=self.amax)
             ops.argmax_finish(self.amax, self.amax.numel() // 2, self.token, self.history, self.state)
             return
         ops.rms_norm(self.x[S - 1:S], self.fnorm, self.cfg.eps, out=self.hf)
-        ops.gemm(self.hf, self.embed.t(), self.logits)             # tied LM head, fp32 logits
+        ops.gemm(self.hf, self.lm_head.t(), self.logits)           # LM head (tied by default), fp32 logits
         ops.argmax_step(self.logits, self.token, self.history, self.state)
 
     def prefill(self, prompt) -> None:
