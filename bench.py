@@ -14,6 +14,7 @@ the kernels are launched on):
   attn_decode     configs[3] decode attention (GB/s of K/V read)
   rmsnorm_rope    fused RMSNorm+RoPE on configs[2] shapes at S=8192 (GB/s)
   qwen3_0p6b      configs[4] shape: 512-token prefill + greedy decode tok/s
+  yt_checkpoint   .yt checkpoint of the Qwen3-0.6B shape loaded to the device (GB/s)
   roofline        the headline kernel against MI355X dense bf16 MFMA peak
   cpu_baseline    YTensor's own CPU sgemm (compiled reference when present,
                   else the oracle restatement) on the host cores, same shape;
@@ -64,7 +65,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only (no sweep, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list of sections to run "
-                                               "(gemm,sweep,fp32,prefill,decode,norm,qwen3)")
+                                               "(gemm,sweep,fp32,prefill,decode,norm,qwen3,ytload)")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain conversion-copy kernel of known size (HBM counter calibration)")
     return ap.parse_args()
@@ -189,6 +190,7 @@ def cpu_rows(path, kind: str) -> dict:
       decode    the same with one query row per batch entry, B=16, ctx=8192
       norm_rope rmsNorm_ of the q and k heads + RoPE of both, S=8192
                 (src/function/normalization.inl:256-277, example/qwen3/qwen3.cpp:101-133)
+      yt_load   YTensorIO::load of a 256 MiB bf16 tensor (src/ytensor_io.inl:785-830)
     Inputs are N(0,1) (weights N(0,0.02)) rounded to bf16, as on the GPU."""
     import numpy as np
     import oracle
@@ -232,6 +234,21 @@ def cpu_rows(path, kind: str) -> dict:
     byts = 2.0 * 32 * 128 * S * 2 + 2.0 * S * 128 * 4
     rows["rmsnorm_rope_S8192"] = {"s_per_call": round(t, 4), "gbs_bf16_equiv": round(byts / t / 1e9, 3)}
     del qk
+    if kind == "reference":
+        # yt::io::YTensorIO::load of one 256 MiB bf16 tensor from a page-cache file
+        import shutil
+        import tempfile
+        from oracle import ytio
+        tmp = tempfile.mkdtemp(prefix="ythip_cpu_")
+        try:
+            p = os.path.join(tmp, "w.yt")
+            w = np.arange(128 << 20, dtype=np.uint16)
+            ytio.write(p, {"w": w}, types={"w": "bfloat16"})
+            path.yt_load(p, "w", cap=w.nbytes)
+            t = med(lambda: path.yt_load(p, "w", cap=w.nbytes), 3)
+            rows["yt_load_256MiB_bf16"] = {"s_per_call": round(t, 4), "gbs": round(w.nbytes / t / 1e9, 3)}
+        finally:
+            shutil.rmtree(tmp, ignore_errors=True)
     return rows
 
 
@@ -282,6 +299,77 @@ def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256) -> dict:
             "distinct_tokens": int(len(set(toks.tolist()))),
             "note": "batch 1, greedy, decode step = one HIP graph replay of 200 kernels "
                     "(7 per layer: RMSNorm and SwiGLU fused into the GEMV prologues)"}
+
+
+def bench_yt_load(torch, dev, reps: int = 3) -> dict:
+    """.yt checkpoint to device: a Qwen3-0.6B-shaped checkpoint (the example's
+    tensor names, bf16 matrices, fp32 norms, random device weights) written by
+    ythip_yt_save to a temporary file, then loaded back into preallocated
+    device buffers (ythip_yt_load through YTensorIO.load_many, one wait at the
+    end) with the file in the page cache. GB/s of payload bytes; beside it a
+    pinned host-to-device copy of 256 MiB, the PCIe ceiling the loader feeds."""
+    import shutil
+    import tempfile
+    import numpy as np
+    from ytensor_amd import io as yio
+    from ytensor_amd.qwen3 import Qwen3Config, hf_names
+    cfg = Qwen3Config()
+    H, I, hd, nh, nkv = cfg.hidden, cfg.inter, cfg.head_dim, cfg.n_heads, cfg.n_kv
+    shapes = {hf_names(cfg)["embed"]: (cfg.vocab, H), hf_names(cfg)["norm"]: (H,)}
+    for i in range(cfg.layers):
+        n = hf_names(cfg, i)
+        shapes.update({n["q"]: (nh * hd, H), n["k"]: (nkv * hd, H), n["v"]: (nkv * hd, H), n["o"]: (H, nh * hd),
+                       n["q_norm"]: (hd,), n["k_norm"]: (hd,), n["gate"]: (I, H), n["up"]: (I, H),
+                       n["down"]: (H, I), n["norm1"]: (H,), n["norm2"]: (H,)})
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    src = {k: (torch.randn(s, device=dev, generator=g) * 0.02).to(torch.float32 if len(s) == 1 else torch.bfloat16)
+           for k, s in shapes.items()}
+    payload = sum(t.numel() * t.element_size() for t in src.values())
+    tmp = tempfile.mkdtemp(prefix="ythip_bench_")
+    path = os.path.join(tmp, "model.yt")
+    try:
+        f = yio.YTensorIO()
+        t0 = time.perf_counter()
+        f.open(path, yio.Write)
+        for k, t in src.items():
+            f.save(t, k)
+        if not f.close():
+            return {"error": "writing the checkpoint failed"}
+        t_write = time.perf_counter() - t0
+        dst = [(k, torch.empty_like(t)) for k, t in src.items()]
+        f = yio.YTensorIO()
+        f.open(path, yio.Read)
+        f.load_many(dst)  # warm: page cache, pinned staging
+        times = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            f.load_many(dst)
+            times.append(time.perf_counter() - t0)
+        f.close()
+        ok = all(torch.equal(src[k], d) for k, d in dst)
+        best = min(times)
+        # PCIe ceiling: one pinned 256 MiB host buffer copied to the device
+        h = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+        dd = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        dd.copy_(h, non_blocking=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(4):
+            dd.copy_(h, non_blocking=True)
+        e.record()
+        torch.cuda.synchronize()
+        h2d = 4 * (256 << 20) / (s.elapsed_time(e) * 1e-3) / 1e9
+        return {"payload_bytes": payload, "file_bytes": os.path.getsize(path), "tensors": len(src),
+                "load_s": round(best, 4), "load_gbs": round(payload / best / 1e9, 2),
+                "load_s_all": [round(t, 4) for t in times], "write_s": round(t_write, 3),
+                "pinned_h2d_gbs": round(h2d, 2), "frac_of_pinned_h2d": round(payload / best / 1e9 / h2d, 3),
+                "bit_exact": bool(ok),
+                "note": "page-cache resident file; bf16 stored = bf16 on device (no conversion)"}
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
 
 
 def main() -> int:
@@ -432,6 +520,13 @@ def main() -> int:
 
     if want("qwen3") and not args.quick:
         sections["qwen3_0p6b_decode"] = bench_qwen3(torch, dev)
+
+    if want("ytload") and not args.quick:
+        try:
+            sections["yt_checkpoint_load"] = bench_yt_load(torch, dev)
+        except Exception as exc:  # reported, never required
+            sections["yt_checkpoint_load"] = {"error": repr(exc)}
+        torch.cuda.empty_cache()
 
     # ---- the timed headline region: exactly K steps, synchronised both sides ----
     for _ in range(args.warmup):

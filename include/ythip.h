@@ -265,6 +265,14 @@ int ythip_yt_info(const ythip_yt_file* f, int index, ythip_yt_tensor_info* info)
  * type_size * prod(shape) is rejected (YTHIP_EFORMAT).
  */
 int ythip_yt_load(ythip_yt_file* f, int index, void* dst, int dtype, uint64_t dst_bytes, void* stream);
+/*
+ * The same for n tensors at once (a whole checkpoint): index[i] into dst[i]
+ * as dtype[i] with dst_bytes[i] available. Every argument is checked before
+ * anything is queued. Tensors copied unchanged are read in file order in
+ * spans of many neighbouring payloads per staging buffer.
+ */
+int ythip_yt_load_many(ythip_yt_file* f, int n, const int* index, void* const* dst, const int* dtype,
+                       const uint64_t* dst_bytes, void* stream);
 /* Waits until every copy queued by this handle has completed. */
 int ythip_yt_sync(ythip_yt_file* f);
 

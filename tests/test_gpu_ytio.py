@@ -238,6 +238,13 @@ def test_qwen3_from_yt_equals_flat_upload(tmp_path):
     tb = b.generate(prompt, 12)
     assert np.array_equal(ta, tb)
     assert torch.equal(la, b.logits)
+    # the same weights stored as float32 (narrowed to bf16 on the way, exactly: they are bf16 values)
+    arrays32 = {k: (orc.bf16_to_f32(v) if k in types else v) for k, v in arrays.items()}
+    d32 = tmp_path / "model32.yt"
+    ytio.write(str(d32), arrays32)
+    b32 = Qwen3.from_yt(str(d32), cfg, max_ctx=128, max_prompt=32)
+    assert all(torch.equal(b32.layers[i][k], b.layers[i][k]) for i in range(cfg.layers) for k in b.layers[i])
+    assert torch.equal(b32.embed, b.embed)
     # an explicit LM head (here: the embedding reversed) is used instead of the tied one
     arrays[top["lm_head"]] = arrays[top["embed"]][::-1].copy()
     types[top["lm_head"]] = "bfloat16"

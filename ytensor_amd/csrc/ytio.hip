@@ -29,8 +29,13 @@
 #include <zlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <condition_variable>
 #include <cstring>
+#include <functional>
+#include <memory>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -42,7 +47,7 @@ namespace {
 
 constexpr char kMagic[8] = {'Y', 'T', 'E', 'N', 'S', 'O', 'R', 'F'};  // include/ytensor_infos.hpp:119
 constexpr uint8_t kVersion = 0;                                         // include/ytensor_infos.hpp:122
-constexpr size_t kChunk = 16u << 20;                                    // staging buffer bytes
+constexpr size_t kChunk = 64u << 20;                                    // staging buffer bytes
 constexpr int kMaxDims = 64;
 
 // ---------------------------------------------------------------- type rules
@@ -166,21 +171,89 @@ void convert(Src s, int dtype, const unsigned char* src, unsigned char* dst, siz
     }
 }
 
-// Conversion of a large chunk split over a few host threads.
+// A process-wide pool of host workers for the page-cache reads and the type
+// conversions (created on first use, never torn down: its threads sleep on a
+// condition variable and end with the process). run(n, fn) calls fn(i) exactly
+// once for each i in [0, n), on the workers and the calling thread, and
+// returns when every call has returned; concurrent callers take turns. Each
+// run has its own index counter, so a worker that wakes late only finds that
+// run's counter exhausted and never touches a later run.
+class Pool {
+   public:
+    static Pool& get() {
+        static Pool* p = new Pool(static_cast<int>(std::min(8u, std::max(1u, std::thread::hardware_concurrency()))));
+        return *p;
+    }
+    int size() const { return nthreads_ + 1; }
+    void run(int n, const std::function<void(int)>& fn) {
+        std::lock_guard<std::mutex> serial(run_m_);
+        auto job = std::make_shared<Job>();
+        job->fn = &fn;
+        job->n = n;
+        job->pending.store(n);
+        {
+            std::lock_guard<std::mutex> lk(m_);
+            job_ = job;
+            ++gen_;
+        }
+        cv_.notify_all();
+        work(*job);
+        std::unique_lock<std::mutex> lk(m_);
+        done_cv_.wait(lk, [&] { return job->pending.load() == 0; });
+    }
+
+   private:
+    struct Job {
+        const std::function<void(int)>* fn = nullptr;
+        int n = 0;
+        std::atomic<int> next{0}, pending{0};
+    };
+    explicit Pool(int n) : nthreads_(n) {
+        for (int i = 0; i < n; ++i) std::thread([this] { loop(); }).detach();
+    }
+    void work(Job& j) {
+        for (;;) {
+            const int i = j.next.fetch_add(1);
+            if (i >= j.n) break;
+            (*j.fn)(i);
+            if (j.pending.fetch_sub(1) == 1) {
+                std::lock_guard<std::mutex> lk(m_);
+                done_cv_.notify_all();
+            }
+        }
+    }
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            std::shared_ptr<Job> j;
+            {
+                std::unique_lock<std::mutex> lk(m_);
+                cv_.wait(lk, [&] { return gen_ != seen; });
+                seen = gen_;
+                j = job_;
+            }
+            work(*j);
+        }
+    }
+    const int nthreads_;
+    std::mutex run_m_, m_;
+    std::condition_variable cv_, done_cv_;
+    uint64_t gen_ = 0;
+    std::shared_ptr<Job> job_;
+};
+
+// Conversion of a large chunk split over the pool.
 void convert_parallel(Src s, int dtype, const unsigned char* src, unsigned char* dst, size_t n) {
     const int ss = s == SRC_F64 ? 8 : (s == SRC_BF16 || s == SRC_F16) ? 2 : 4;
     const int ds = dst_size(dtype);
-    const size_t per = 1u << 20;
-    const int nt = static_cast<int>(std::min<size_t>(8, (n + per - 1) / per));
-    if (nt <= 1) return convert(s, dtype, src, dst, n);
-    std::vector<std::thread> th;
-    const size_t step = (n + nt - 1) / nt;
-    for (int t = 0; t < nt; ++t) {
+    const size_t per = 1u << 19;
+    const int parts = static_cast<int>(std::min<size_t>(Pool::get().size(), (n + per - 1) / per));
+    if (parts <= 1) return convert(s, dtype, src, dst, n);
+    const size_t step = (n + parts - 1) / parts;
+    Pool::get().run(parts, [&](int t) {
         const size_t b = t * step, e = std::min(n, b + step);
-        if (b >= e) break;
-        th.emplace_back(convert, s, dtype, src + b * ss, dst + b * ds, e - b);
-    }
-    for (auto& x : th) x.join();
+        if (b < e) convert(s, dtype, src + b * ss, dst + b * ds, e - b);
+    });
 }
 
 // ---------------------------------------------------------------- file I/O
@@ -196,22 +269,19 @@ bool pread_all(int fd, void* buf, size_t n, uint64_t off) {
     return true;
 }
 
-// Large reads split over a few threads (page-cache copies are per-core bound).
+// Large reads split over the pool (page-cache copies are per-core bound).
 bool pread_parallel(int fd, void* buf, size_t n, uint64_t off) {
-    const size_t per = 4u << 20;
-    const int nt = static_cast<int>(std::min<size_t>(4, (n + per - 1) / per));
-    if (nt <= 1) return pread_all(fd, buf, n, off);
-    std::vector<std::thread> th;
-    std::vector<char> ok(nt, 0);
-    const size_t step = ((n + nt - 1) / nt + 4095) & ~size_t(4095);
-    for (int t = 0; t < nt; ++t) {
+    const size_t per = 2u << 20;
+    const int parts = static_cast<int>(std::min<size_t>(Pool::get().size(), (n + per - 1) / per));
+    if (parts <= 1) return pread_all(fd, buf, n, off);
+    const size_t step = ((n + parts - 1) / parts + 4095) & ~size_t(4095);
+    std::atomic<int> bad{0};
+    Pool::get().run(parts, [&](int t) {
         const size_t b = t * step;
-        if (b >= n) { ok[t] = 1; continue; }
-        const size_t len = std::min(n - b, step);
-        th.emplace_back([&, t, b, len] { ok[t] = pread_all(fd, static_cast<unsigned char*>(buf) + b, len, off + b); });
-    }
-    for (auto& x : th) x.join();
-    return std::all_of(ok.begin(), ok.end(), [](char c) { return c != 0; });
+        if (b >= n) return;
+        if (!pread_all(fd, static_cast<unsigned char*>(buf) + b, std::min(n - b, step), off + b)) bad.store(1);
+    });
+    return bad.load() == 0;
 }
 
 bool write_all(int fd, const void* buf, size_t n) {
@@ -268,6 +338,7 @@ struct ythip_yt_file {
     void* pinned[2] = {nullptr, nullptr};
     hipEvent_t ev[2] = {nullptr, nullptr};
     bool pending[2] = {false, false};
+    int next_buf = 0;  // staging buffer for the next chunk (alternates across calls)
     std::vector<unsigned char> host;  // conversion source / compressed input
 };
 
@@ -439,7 +510,7 @@ int load_entry(ythip_yt_file* f, const Entry& e, void* dst, int dtype, hipStream
             return fail(YTHIP_EFORMAT, "ythip_yt_load: tensor '%s': %llu payload bytes for %llu expected",
                         e.name.c_str(), (unsigned long long)e.compressed_size, (unsigned long long)e.nbytes);
         uint64_t off = 0;
-        int b = 0;
+        int& b = f->next_buf;
         while (off < e.nbytes) {
             const size_t bytes = static_cast<size_t>(std::min<uint64_t>(per_chunk * es, e.nbytes - off));
             if (int st = acquire(f, b)) return st;
@@ -458,7 +529,8 @@ int load_entry(ythip_yt_file* f, const Entry& e, void* dst, int dtype, hipStream
     if (inflateInit2(&zs, 15 + 32) != Z_OK) return fail(YTHIP_EIO, "ythip_yt_load: inflateInit2 failed");
     std::vector<unsigned char> in(1u << 20);
     uint64_t in_off = 0, produced = 0;
-    int b = 0, zr = Z_OK, st = 0;
+    int& b = f->next_buf;
+    int zr = Z_OK, st = 0;
     while (produced < e.nbytes && st == 0) {
         if ((st = acquire(f, b))) break;
         unsigned char* buf = direct ? static_cast<unsigned char*>(f->pinned[b]) : f->host.data();
@@ -723,8 +795,12 @@ __attribute__((visibility("default"))) int ythip_yt_info(const ythip_yt_file* f,
     return 0;
 }
 
-__attribute__((visibility("default"))) int ythip_yt_load(ythip_yt_file* f, int index, void* dst, int dtype,
-                                                         uint64_t dst_bytes, void* stream) {
+namespace ythip {
+namespace {
+
+// Argument checks shared by the single and the batched load; returns the
+// destination byte count in *need.
+int check_load(const ythip_yt_file* f, int index, const void* dst, int dtype, uint64_t dst_bytes, uint64_t* need) {
     if (!f) return fail(YTHIP_EINVAL, "ythip_yt_load: NULL file");
     if (index < 0 || index >= static_cast<int>(f->entries.size()))
         return fail(YTHIP_EINVAL, "ythip_yt_load: index %d of %zu", index, f->entries.size());
@@ -738,13 +814,91 @@ __attribute__((visibility("default"))) int ythip_yt_load(ythip_yt_file* f, int i
     if (dtype != YTHIP_YT_RAW && s == SRC_OTHER)
         return fail(YTHIP_EUNSUPPORTED, "ythip_yt_load: tensor '%s' of type %s cannot convert to %s", e.name.c_str(),
                     e.dtype.c_str(), dtype_name(dtype));
-    const uint64_t need = dtype == YTHIP_YT_RAW ? e.nbytes : e.nbytes / e.type_size * dst_size(dtype);
-    if (dst_bytes < need)
+    *need = dtype == YTHIP_YT_RAW ? e.nbytes : e.nbytes / e.type_size * dst_size(dtype);
+    if (dst_bytes < *need)
         return fail(YTHIP_EINVAL, "ythip_yt_load: tensor '%s' needs %llu bytes, destination has %llu", e.name.c_str(),
-                    (unsigned long long)need, (unsigned long long)dst_bytes);
+                    (unsigned long long)*need, (unsigned long long)dst_bytes);
+    if (*need && !dst) return fail(YTHIP_EINVAL, "ythip_yt_load: NULL destination");
+    return 0;
+}
+
+// A tensor whose stored bytes go to the device unchanged and whole.
+bool is_verbatim(const Entry& e, int dtype) {
+    return e.compress != "zlib" && e.compressed_size == e.nbytes && e.nbytes > 0 && e.nbytes <= kChunk &&
+           (dtype == YTHIP_YT_RAW || same_type(src_kind(e.dtype, e.type_size), dtype));
+}
+
+}  // namespace
+}  // namespace ythip
+
+__attribute__((visibility("default"))) int ythip_yt_load(ythip_yt_file* f, int index, void* dst, int dtype,
+                                                         uint64_t dst_bytes, void* stream) {
+    uint64_t need = 0;
+    if (int st = check_load(f, index, dst, dtype, dst_bytes, &need)) return st;
     if (need == 0) return 0;
-    if (!dst) return fail(YTHIP_EINVAL, "ythip_yt_load: NULL destination");
-    return load_entry(f, e, dst, dtype == YTHIP_YT_RAW ? -1 : dtype, static_cast<hipStream_t>(stream));
+    return load_entry(f, f->entries[static_cast<size_t>(index)], dst, dtype == YTHIP_YT_RAW ? -1 : dtype,
+                      static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int ythip_yt_load_many(ythip_yt_file* f, int n, const int* index,
+                                                              void* const* dst, const int* dtype,
+                                                              const uint64_t* dst_bytes, void* stream) {
+    if (!f || n < 0 || (n > 0 && (!index || !dst || !dtype || !dst_bytes)))
+        return fail(YTHIP_EINVAL, "ythip_yt_load_many: bad arguments");
+    for (int i = 0; i < n; ++i) {  // everything is checked before anything is queued
+        uint64_t need = 0;
+        if (int st = check_load(f, index[i], dst[i], dtype[i], dst_bytes[i], &need)) return st;
+    }
+    const hipStream_t hs = static_cast<hipStream_t>(stream);
+    // Verbatim tensors in file order are read in spans of up to one staging
+    // buffer (one parallel read covers many neighbouring payloads and the
+    // small record headers between them) and copied out of the buffer one
+    // tensor at a time; the rest go through the per-tensor path.
+    std::vector<int> order;
+    for (int i = 0; i < n; ++i)
+        if (f->entries[static_cast<size_t>(index[i])].nbytes > 0) order.push_back(i);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+        return f->entries[static_cast<size_t>(index[a])].data_offset <
+               f->entries[static_cast<size_t>(index[b])].data_offset;
+    });
+    if (int st = ensure_staging(f)) return st;
+    size_t k = 0;
+    while (k < order.size()) {
+        const Entry& e0 = f->entries[static_cast<size_t>(index[order[k]])];
+        if (!is_verbatim(e0, dtype[order[k]])) {
+            const int i = order[k++];
+            if (int st = load_entry(f, e0, dst[i], dtype[i] == YTHIP_YT_RAW ? -1 : dtype[i], hs)) return st;
+            continue;
+        }
+        const uint64_t begin = e0.data_offset;
+        size_t k1 = k + 1;
+        uint64_t end = e0.data_offset + e0.nbytes;
+        while (k1 < order.size()) {
+            const Entry& e = f->entries[static_cast<size_t>(index[order[k1]])];
+            if (!is_verbatim(e, dtype[order[k1]]) || e.data_offset < end ||
+                e.data_offset + e.nbytes - begin > kChunk)
+                break;
+            end = e.data_offset + e.nbytes;
+            ++k1;
+        }
+        int& b = f->next_buf;
+        if (int st = acquire(f, b)) return st;
+        unsigned char* buf = static_cast<unsigned char*>(f->pinned[b]);
+        if (!pread_parallel(f->fd, buf, static_cast<size_t>(end - begin), begin))
+            return fail(YTHIP_EIO, "ythip_yt_load_many: read failed at offset %llu", (unsigned long long)begin);
+        for (size_t j = k; j < k1; ++j) {
+            const int i = order[j];
+            const Entry& e = f->entries[static_cast<size_t>(index[i])];
+            hipError_t he = hipMemcpyAsync(dst[i], buf + (e.data_offset - begin), e.nbytes, hipMemcpyHostToDevice, hs);
+            if (he != hipSuccess) return status_of(he);
+        }
+        hipError_t he = hipEventRecord(f->ev[b], hs);
+        if (he != hipSuccess) return status_of(he);
+        f->pending[b] = true;
+        b ^= 1;
+        k = k1;
+    }
+    return 0;
 }
 
 __attribute__((visibility("default"))) int ythip_yt_sync(ythip_yt_file* f) {

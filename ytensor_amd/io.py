@@ -253,13 +253,27 @@ class YTensorIO:
         return out
 
     def load_many(self, items) -> None:
-        """Loads several tensors into given device views with one final wait:
-        items = [(name, out_tensor), ...]; every out must be contiguous and of
-        the stored size, its dtype picks the conversion (stored type = copy).
-        Raises RuntimeError naming the first tensor that fails."""
+        """Loads several tensors into given device views with one C call and
+        one final wait: items = [(name, out_tensor), ...]; every out must be
+        contiguous and of the stored size, its dtype picks the conversion
+        (the stored type = bytes copied unchanged). Raises RuntimeError naming
+        the problem; nothing is queued unless every item is valid."""
         lib = _lib.lib()
-        for name, out in items:
-            info = self.getTensorInfo(name)
+        if self._h is None:
+            raise RuntimeError("load_many: no file open for reading")
+        pos: dict = {}
+        for k, i in enumerate(self._disk):
+            pos.setdefault(i.name, k)  # the first of a repeated name, as ythip_yt_find
+        n = len(items)
+        idx = (ctypes.c_int * max(1, n))()
+        dsts = (ctypes.c_void_p * max(1, n))()
+        codes = (ctypes.c_int * max(1, n))()
+        sizes = (ctypes.c_uint64 * max(1, n))()
+        dev = None
+        for j, (name, out) in enumerate(items):
+            if name not in pos:
+                raise RuntimeError(f"load_many: tensor not found: {name}")
+            info = self._disk[pos[name]]
             if _TORCH.get(info.typeName) == out.dtype:
                 code = _lib.YT_RAW
             elif out.dtype in _CODE:
@@ -268,13 +282,20 @@ class YTensorIO:
                 raise RuntimeError(f"load_many: '{name}' is {info.typeName}; no conversion to {out.dtype}")
             if not (out.is_cuda and out.is_contiguous() and out.numel() == _numel(info.shape)):
                 raise RuntimeError(f"load_many: '{name}' has shape {info.shape}, the destination {tuple(out.shape)}")
-            idx = lib.ythip_yt_find(self._h, name.encode())
-            with torch.cuda.device(out.device):
-                st = lib.ythip_yt_load(self._h, idx, out.data_ptr() if out.numel() else None, code,
-                                       out.numel() * out.element_size(), torch.cuda.current_stream().cuda_stream)
+            if dev is None:
+                dev = out.device
+            elif out.device != dev:
+                raise RuntimeError("load_many: all destinations must be on one device")
+            idx[j], codes[j] = pos[name], code
+            dsts[j] = out.data_ptr() if out.numel() else None
+            sizes[j] = out.numel() * out.element_size()
+        if n == 0:
+            return
+        with torch.cuda.device(dev):
+            st = lib.ythip_yt_load_many(self._h, n, idx, dsts, codes, sizes, torch.cuda.current_stream().cuda_stream)
             if st != 0:
-                raise RuntimeError(f"loading '{name}' failed ({st}): {lib.ythip_last_error().decode()}")
-        _lib.check(lib.ythip_yt_sync(self._h), "ythip_yt_sync")
+                raise RuntimeError(f"ythip_yt_load_many failed ({st}): {lib.ythip_last_error().decode()}")
+            _lib.check(lib.ythip_yt_sync(self._h), "ythip_yt_sync")
 
 
 def _numel(shape) -> int:
