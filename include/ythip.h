@@ -46,8 +46,14 @@ enum ythip_mask_kind {
     YTHIP_MASK_NONE = 0,   /* every key visible */
     YTHIP_MASK_CAUSAL = 1, /* key j visible to query i iff j <= (kv_len - q_len) + i
                               (example/qwen3/src/qwen3.cpp:46-55) */
-    YTHIP_MASK_BOOL = 2    /* byte mask [q_len, mask_ld]; nonzero = visible
+    YTHIP_MASK_BOOL = 2,   /* byte mask [q_len, mask_ld]; nonzero = visible
                               (include/kernel/avx2/flash_attention.hpp:21-44 `const bool* mask`) */
+    YTHIP_MASK_DIAG = 3    /* predicate: key j visible to query i iff j <= i + mask_ld (the offset
+                              travels in mask_ld, mask is NULL) -- the predicate-functor masks of
+                              scaledDotProductAttention / masked_matmul (src/function/ops.inl:449-503,
+                              src/ytensor_math.inl:372-410), e.g. [](int i, int j){ return j <= i; }
+                              (doc/en/api/function/fused.mdx:200) with offset 0. Other predicates
+                              are evaluated into a bool mask by the caller. */
 };
 
 /* ABI version of this header; bumped on any signature change. */
@@ -95,6 +101,45 @@ int ythip_attn_prefill(int dtype, int B, int Hq, int Hkv, int q_len, int kv_len,
                        void* O, const int64_t o_str[4],
                        float scale, int mask_kind, const uint8_t* mask, int64_t mask_ld,
                        const float* bias, int64_t rs_bias, int64_t cs_bias, void* stream);
+
+/*
+ * Attention forward with the MATH backend (scaledDotProductAttention with
+ * sdpaBackend::MATH, src/function/ops.inl:388-418, 474-490): the score matrix is
+ * materialised,
+ *   S = masked_matmul(Q, K^T, mask, -1e9) * scale + bias,  P = softmax_(S, -1),
+ *   O = P . V,  rows with no visible key -> 0 (ops.inl:18-40),
+ * with S in fp32 and P in the input type (the reference's score tensor has the
+ * input type). Same tensor and mask arguments as ythip_attn_prefill, except that
+ * every stride may be any value (transposed K / V included). workspace: device
+ * scratch of ythip_attn_math_workspace_size(dtype, B, Hq, q_len, kv_len) bytes.
+ */
+size_t ythip_attn_math_workspace_size(int dtype, int B, int Hq, int q_len, int kv_len);
+int ythip_attn_math(int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv,
+                    const void* Q, const int64_t q_str[4],
+                    const void* K, const int64_t k_str[4],
+                    const void* V, const int64_t v_str[4],
+                    void* O, const int64_t o_str[4],
+                    float scale, int mask_kind, const uint8_t* mask, int64_t mask_ld,
+                    const float* bias, int64_t rs_bias, int64_t cs_bias,
+                    void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Masked GEMM (yt::kernel::avx2::sgemm_masked, src/kernel/avx2/sgemm.inl:342-584;
+ * YTensor::masked_matmul, src/ytensor_math.inl:318-410): operands as ythip_gemm;
+ * for every batch entry, where the [m, n] mask is set
+ *   C = alpha * A.B + beta * C   (k == 0 or alpha == 0: C *= beta, 0 for beta == 0)
+ * and elsewhere C is left unchanged, or set to masked_value when fill_masked != 0
+ * (masked_matmul's fill). mask_kind / mask / mask_ld as for attention, with the
+ * causal offset n - m. workspace: ythip_gemm_masked_workspace_size(batch, m, n)
+ * bytes of device scratch (the fp32 product).
+ */
+size_t ythip_gemm_masked_workspace_size(int batch, int m, int n);
+int ythip_gemm_masked(int dtype_in, int dtype_out, int batch, int m, int n, int k,
+                      const void* A, int64_t sa_b, int64_t rsa, int64_t csa,
+                      const void* B, int64_t sb_b, int64_t rsb, int64_t csb,
+                      void* C, int64_t sc_b, int64_t rsc, int64_t csc,
+                      float alpha, float beta, int mask_kind, const uint8_t* mask, int64_t mask_ld,
+                      int fill_masked, float masked_value, void* workspace, size_t ws_bytes, void* stream);
 
 /*
  * Single-query decode attention over a KV cache (the q_len == 1 path,

@@ -54,6 +54,10 @@ def _bind(lib: ctypes.CDLL, prefix: str) -> ctypes.CDLL:
         "rope_precompute": (None, [_I, _I, _F, _P, _P]),
         "rope": (None, [_P, _I, _I, _I, _I, _P, _P]),
         "qwen3_generate": (_I, [_P, _P, _P, _P, _I, _I, _P, _P, _P]),
+        "sgemm_masked": (None, [_P, _P, _P, _I, _I, _I, _F, _F, _L, _L, _L, _L, _L, _L, _P]),
+        "sdpa_math": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _I]),
+        "sdpa_ex": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _I, _I]),
+        "masked_matmul": (None, [_P, _P, _P, _I, _I, _I, _P, _I, _I, _F]),
         "yt_save": (_I, [ctypes.c_char_p, _I, _P, _P, _P, _P, _P, ctypes.c_char_p, _I]),
         "yt_names": (_I, [ctypes.c_char_p, _P, _L]),
         "yt_load": (_I, [ctypes.c_char_p, ctypes.c_char_p, _P, _L, _P, _P, _I, _P, _P]),
@@ -166,6 +170,65 @@ class CpuPath:
         O = np.zeros_like(Q)
         self._fn("sdpa_gqa")(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), B, Hq, Hkv, S, KV, D, scale, int(causal))
         return O
+
+    # --- masked matmul / MATH SDPA -----------------------------------------------
+    def sgemm_masked(self, A, B, C, mask, alpha=1.0, beta=0.0):
+        """sgemm_masked on contiguous A [m,k], B [k,n]; C [m,n] updated in place
+        where mask [m,n] is set (returned)."""
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        B = np.ascontiguousarray(B, dtype=np.float32)
+        assert C.flags.c_contiguous and C.dtype == np.float32
+        mk = np.ascontiguousarray(mask, dtype=np.uint8)
+        m, k = A.shape
+        n = B.shape[1]
+        self._fn("sgemm_masked")(_ptr(A), _ptr(B), _ptr(C), m, n, k, alpha, beta, k, 1, n, 1, n, 1, _ptr(mk))
+        return C
+
+    def sdpa_math(self, Q, K, V, scale=0.0, mask=None, bias=None, diag=None):
+        """scaledDotProductAttention(MATH) over [H, L, D] fp32 tensors; mask bool
+        [Lq, Lkv], or diag = offset for the predicate j <= i + offset."""
+        return self._sdpa(Q, K, V, scale, mask, bias, diag, 0)
+
+    def sdpa_flash(self, Q, K, V, scale=0.0, mask=None, bias=None, diag=None):
+        """scaledDotProductAttention(FLASH_AVX2) through the tensor API (reference only)."""
+        return self._sdpa(Q, K, V, scale, mask, bias, diag, 1)
+
+    def _sdpa(self, Q, K, V, scale, mask, bias, diag, backend):
+        Q = np.ascontiguousarray(Q, dtype=np.float32)
+        K = np.ascontiguousarray(K, dtype=np.float32)
+        V = np.ascontiguousarray(V, dtype=np.float32)
+        H, Lq, D = Q.shape
+        Lkv, Dv = V.shape[1], V.shape[2]
+        O = np.zeros((H, Lq, Dv), np.float32)
+        mk = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+        bs = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        dg, off = (0, 0) if diag is None else (1, int(diag))
+        if self.prefix == "ref":
+            self._fn("sdpa_ex")(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), H, Lq, Lkv, D, Dv, scale, _ptr(mk), _ptr(bs),
+                                backend, dg, off)
+        else:
+            if backend != 0:
+                raise NotImplementedError("the oracle's FLASH is flash_attention / sdpa_gqa")
+            self._fn("sdpa_math")(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), H, Lq, Lkv, D, Dv, scale, _ptr(mk), _ptr(bs),
+                                  dg, off)
+        return O
+
+    def masked_matmul(self, A, B, mask=None, diag=None, value=0.0):
+        """YTensor::masked_matmul (reference) / fill + sgemm_masked (oracle)."""
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        B = np.ascontiguousarray(B, dtype=np.float32)
+        m, k = A.shape
+        n = B.shape[1]
+        if self.prefix == "ref":
+            O = np.empty((m, n), np.float32)
+            mk = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+            dg, off = (0, 0) if diag is None else (1, int(diag))
+            self._fn("masked_matmul")(_ptr(A), _ptr(B), _ptr(O), m, n, k, _ptr(mk), dg, off, value)
+            return O
+        if diag is not None:
+            mask = np.arange(n)[None, :] <= np.arange(m)[:, None] + int(diag)
+        O = np.full((m, n), value, np.float32)
+        return self.sgemm_masked(A, B, O, mask)
 
     # --- RMSNorm / RoPE ----------------------------------------------------------
     def rms_norm(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:

@@ -278,3 +278,75 @@ REXPORT int ref_yt_load(const char* path, const char* name, void* out, int64_t c
     for (size_t i = 0; i < sh.size() && i < 16; ++i) shape[i] = sh[i];
     return 0;
 }
+
+// ---------------------------------------------------------------------------
+// MATH backend, masked matmul and predicate masks
+// ---------------------------------------------------------------------------
+
+// yt::function::scaledDotProductAttention on fp32 [H, Lq, D] / [H, Lkv, D] /
+// [H, Lkv, Dv] tensors (src/function/ops.inl:368-503): backend 0 = MATH,
+// 1 = FLASH_AVX2; mask = bool bytes [Lq, Lkv] or NULL; diag != 0 passes the
+// predicate functor j <= i + diag_off instead (the doc's
+// [](int i, int j){ return j <= i; } for diag_off = 0); bias [Lq, Lkv] or NULL.
+REXPORT void ref_sdpa_ex(const float* Q, const float* K, const float* V, float* O, int H, int Lq, int Lkv, int D,
+                         int Dv, float scale, const uint8_t* mask, const float* bias, int backend, int diag,
+                         int diag_off) {
+    yt::YTensor<float, 3> q(H, Lq, D), k(H, Lkv, D), v(H, Lkv, Dv);
+    std::memcpy(q.data(), Q, sizeof(float) * q.size());
+    std::memcpy(k.data(), K, sizeof(float) * k.size());
+    std::memcpy(v.data(), V, sizeof(float) * v.size());
+    yt::YTensor<float, 2> bt;
+    yt::YTensor<float, 2>* bp = nullptr;
+    if (bias) {
+        bt = yt::YTensor<float, 2>(Lq, Lkv);
+        std::memcpy(bt.data(), bias, sizeof(float) * bt.size());
+        bp = &bt;
+    }
+    const auto be = backend == 0 ? yt::function::sdpaBackend::MATH : yt::function::sdpaBackend::FLASH_AVX2;
+    yt::YTensor<float, 3> o;
+    if (diag) {
+        auto pred = [diag_off](int i, int j) { return j <= i + diag_off; };
+        o = yt::function::scaledDotProductAttention(q, k, v, scale, pred, bp, be);
+    } else if (mask) {
+        yt::YTensor<bool, 2> m(Lq, Lkv);
+        for (int i = 0; i < Lq; ++i)
+            for (int j = 0; j < Lkv; ++j) m.at(i, j) = mask[static_cast<size_t>(i) * Lkv + j] != 0;
+        o = yt::function::scaledDotProductAttention(q, k, v, scale, &m, bp, be);
+    } else {
+        o = yt::function::scaledDotProductAttention(q, k, v, scale, static_cast<yt::YTensor<bool, 2>*>(nullptr),
+                                                    bp, be);
+    }
+    auto oc = o.contiguous();
+    std::memcpy(O, oc.data(), sizeof(float) * static_cast<size_t>(H) * Lq * Dv);
+}
+
+// yt::kernel::avx2::sgemm_masked with a bool mask [m, n] (src/kernel/avx2/sgemm.inl:342-447).
+REXPORT void ref_sgemm_masked(const float* A, const float* B, float* C, int m, int n, int k, float alpha,
+                              float beta, int64_t rsa, int64_t csa, int64_t rsb, int64_t csb, int64_t rsc,
+                              int64_t csc, const uint8_t* mask) {
+    std::vector<char> mb(static_cast<size_t>(m) * n);
+    for (size_t i = 0; i < mb.size(); ++i) mb[i] = mask[i] ? 1 : 0;
+    yt::kernel::avx2::sgemm_masked(A, B, C, m, n, k, alpha, beta, rsa, csa, rsb, csb, rsc, csc,
+                                   reinterpret_cast<const bool*>(mb.data()));
+}
+
+// YTensor<float,2>::masked_matmul (src/ytensor_math.inl:318-410): A [m,k] . B [k,n]
+// where the bool mask [m,n] (or, diag != 0, the predicate j <= i + diag_off) is
+// true, masked_value elsewhere.
+REXPORT void ref_masked_matmul(const float* A, const float* B, float* O, int m, int n, int k,
+                               const uint8_t* mask, int diag, int diag_off, float masked_value) {
+    yt::YTensor<float, 2> a(m, k), b(k, n);
+    std::memcpy(a.data(), A, sizeof(float) * a.size());
+    std::memcpy(b.data(), B, sizeof(float) * b.size());
+    yt::YTensor<float, 2> o;
+    if (diag) {
+        o = a.masked_matmul(b, [diag_off](int i, int j) { return j <= i + diag_off; }, masked_value);
+    } else {
+        yt::YTensor<bool, 2> mk(m, n);
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j) mk.at(i, j) = mask[static_cast<size_t>(i) * n + j] != 0;
+        o = a.masked_matmul(b, mk, masked_value);
+    }
+    auto oc = o.contiguous();
+    std::memcpy(O, oc.data(), sizeof(float) * static_cast<size_t>(m) * n);
+}

@@ -610,6 +610,96 @@ OEXPORT void oracle_rope(float* x, int B, int H, int L, int D, const float* cosv
     }
 }
 
+// ---------------------------------------------------------------------------
+// Masked matmul and the MATH SDPA backend.
+// ---------------------------------------------------------------------------
+
+// sgemm_masked with a bool mask [m, n] (src/kernel/avx2/sgemm.inl:342-447): where
+// the mask is set, C = alpha * (A.B) + beta * C; elsewhere C is left as it was.
+// k == 0 or alpha == 0 only scales (beta == 0 writes 0) the visible entries
+// (351-363). The visible products are those of sgemm (one FMA chain per
+// element over each k block, as its full tiles compute them); the blend is
+// alpha * dot + beta * c. Positions where the mask is clear are never read.
+OEXPORT void oracle_sgemm_masked(const float* A, const float* B, float* C, int m, int n, int k, float alpha,
+                                 float beta, int64_t rsa, int64_t csa, int64_t rsb, int64_t csb, int64_t rsc,
+                                 int64_t csc, const uint8_t* mask) {
+    if (m == 0 || n == 0) return;
+    if (k == 0 || alpha == 0.0f) {
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j)
+                if (mask[static_cast<size_t>(i) * n + j]) {
+                    float& c = C[i * rsc + j * csc];
+                    if (beta == 0.0f) c = 0.0f;
+                    else if (beta != 1.0f) c *= beta;
+                }
+        return;
+    }
+    std::vector<float> prod(static_cast<size_t>(m) * n);
+    sgemm_full(A, B, prod.data(), m, n, k, 1.0f, 0.0f, rsa, csa, rsb, csb, n, 1);
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j)
+            if (mask[static_cast<size_t>(i) * n + j]) {
+                float& c = C[i * rsc + j * csc];
+                const float p = prod[static_cast<size_t>(i) * n + j];
+                if (alpha == 1.0f && beta == 0.0f) c = p;
+                else c = alpha * p + beta * c;
+            }
+}
+
+// scaledDotProductAttention, MATH backend (src/function/ops.inl:388-418 and,
+// for a predicate, 474-490), one [Lq, D] x [Lkv, D] x [Lkv, Dv] problem per
+// head h of H contiguous heads:
+//   score = masked_matmul(q, k^T, mask, -1e9)   (plain matmul without a mask)
+//   score *= scale; score += bias
+//   softmax_(score, -1): max, exp(x - max), running sum, x /= sum
+//     (src/function/activation.inl:313-329)
+//   out = matmul(score, v); rows whose mask has no visible key -> 0 (18-40)
+// mask: bool bytes [Lq, Lkv] or NULL; diag != 0 uses the predicate
+// j <= i + diag_off instead. bias [Lq, Lkv] or NULL. scale 0 -> 1/sqrt(D).
+OEXPORT void oracle_sdpa_math(const float* Q, const float* K, const float* V, float* O, int H, int Lq, int Lkv,
+                              int D, int Dv, float scale, const uint8_t* mask, const float* bias, int diag,
+                              int diag_off) {
+    if (scale == 0.0f) scale = 1.0f / std::sqrt(static_cast<float>(D));
+    const bool masked = diag != 0 || mask != nullptr;
+    auto visible = [&](int i, int j) -> bool {
+        if (diag) return j <= i + diag_off;
+        return mask == nullptr || mask[static_cast<size_t>(i) * Lkv + j] != 0;
+    };
+    std::vector<float> s(static_cast<size_t>(Lq) * Lkv);
+    for (int h = 0; h < H; ++h) {
+        const float* q = Q + static_cast<size_t>(h) * Lq * D;
+        const float* k = K + static_cast<size_t>(h) * Lkv * D;
+        const float* v = V + static_cast<size_t>(h) * Lkv * Dv;
+        float* o = O + static_cast<size_t>(h) * Lq * Dv;
+        // k^T is the view (p, j) -> k[j * D + p]: rsb = 1, csb = D
+        sgemm_full(q, k, s.data(), Lq, Lkv, D, 1.0f, 0.0f, D, 1, 1, D, Lkv, 1);
+        for (int i = 0; i < Lq; ++i) {
+            float* row = s.data() + static_cast<size_t>(i) * Lkv;
+            for (int j = 0; j < Lkv; ++j) {
+                if (!visible(i, j)) row[j] = -1e9f;
+                row[j] *= scale;
+                if (bias) row[j] += bias[static_cast<size_t>(i) * Lkv + j];
+            }
+            float mx = std::numeric_limits<float>::lowest();
+            for (int j = 0; j < Lkv; ++j) mx = std::max(mx, row[j]);
+            float sum = 0.0f;
+            for (int j = 0; j < Lkv; ++j) {
+                row[j] = std::exp(row[j] - mx);
+                sum += row[j];
+            }
+            for (int j = 0; j < Lkv; ++j) row[j] /= sum;
+        }
+        sgemm_full(s.data(), v, o, Lq, Dv, Lkv, 1.0f, 0.0f, Lkv, 1, Dv, 1, Dv, 1);
+        if (masked)
+            for (int i = 0; i < Lq; ++i) {
+                bool any = false;
+                for (int j = 0; j < Lkv && !any; ++j) any = visible(i, j);
+                if (!any)
+                    for (int d = 0; d < Dv; ++d) o[static_cast<size_t>(i) * Dv + d] = 0.0f;
+            }
+    }
+}
+
 OEXPORT int oracle_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -13,8 +13,10 @@ from .ops import (  # noqa: F401
     decode_attention,
     embedding,
     gemm,
+    gemm_masked,
     gemv_fused,
     linear,
+    masked_matmul,
     matmul,
     rms_norm,
     rms_norm_rope,
@@ -32,5 +34,5 @@ def load():
 __all__ = [
     "YthipError", "lib", "gemm", "matmul", "linear", "scaled_dot_product_attention",
     "decode_attention", "rms_norm", "rms_norm_rope", "silu_mul", "embedding", "argmax_step",
-    "gemv_fused", "argmax_finish", "io",
+    "gemv_fused", "argmax_finish", "io", "masked_matmul", "gemm_masked",
 ]

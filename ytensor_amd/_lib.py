@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libythip.so")
 
 F32, F16, BF16 = 0, 1, 2
-MASK_NONE, MASK_CAUSAL, MASK_BOOL = 0, 1, 2
+MASK_NONE, MASK_CAUSAL, MASK_BOOL, MASK_DIAG = 0, 1, 2, 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -48,6 +48,12 @@ SIGNATURES = {
     "ythip_gemm": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _F, _F, _P]),
     "ythip_attn_prefill": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _LP, _P, _LP, _P, _LP, _P, _LP,
                                 _F, _I, _P, _L, _P, _L, _L, _P]),
+    "ythip_attn_math_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
+    "ythip_attn_math": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _LP, _P, _LP, _P, _LP, _P, _LP,
+                             _F, _I, _P, _L, _P, _L, _L, _P, ctypes.c_size_t, _P]),
+    "ythip_gemm_masked_workspace_size": (ctypes.c_size_t, [_I, _I, _I]),
+    "ythip_gemm_masked": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _F, _F,
+                               _I, _P, _L, _I, _F, _P, ctypes.c_size_t, _P]),
     "ythip_attn_decode_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I]),
     "ythip_attn_decode": (_I, [_I, _I, _I, _I, _I, _I, _P, _LP, _P, _P, _LP, _P, _P, _LP, _F, _P,
                                ctypes.c_size_t, _P]),

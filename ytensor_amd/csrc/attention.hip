@@ -27,6 +27,7 @@
 //   per-lane online softmax, then a cross-slot merge in LDS; a second kernel
 //   merges the splits (log-sum-exp).
 
+#include <algorithm>
 #include <cfloat>
 
 #include "common.hpp"
@@ -42,7 +43,9 @@ struct AttnArgs {
     const void* V;
     void* O;
     int64_t qs0, qs1, qs2, ks0, ks1, ks2, vs0, vs1, vs2, os0, os1, os2;
+    int64_t qs3, ks3, vs3, os3;  // element strides along d (1 on the MFMA path)
     int B, Hq, Hkv, Sq, Skv, D, Dv;
+    int diag_off;  // causal / diagonal masks: key j visible to query i iff j <= i + diag_off
     float scale_log2;  // scale * log2(e)
     const uint8_t* mask;
     int64_t mask_ld;
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         }
     }
 
-    const int off = a.Skv - a.Sq;  // causal: key j visible to query i iff j <= i + off
+    const int off = a.diag_off;  // causal: key j visible to query i iff j <= i + off
     int kv_end = a.Skv;
     if (MODE == 1) kv_end = min(a.Skv, qb * BQ + BQ + off);
     const int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;
@@ -338,7 +341,7 @@ __global__ __launch_bounds__(64) void attn_rowwise(AttnArgs a) {
     const int64_t ko = b * a.ks0 + kvh * a.ks1;
     const int64_t vo = b * a.vs0 + kvh * a.vs1;
     const float scale = a.scale_log2 / LOG2E;
-    const int off = a.Skv - a.Sq;
+    const int off = a.diag_off;
     float mx = -INFINITY;
     for (int j = lane; j < a.Skv; j += 64) {
         bool vis = true;
@@ -348,7 +351,8 @@ __global__ __launch_bounds__(64) void attn_rowwise(AttnArgs a) {
         if (vis) {
             float acc = 0.f;
             for (int d = 0; d < a.D; ++d)
-                acc = fmaf(load_as_f32<T>(a.Q, qo + d), load_as_f32<T>(a.K, ko + (int64_t)j * a.ks2 + d), acc);
+                acc = fmaf(load_as_f32<T>(a.Q, qo + d * a.qs3),
+                           load_as_f32<T>(a.K, ko + (int64_t)j * a.ks2 + d * a.ks3), acc);
             x = acc * scale;
             if (a.bias != nullptr) x += a.bias[(int64_t)qi * a.brs + (int64_t)j * a.bcs];
         }
@@ -372,8 +376,9 @@ __global__ __launch_bounds__(64) void attn_rowwise(AttnArgs a) {
         float acc = 0.f;
         if (sum > 0.f)
             for (int j = 0; j < a.Skv; ++j)
-                if (sc[j] != 0.f) acc = fmaf(sc[j] * inv, load_as_f32<T>(a.V, vo + (int64_t)j * a.vs2 + d), acc);
-        store_from_f32<T>(a.O, oo + d, acc);
+                if (sc[j] != 0.f)
+                    acc = fmaf(sc[j] * inv, load_as_f32<T>(a.V, vo + (int64_t)j * a.vs2 + d * a.vs3), acc);
+        store_from_f32<T>(a.O, oo + d * a.os3, acc);
     }
 }
 
@@ -597,7 +602,9 @@ int prefill_typed(AttnArgs a, hipStream_t s) {
     constexpr int es = sizeof(typename T::raw);
     const bool simple_mask = a.mask == nullptr && a.bias == nullptr;
     const int mode = a.causal ? 1 : (simple_mask ? 0 : 2);
-    const bool mfma_ok = es == 2 && (a.D == 64 || a.D == 128) && a.Dv == a.D && !(a.causal && !simple_mask) &&
+    const bool unit_d = a.qs3 == 1 && a.ks3 == 1 && a.vs3 == 1 && a.os3 == 1;
+    const bool mfma_ok = es == 2 && unit_d && (a.D == 64 || a.D == 128) && a.Dv == a.D &&
+                         !(a.causal && !simple_mask) &&
                          a.scale_log2 > 0.f &&
                          al(a.Q, 16) && al(a.K, 16) && al(a.V, 16) && al(a.O, 8) &&
                          a.qs0 % 8 == 0 && a.qs1 % 8 == 0 && a.qs2 % 8 == 0 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
@@ -672,11 +679,10 @@ __attribute__((visibility("default"))) int ythip_attn_prefill(
     if ((int64_t)B * Hq * q_len == 0 || dv == 0) return 0;
     if (Hkv == 0 || Hq % Hkv != 0) return fail(YTHIP_EINVAL, "ythip_attn_prefill: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
     if (d == 0 || d > 256 || dv > 256) return fail(YTHIP_EUNSUPPORTED, "ythip_attn_prefill: head dims %d/%d (1..256)", d, dv);
-    if (!Q || !K || !V || !O || !q_str || !k_str || !v_str || !o_str)
+    if (!Q || !O || !q_str || !k_str || !v_str || !o_str || (kv_len > 0 && (!K || !V)))
         return fail(YTHIP_EINVAL, "ythip_attn_prefill: NULL tensor or stride array");
-    if (q_str[3] != 1 || k_str[3] != 1 || v_str[3] != 1 || o_str[3] != 1)
-        return fail(YTHIP_EUNSUPPORTED, "ythip_attn_prefill: the last (head-dim) stride must be 1");
-    if (mask_kind < 0 || mask_kind > 2) return fail(YTHIP_EINVAL, "ythip_attn_prefill: mask_kind %d", mask_kind);
+    if (mask_kind < 0 || mask_kind > YTHIP_MASK_DIAG)
+        return fail(YTHIP_EINVAL, "ythip_attn_prefill: mask_kind %d", mask_kind);
     if (mask_kind == YTHIP_MASK_BOOL && (mask == nullptr || mask_ld < kv_len))
         return fail(YTHIP_EINVAL, "ythip_attn_prefill: bool mask needs a pointer and mask_ld >= kv_len");
     if (scale == 0.0f) scale = 1.0f / sqrtf((float)d);  // src/function/ops.inl:378-381
@@ -686,9 +692,15 @@ __attribute__((visibility("default"))) int ythip_attn_prefill(
     a.ks0 = k_str[0]; a.ks1 = k_str[1]; a.ks2 = k_str[2];
     a.vs0 = v_str[0]; a.vs1 = v_str[1]; a.vs2 = v_str[2];
     a.os0 = o_str[0]; a.os1 = o_str[1]; a.os2 = o_str[2];
+    a.qs3 = q_str[3]; a.ks3 = k_str[3]; a.vs3 = v_str[3]; a.os3 = o_str[3];
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.Sq = q_len; a.Skv = kv_len; a.D = d; a.Dv = dv;
     a.scale_log2 = scale * LOG2E;
-    a.causal = mask_kind == YTHIP_MASK_CAUSAL;
+    a.causal = mask_kind == YTHIP_MASK_CAUSAL || mask_kind == YTHIP_MASK_DIAG;
+    {
+        // j <= i + off for every (i, j) once off >= kv_len; for none once off < -q_len
+        const int64_t off = mask_kind == YTHIP_MASK_DIAG ? mask_ld : (int64_t)kv_len - q_len;
+        a.diag_off = (int)std::max<int64_t>(-(int64_t)q_len - 1, std::min<int64_t>(off, kv_len));
+    }
     a.mask = mask_kind == YTHIP_MASK_BOOL ? mask : nullptr;
     a.mask_ld = mask_ld;
     a.bias = bias; a.brs = rs_bias; a.bcs = cs_bias;

@@ -5,7 +5,9 @@ Names and argument meaning follow the reference's operator API
 
     matmul(a, b)                     YTensor::matmul / yt::function::matmul
     linear(x, weight)                yt::function::linear (weight [out, in])
-    scaled_dot_product_attention(q, k, v, scale=0, mask=None, bias=None)
+    scaled_dot_product_attention(q, k, v, scale=0, mask=None, bias=None, backend="flash"|"math")
+    masked_matmul(a, b, mask, masked_value)   YTensor::masked_matmul
+    gemm_masked(a, b, out, mask, alpha, beta) yt::kernel::avx2::sgemm_masked
     rms_norm(x, weight, eps)         yt::function::rmsNorm (last axis)
     rms_norm_rope(...)               fused per-head rmsNorm_ + rope (qwen3 example)
     decode_attention(...)            the q_len == 1 SDPA path over a KV cache
@@ -123,55 +125,209 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
 # Attention
 # ---------------------------------------------------------------------------
 
-def scaled_dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = 0.0,
-                                 mask=None, bias: torch.Tensor | None = None,
-                                 out: torch.Tensor | None = None) -> torch.Tensor:
-    """Prefill SDPA over [B, Hq, Sq, D] queries and [B, Hkv, Skv, D] keys/values.
+def _predicate_mask(f, m: int, n: int, device) -> torch.Tensor:
+    """A predicate f(row, col) -> bool evaluated into a [m, n] byte mask, as the
+    reference calls it per element (src/kernel/avx2/flash_attention.inl:14-49).
+    Tried once on index grids (numpy broadcasting), else element by element."""
+    import numpy as np
+    ii, jj = np.arange(m)[:, None], np.arange(n)[None, :]
+    try:
+        r = np.broadcast_to(np.asarray(f(ii, jj), dtype=bool), (m, n))
+    except Exception:
+        r = np.array([[bool(f(i, j)) for j in range(n)] for i in range(m)], dtype=bool).reshape(m, n)
+    return torch.from_numpy(np.ascontiguousarray(r, dtype=np.uint8)).to(device)
 
-    mask: None (all visible), "causal" (key j visible to query i iff
-    j <= Skv - Sq + i), or a bool/uint8 tensor [Sq, Skv] (True = visible).
-    bias: optional float32 [Sq, Skv] added after scaling. GQA: query head h
-    reads key/value head h // (Hq // Hkv).
-    """
-    _dev(q, k, v)
-    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
-        raise ValueError("scaled_dot_product_attention expects 4-D [B, H, S, D] tensors")
-    B, Hq, Sq, D = q.shape
-    Hkv, Skv = k.shape[1], k.shape[2]
-    if k.shape[3] != D:
-        raise ValueError("query/key head dims differ")  # ops.inl:382-384
-    if v.shape[2] != Skv or v.shape[1] != Hkv:
-        raise ValueError("key/value lengths differ")  # ops.inl:385-387
-    if Hq % Hkv != 0:
-        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
-    dv = v.shape[3]
-    if out is None:
-        out = torch.empty((B, Hq, Sq, dv), dtype=q.dtype, device=q.device)
-    mask_kind, mptr, mld, mask_keep = _lib.MASK_NONE, None, 0, None
+
+def _mask_args(mask, m: int, n: int, device):
+    """-> (kind, pointer, ld, keep-alive) for the C ABI's mask arguments.
+    mask: None, "causal" (j <= i + n - m), ("diag", offset) (j <= i + offset),
+    a bool / uint8 tensor [m, n] (True = visible), or a predicate f(i, j)."""
+    if mask is None:
+        return _lib.MASK_NONE, None, 0, None
     if isinstance(mask, str):
         if mask != "causal":
             raise ValueError(f"unknown mask kind {mask!r}")
-        mask_kind = _lib.MASK_CAUSAL
-    elif mask is not None:
-        if tuple(mask.shape) != (Sq, Skv):
-            raise ValueError(f"mask shape {tuple(mask.shape)} != {(Sq, Skv)}")
-        mask_keep = mask.to(torch.uint8)
-        if mask_keep.stride(1) != 1:
-            mask_keep = mask_keep.contiguous()
-        mask_kind, mptr, mld = _lib.MASK_BOOL, mask_keep.data_ptr(), mask_keep.stride(0)
+        return _lib.MASK_CAUSAL, None, 0, None
+    if isinstance(mask, tuple):
+        if len(mask) != 2 or mask[0] != "diag":
+            raise ValueError(f"unknown mask {mask!r}; use ('diag', offset)")
+        return _lib.MASK_DIAG, None, int(mask[1]), None
+    if callable(mask) and not isinstance(mask, torch.Tensor):
+        mask = _predicate_mask(mask, m, n, device)
+    if tuple(mask.shape) != (m, n):
+        raise ValueError(f"mask shape {tuple(mask.shape)} != {(m, n)}")  # ops.inl:390-393
+    keep = mask.to(device=device, dtype=torch.uint8)
+    if keep.stride(1) != 1:
+        keep = keep.contiguous()
+    return _lib.MASK_BOOL, keep.data_ptr(), keep.stride(0), keep
+
+
+def _fold(shape, strides):
+    """(size, stride) of dims read as one, or None when their strides do not nest."""
+    dims = [(sz, st) for sz, st in zip(shape, strides) if sz != 1]
+    total = 1
+    for sz, _ in dims:
+        total *= sz
+    for (s0, st0), (s1, st1) in zip(dims, dims[1:]):
+        if st0 != st1 * s1:
+            return None
+    return total, (dims[-1][1] if dims else 0)
+
+
+def scaled_dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = 0.0,
+                                 mask=None, bias: torch.Tensor | None = None,
+                                 out: torch.Tensor | None = None, backend: str = "flash",
+                                 workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """yt::function::scaledDotProductAttention (src/function/ops.inl:368-503).
+
+    q [..., Sq, D], k [..., Skv, D], v [..., Skv, Dv]: the leading dims
+    broadcast against each other as the reference's matView does (0-stride
+    views such as the examples' repeat_kv are read in place; the innermost
+    leading dims over which k and v are broadcast become the GQA group). The
+    Qwen3 form q [B, Hq, Sq, D] with k/v [B, Hkv, Skv, D], Hq a multiple of Hkv,
+    is accepted directly: query head h reads key/value head h // (Hq // Hkv).
+    Any element strides, including transposed keys (a [..., D, Skv] cache seen
+    through .transpose(-1, -2)).
+    mask: None, "causal" (key j visible to query i iff j <= Skv - Sq + i),
+    ("diag", off) (j <= i + off), a bool / uint8 tensor [Sq, Skv] (True =
+    visible) or a predicate f(i, j) -> bool (evaluated into a bool mask here).
+    bias: optional float32 [Sq, Skv] added after scaling. Rows with no visible
+    key come out zero. backend: "flash" (FLASH_AVX2's counterpart, online
+    softmax, no score matrix) or "math" (MATH: materialised scores in a
+    workspace of ythip_attn_math_workspace_size bytes, allocated if not given).
+    """
+    _dev(q, k, v)
+    if backend not in ("flash", "math"):
+        raise ValueError(f"unknown backend {backend!r}")  # throwNotSupport (ops.inl:423)
+    if q.dim() < 2 or k.dim() < 2 or v.dim() < 2:
+        raise ValueError("scaled_dot_product_attention expects [..., S, D] tensors")
+    Sq, D = q.shape[-2], q.shape[-1]
+    Skv, dv = k.shape[-2], v.shape[-1]
+    if k.shape[-1] != D:
+        raise ValueError("Query and key head dim must match.")  # ops.inl:382-384
+    if v.shape[-2] != Skv:
+        raise ValueError("Key/value sequence length must match.")  # ops.inl:385-387
+    gqa = (q.dim() == 4 and k.dim() == 4 and v.dim() == 4 and q.shape[0] == k.shape[0] == v.shape[0]
+           and k.shape[1] == v.shape[1] and k.shape[1] != q.shape[1] and q.shape[1] % k.shape[1] == 0)
+    if gqa:
+        lead = tuple(q.shape[:2])
+        B, Hq, Hkv = q.shape[0], q.shape[1], k.shape[1]
+        qv, kv_, vv = q, k, v
+    else:
+        lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
+        qv = q.expand(*lead, Sq, D)
+        kv_ = k.expand(*lead, Skv, D)
+        vv = v.expand(*lead, Skv, dv)
+    if out is None:
+        out = torch.empty((*lead, Sq, dv), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (*lead, Sq, dv):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {(*lead, Sq, dv)}")
+    kind, mptr, mld, mask_keep = _mask_args(mask, Sq, Skv, q.device)
     bptr, brs, bcs, bias_keep = None, 0, 0, None
     if bias is not None:
         if tuple(bias.shape) != (Sq, Skv):
-            raise ValueError(f"bias shape {tuple(bias.shape)} != {(Sq, Skv)}")
+            raise ValueError("Bias shape must match the last two dimensions of the score tensor.")
         bias_keep = bias.to(torch.float32)
         bptr, brs, bcs = bias_keep.data_ptr(), bias_keep.stride(0), bias_keep.stride(1)
-    st = _lib.lib().ythip_attn_prefill(
-        _code(q), B, Hq, Hkv, Sq, Skv, D, dv,
-        q.data_ptr(), i64array(q.stride()), k.data_ptr(), i64array(k.stride()),
-        v.data_ptr(), i64array(v.stride()), out.data_ptr(), i64array(out.stride()),
-        float(scale), mask_kind, mptr, mld, bptr, brs, bcs, _stream())
-    check(st, "ythip_attn_prefill")
+
+    def call(qt, kt, vt, ot, B, Hq, Hkv, qs, ks, vs, os_):
+        if backend == "math":
+            need = int(_lib.lib().ythip_attn_math_workspace_size(_code(q), B, Hq, Sq, Skv))
+            ws = workspace
+            if ws is None or ws.numel() * ws.element_size() < need:
+                ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+            st = _lib.lib().ythip_attn_math(
+                _code(q), B, Hq, Hkv, Sq, Skv, D, dv, qt.data_ptr(), i64array(qs), kt.data_ptr(), i64array(ks),
+                vt.data_ptr(), i64array(vs), ot.data_ptr(), i64array(os_), float(scale), kind, mptr, mld,
+                bptr, brs, bcs, ws.data_ptr(), ws.numel() * ws.element_size(), _stream())
+            check(st, "ythip_attn_math")
+        else:
+            st = _lib.lib().ythip_attn_prefill(
+                _code(q), B, Hq, Hkv, Sq, Skv, D, dv, qt.data_ptr(), i64array(qs), kt.data_ptr(), i64array(ks),
+                vt.data_ptr(), i64array(vs), ot.data_ptr(), i64array(os_), float(scale), kind, mptr, mld,
+                bptr, brs, bcs, _stream())
+            check(st, "ythip_attn_prefill")
+
+    if gqa:
+        call(qv, kv_, vv, out, B, Hq, Hkv, qv.stride(), kv_.stride(), vv.stride(), out.stride())
+        return out
+    # (batch, kv-head, group) from the leading dims: the innermost dims over
+    # which k and v do not move form the group, the first dim is the batch.
+    n = len(lead)
+    p = n
+    while p > 0 and (lead[p - 1] == 1 or (kv_.stride(p - 1) == 0 and vv.stride(p - 1) == 0)):
+        p -= 1
+    bdims = 1 if p >= 1 else 0
+    fq = _fold(lead[bdims:], qv.stride()[bdims:n])
+    fo = _fold(lead[bdims:], out.stride()[bdims:n])
+    fk = _fold(lead[bdims:p], kv_.stride()[bdims:p])
+    fv = _fold(lead[bdims:p], vv.stride()[bdims:p])
+    if None not in (fq, fo, fk, fv) and n >= 1:
+        B = lead[0] if bdims else 1
+        s0 = lambda t: t.stride(0) if bdims else 0  # noqa: E731
+        Hq, Hkv = fq[0], fk[0]
+        call(qv, kv_, vv, out, B, Hq, Hkv,
+             (s0(qv), fq[1], qv.stride(-2), qv.stride(-1)), (s0(kv_), fk[1], kv_.stride(-2), kv_.stride(-1)),
+             (s0(vv), fv[1], vv.stride(-2), vv.stride(-1)), (s0(out), fo[1], out.stride(-2), out.stride(-1)))
+        return out
+    # leading dims that do not fold: one matrix per call
+    import itertools
+    for idx in itertools.product(*[range(x) for x in lead]):
+        qt, kt, vt, ot = qv[idx], kv_[idx], vv[idx], out[idx]
+        call(qt, kt, vt, ot, 1, 1, 1, (0, 0, qt.stride(0), qt.stride(1)), (0, 0, kt.stride(0), kt.stride(1)),
+             (0, 0, vt.stride(0), vt.stride(1)), (0, 0, ot.stride(0), ot.stride(1)))
     return out
+
+
+def masked_gemm_workspace_bytes(batch: int, m: int, n: int) -> int:
+    return int(_lib.lib().ythip_gemm_masked_workspace_size(batch, m, n))
+
+
+def gemm_masked(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, mask, alpha: float = 1.0, beta: float = 0.0,
+                fill: float | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """sgemm_masked (src/kernel/avx2/sgemm.inl:342-584) on 2-D or batched 3-D
+    operands: where `mask` ([m, n], shared by the batch; forms as for attention)
+    is set, out = alpha * a @ b + beta * out; elsewhere out is kept, or set to
+    `fill` when given (masked_matmul's maskedValue)."""
+    _dev(a, b, out)
+    if a.dtype != b.dtype:
+        raise ValueError("a and b must share a dtype")
+    A = a if a.dim() == 3 else a.unsqueeze(0)
+    Bm = b if b.dim() == 3 else b.unsqueeze(0)
+    C = out if out.dim() == 3 else out.unsqueeze(0)
+    bt, m, k = A.shape
+    n = Bm.shape[2]
+    if Bm.shape[1] != k:
+        raise ValueError(f"masked_matmul: inner dimensions differ ({k} vs {Bm.shape[1]})")
+    if tuple(C.shape) != (bt, m, n) or Bm.shape[0] not in (1, bt):
+        raise ValueError("masked_matmul: shapes do not match")
+    kind, mptr, mld, keep = _mask_args(mask, m, n, a.device)
+    need = masked_gemm_workspace_bytes(bt, m, n)
+    ws = workspace
+    if ws is None or ws.numel() * ws.element_size() < need:
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=a.device)
+    st = _lib.lib().ythip_gemm_masked(
+        _code(a), _code(out), bt, m, n, k,
+        A.data_ptr(), A.stride(0), A.stride(1), A.stride(2),
+        Bm.data_ptr(), 0 if Bm.shape[0] == 1 else Bm.stride(0), Bm.stride(1), Bm.stride(2),
+        C.data_ptr(), C.stride(0), C.stride(1), C.stride(2), float(alpha), float(beta),
+        kind, mptr, mld, int(fill is not None), float(fill or 0.0), ws.data_ptr(), ws.numel() * ws.element_size(),
+        _stream())
+    check(st, "ythip_gemm_masked")
+    return out
+
+
+def masked_matmul(a: torch.Tensor, b: torch.Tensor, mask, masked_value: float = 0.0) -> torch.Tensor:
+    """YTensor::masked_matmul (src/ytensor_math.inl:318-410): a [..., m, k] @
+    b [k, n] or [..., k, n] where `mask` [m, n] is set, masked_value elsewhere."""
+    m, k = a.shape[-2], a.shape[-1]
+    n = b.shape[-1]
+    lead = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    a3 = a.expand(*lead, m, k).reshape(-1, m, k)
+    b3 = b if b.dim() == 2 else b.expand(*lead, k, n).reshape(-1, k, n)
+    out = torch.empty((a3.shape[0], m, n), dtype=a.dtype, device=a.device)
+    gemm_masked(a3, b3, out, mask, fill=masked_value)
+    return out.reshape(*lead, m, n)
 
 
 def decode_workspace_bytes(B: int, Hq: int, max_ctx: int, d: int) -> int:
