@@ -13,6 +13,8 @@ the kernels are launched on):
   attn_prefill    configs[2] causal flash prefill S = 512/2048/8192 (TFLOP/s)
   attn_decode     configs[3] decode attention (GB/s of K/V read)
   rmsnorm_rope    fused RMSNorm+RoPE on configs[2] shapes at S=8192 (GB/s)
+  attn_math       the MATH attention backend (materialised scores) at S=2048, and
+                  a causal masked matmul at 4096^3
   qwen3_0p6b      configs[4] shape: 512-token prefill + greedy decode tok/s
   yt_checkpoint   .yt checkpoint of the Qwen3-0.6B shape loaded to the device (GB/s)
   roofline        the headline kernel against MI355X dense bf16 MFMA peak
@@ -65,7 +67,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only (no sweep, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list of sections to run "
-                                               "(gemm,sweep,fp32,prefill,decode,norm,qwen3,ytload)")
+                                               "(gemm,sweep,fp32,prefill,decode,norm,math,qwen3,ytload)")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain conversion-copy kernel of known size (HBM counter calibration)")
     return ap.parse_args()
@@ -190,6 +192,8 @@ def cpu_rows(path, kind: str) -> dict:
       decode    the same with one query row per batch entry, B=16, ctx=8192
       norm_rope rmsNorm_ of the q and k heads + RoPE of both, S=8192
                 (src/function/normalization.inl:256-277, example/qwen3/qwen3.cpp:101-133)
+      math      scaledDotProductAttention(MATH), causal, S=2048 (src/function/ops.inl:388-418)
+      masked    YTensor::masked_matmul 2048^3 with a causal predicate (src/ytensor_math.inl:372-410)
       yt_load   YTensorIO::load of a 256 MiB bf16 tensor (src/ytensor_io.inl:785-830)
     Inputs are N(0,1) (weights N(0,0.02)) rounded to bf16, as on the GPU."""
     import numpy as np
@@ -235,6 +239,17 @@ def cpu_rows(path, kind: str) -> dict:
     rows["rmsnorm_rope_S8192"] = {"s_per_call": round(t, 4), "gbs_bf16_equiv": round(byts / t / 1e9, 3)}
     del qk
     if kind == "reference":
+        # scaledDotProductAttention(MATH), causal predicate, 16 heads, S=2048, fp32
+        S = 2048
+        q, k = bf(16, S, 128), bf(16, S, 128)
+        t = med(lambda: path.sdpa_math(q, k, k, 0.0, diag=0), 2)
+        rows["attn_math_S2048"] = {"s_per_call": round(t, 4),
+                                   "tflops_full_square": round(4.0 * 16 * 128 * S * S / t / 1e12, 4)}
+        del q, k
+        a = bf(2048, 2048)
+        t = med(lambda: path.masked_matmul(a, a, diag=0, value=-1e9), 2)
+        rows["masked_matmul_2048_causal"] = {"s_per_call": round(t, 4), "tflops_full": round(2.0 * 2048 ** 3 / t / 1e12, 4)}
+        del a
         # yt::io::YTensorIO::load of one 256 MiB bf16 tensor from a page-cache file
         import shutil
         import tempfile
@@ -517,6 +532,39 @@ def main() -> int:
                           args.steps, args.warmup, torch)
         sections["rmsnorm_rope_bf16_S8192"] = {"ms": round(t, 5), "gbs": round(byts / t / 1e6, 1),
                                                "frac_hbm": round(byts / t / 1e6 / PEAK_HBM_GBS, 4)}
+
+    if want("math") and not args.quick:
+        # MATH backend (materialised scores) and masked matmul: the whole S x S
+        # product is computed, so flops count the full square; bytes are the
+        # fp32 scores written + read and the bf16 weights written + read.
+        S = 2048
+        q = torch.randn(1, 16, S, 128, device=dev).to(torch.bfloat16)
+        k = torch.randn(1, 8, S, 128, device=dev).to(torch.bfloat16)
+        v = torch.randn(1, 8, S, 128, device=dev).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        ws = torch.empty(int(yt.lib().ythip_attn_math_workspace_size(2, 1, 16, S, S)), dtype=torch.uint8,
+                         device=dev)
+        t = time_launches(lambda: ops.scaled_dot_product_attention(q, k, v, 0.0, "causal", out=o, backend="math",
+                                                                   workspace=ws), max(args.steps // 2, 10),
+                          args.warmup, torch)
+        fl = 4.0 * 16 * 128 * S * S
+        byts = 16.0 * S * S * (4 + 4 + 2 + 2)
+        M2 = 4096
+        a2 = torch.randn(M2, M2, device=dev).to(torch.bfloat16)
+        b2 = (torch.randn(M2, M2, device=dev) * 0.02).to(torch.bfloat16)
+        c2 = torch.empty(M2, M2, device=dev, dtype=torch.bfloat16)
+        w2 = torch.empty(ops.masked_gemm_workspace_bytes(1, M2, M2), dtype=torch.uint8, device=dev)
+        t2 = time_launches(lambda: ops.gemm_masked(a2, b2, c2, "causal", fill=-1e9, workspace=w2),
+                           max(args.steps // 2, 10), args.warmup, torch)
+        sections["attn_math_bf16_S2048"] = {
+            "ms": round(t, 5), "tflops_full_square": round(fl / t / 1e9, 2),
+            "gbs_scores": round(byts / t / 1e6, 1), "frac_hbm": round(byts / t / 1e6 / PEAK_HBM_GBS, 4),
+            "note": "causal, 16 q / 8 kv heads, D=128; scores fp32 + weights bf16 materialised (HBM-bound)"}
+        sections["masked_matmul_bf16_4096_causal"] = {
+            "ms": round(t2, 5), "tflops_full": round(2.0 * M2 ** 3 / t2 / 1e9, 2),
+            "note": "fill -1e9 above the diagonal; the product is computed whole, then masked"}
+        del q, k, v, o, ws, a2, b2, c2, w2
+        torch.cuda.empty_cache()
 
     if want("qwen3") and not args.quick:
         sections["qwen3_0p6b_decode"] = bench_qwen3(torch, dev)

@@ -241,3 +241,23 @@ def test_math_edge_cases(yt, dev):
     v = torch.randn(1, 2, 6, 8, device=dev)
     with pytest.raises(ValueError):
         yt.scaled_dot_product_attention(q, k, v, mask=torch.ones(3, 6, dtype=torch.bool), backend="math")
+
+
+@pytest.mark.parametrize("Lkv", [1500, 4096, 5000])
+def test_math_long_rows(orc, yt, dev, Lkv):
+    """Rows of up to 1024 / 4096 keys are read once into registers; longer
+    rows take the three-pass softmax. Both against the oracle."""
+    rng = np.random.default_rng(Lkv)
+    H, Lq, D = 2, 8, 64
+    Q = rng.standard_normal((H, Lq, D)).astype(np.float32)
+    K = rng.standard_normal((H, Lkv, D)).astype(np.float32)
+    V = rng.standard_normal((H, Lkv, D)).astype(np.float32)
+    m = rng.random((Lq, Lkv)) < 0.5
+    m[3] = False
+    b = rng.standard_normal((Lq, Lkv)).astype(np.float32)
+    got = yt.scaled_dot_product_attention(_t(Q, dev), _t(K, dev), _t(V, dev), 0.0, mask=torch.from_numpy(m),
+                                          bias=_t(b, dev), backend="math")
+    torch.cuda.synchronize()
+    ref = orc.sdpa_math(Q, K, V, 0.0, mask=m, bias=b)
+    assert np.abs(_f(got) - ref).max() <= 1e-4
+    assert torch.count_nonzero(got[:, 3]) == 0

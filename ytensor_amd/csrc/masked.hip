@@ -131,7 +131,65 @@ __global__ __launch_bounds__(256) void math_softmax_kernel(const float* __restri
     }
 }
 
+// The same for rows of at most 256 * CACHE keys, read once: each thread keeps
+// its scores, then their exponentials, in registers.
+template <class T, int CACHE>
+__global__ __launch_bounds__(256) void math_softmax_cached_kernel(const float* __restrict__ S, void* P, int Lq,
+                                                                  int Lkv, MaskDesc mk, float scale,
+                                                                  const float* __restrict__ bias, int64_t brs,
+                                                                  int64_t bcs, int zero_empty) {
+    __shared__ float red[4];
+    const int i = blockIdx.x;
+    const int64_t row = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * Lq + i;
+    const float* s = S + row * Lkv;
+    float x[CACHE];
+    float mx = -FLT_MAX;  // std::numeric_limits<float>::lowest()
+    int any = 0;
+#pragma unroll
+    for (int c = 0; c < CACHE; ++c) {
+        const int j = c * 256 + threadIdx.x;
+        x[c] = -INFINITY;
+        if (j < Lkv) {
+            const bool vis = visible(mk, i, j);
+            float v = vis ? s[j] : -1e9f;  // masked_matmul's fill value (ops.inl:395-399)
+            v *= scale;
+            if (bias) v += bias[(int64_t)i * brs + (int64_t)j * bcs];
+            x[c] = v;
+            mx = fmaxf(mx, v);
+            any |= vis ? 1 : 0;
+        }
+    }
+    mx = block_max(mx, red);
+    const int any_all = __syncthreads_or(any);
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < CACHE; ++c) {
+        x[c] = (c * 256 + (int)threadIdx.x < Lkv) ? expf(x[c] - mx) : 0.f;
+        sum += x[c];
+    }
+    sum = block_sum(sum, red);
+    const bool empty = zero_empty && !any_all;
+#pragma unroll
+    for (int c = 0; c < CACHE; ++c) {
+        const int j = c * 256 + threadIdx.x;
+        if (j < Lkv) store_from_f32<T>(P, row * Lkv + j, empty ? 0.0f : x[c] / sum);
+    }
+}
+
 namespace {
+
+template <class T>
+hipError_t launch_softmax(const float* S, void* P, int B, int Hq, int Lq, int Lkv, const MaskDesc& mk, float scale,
+                          const float* bias, int64_t brs, int64_t bcs, int zero_empty, hipStream_t s) {
+    dim3 grid(Lq, Hq, B);
+    if (Lkv <= 256 * 4)
+        math_softmax_cached_kernel<T, 4><<<grid, 256, 0, s>>>(S, P, Lq, Lkv, mk, scale, bias, brs, bcs, zero_empty);
+    else if (Lkv <= 256 * 16)
+        math_softmax_cached_kernel<T, 16><<<grid, 256, 0, s>>>(S, P, Lq, Lkv, mk, scale, bias, brs, bcs, zero_empty);
+    else
+        math_softmax_kernel<T><<<grid, 256, 0, s>>>(S, P, Lq, Lkv, mk, scale, bias, brs, bcs, zero_empty);
+    return hipGetLastError();
+}
 
 MaskDesc make_mask(int kind, const uint8_t* data, int64_t ld, int m, int n) {
     MaskDesc mk{kind, data, ld, 0};
@@ -278,18 +336,15 @@ __attribute__((visibility("default"))) int ythip_attn_math(
     // 2. mask, scale, bias, softmax -> P (input type)
     const MaskDesc mk = make_mask(mask_kind, mask, mask_ld, q_len, kv_len);
     {
-        dim3 grid(q_len, Hq, B);
         const int zero_empty = mask_kind != YTHIP_MASK_NONE;
+        hipError_t e;
         if (dtype == YTHIP_F32)
-            math_softmax_kernel<F32><<<grid, 256, 0, s>>>(S, P, q_len, kv_len, mk, scale, bias, rs_bias, cs_bias,
-                                                          zero_empty);
+            e = launch_softmax<F32>(S, P, B, Hq, q_len, kv_len, mk, scale, bias, rs_bias, cs_bias, zero_empty, s);
         else if (dtype == YTHIP_BF16)
-            math_softmax_kernel<BF16><<<grid, 256, 0, s>>>(S, P, q_len, kv_len, mk, scale, bias, rs_bias, cs_bias,
-                                                           zero_empty);
+            e = launch_softmax<BF16>(S, P, B, Hq, q_len, kv_len, mk, scale, bias, rs_bias, cs_bias, zero_empty, s);
         else
-            math_softmax_kernel<F16><<<grid, 256, 0, s>>>(S, P, q_len, kv_len, mk, scale, bias, rs_bias, cs_bias,
-                                                          zero_empty);
-        if (int st = status_of(hipGetLastError())) return st;
+            e = launch_softmax<F16>(S, P, B, Hq, q_len, kv_len, mk, scale, bias, rs_bias, cs_bias, zero_empty, s);
+        if (int st = status_of(e)) return st;
     }
     // 3. O = P . V
     const char* Pc = static_cast<const char*>(P);
