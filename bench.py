@@ -267,10 +267,11 @@ def cpu_rows(path, kind: str) -> dict:
     return rows
 
 
-def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256) -> dict:
+def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=None) -> dict:
     """configs[4] shape: random-init Qwen3-0.6B (synthetic N(0, 0.02) weights,
-    bf16 matrices, fp32 norms), 512-token prompt, then greedy decode with each
-    step replayed from one captured HIP graph. tok/s counts the decode steps."""
+    bf16 (or `dtype`) matrices, fp32 norms), 512-token prompt, then greedy
+    decode with each step replayed from one captured HIP graph. tok/s counts the
+    decode steps."""
     import numpy as np
     from ytensor_amd.qwen3 import Qwen3, Qwen3Config, weight_layout
     cfg = Qwen3Config()
@@ -278,7 +279,7 @@ def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256) -> dict:
     g = torch.Generator(device=dev)
     g.manual_seed(3)
     W = torch.randn(total, device=dev, generator=g) * 0.02
-    m = Qwen3(cfg, W, max_ctx=prompt_len + n_tokens + 64, max_prompt=prompt_len)
+    m = Qwen3(cfg, W, max_ctx=prompt_len + n_tokens + 64, max_prompt=prompt_len, dtype=dtype or torch.bfloat16)
     del W
     torch.cuda.empty_cache()
     rng = np.random.default_rng(4)
@@ -442,8 +443,12 @@ def main() -> int:
         Wt = (torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16)
         ms_nt = time_launches(lambda: ops.gemm(A, Wt.t(), C), args.steps, args.warmup, torch)
         ms_torch = time_launches(lambda: torch.matmul(A, B, out=C), args.steps, args.warmup, torch)
+        A16, B16, C16 = A.to(torch.float16), B.to(torch.float16), torch.empty_like(C, dtype=torch.float16)
+        ms_f16 = time_launches(lambda: ops.gemm(A16, B16, C16), args.steps, args.warmup, torch)
+        del A16, B16, C16
         sections["gemm_4096_bf16"] = {"NN_tflops": round(tflops, 2), "NT_tflops": round(flops / ms_nt / 1e9, 2),
-                                      "torch_hipblaslt_NN_tflops": round(flops / ms_torch / 1e9, 2)}
+                                      "torch_hipblaslt_NN_tflops": round(flops / ms_torch / 1e9, 2),
+                                      "NN_fp16_tflops": round(flops / ms_f16 / 1e9, 2)}
         del Wt
 
     if want("sweep") and not args.quick:
@@ -568,6 +573,9 @@ def main() -> int:
 
     if want("qwen3") and not args.quick:
         sections["qwen3_0p6b_decode"] = bench_qwen3(torch, dev)
+        torch.cuda.empty_cache()
+        sections["qwen3_0p6b_decode_fp16"] = bench_qwen3(torch, dev, dtype=torch.float16)
+        torch.cuda.empty_cache()
 
     if want("ytload") and not args.quick:
         try:

@@ -318,6 +318,15 @@ int ythip_yt_load(ythip_yt_file* f, int index, void* dst, int dtype, uint64_t ds
  */
 int ythip_yt_load_many(ythip_yt_file* f, int n, const int* index, void* const* dst, const int* dtype,
                        const uint64_t* dst_bytes, void* stream);
+/*
+ * HOST-memory element conversion with the reference's casts, as the loads
+ * above use them: float -> bfloat16 (include/types/bfloat16.hpp:78-80),
+ * float -> float16 (include/types/float_spec.hpp:435-491, subnormals flush to
+ * zero), 16-bit -> float (exact; the reference's fp16 subnormal doubling kept).
+ * For callers that prepare 16-bit weights on the host (src and dst are host
+ * pointers, n elements; dtypes F32 / F16 / BF16).
+ */
+int ythip_convert_host(int src_dtype, int dst_dtype, const void* src, void* dst, int64_t n);
 /* Waits until every copy queued by this handle has completed. */
 int ythip_yt_sync(ythip_yt_file* f);
 

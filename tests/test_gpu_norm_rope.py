@@ -26,7 +26,7 @@ def _oracle_norm_rope(orc, qkv, B, S, Hq, Hkv, d, wq, wk, eps, cos, sin, pos0):
     return q, k, v
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("B,S,pos0", [(1, 7, 0), (2, 33, 5), (1, 512, 0)])
 def test_norm_rope(orc, yt, dtype, B, S, pos0):
     Hq, Hkv, d = 16, 8, 128
@@ -65,7 +65,7 @@ def test_norm_rope_into_cache(orc, yt):
     assert np.all(kh[:, :, :cache_pos] == 7.0) and np.all(kh[:, :, cache_pos + S:] == 7.0)
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,n", [(1, 1024), (37, 1024), (512, 1024), (5, 100)])
 def test_rms_norm_rows(orc, yt, dtype, rows, n):
     rng = np.random.default_rng(rows + n)

@@ -85,3 +85,46 @@ def test_config5_qwen3_0p6b_greedy_32(orc):
     tg = m.generate(pr, 32)
     print("oracle", to.tolist(), "\ngpu   ", tg.tolist(), "\nmargins", np.round(mo, 6).tolist(), flush=True)
     assert np.array_equal(tg, to)
+
+
+@pytest.mark.gpu
+def test_qwen3_small_fp16_end_to_end(orc):
+    """The whole decoder in fp16 (weights rounded with yt::float16's rule,
+    activations, KV cache and GEMM inputs fp16; residual and norms fp32):
+    greedy tokens equal the oracle's on the same fp16-representable weights,
+    first-step logits within the 16-bit bar, graph replay == eager."""
+    import torch
+
+    from ytensor_amd.qwen3 import Qwen3, Qwen3Config
+    kw = SMALL
+    cfg_o = oracle.Qwen3Config(**kw)
+    W = _small_weights(orc, cfg_o)
+    W16 = orc.f16_to_f32(orc.f16_round(W))  # what the device holds for the matrices
+    names = [n for n, _ in oracle.qwen3_weight_layout(cfg_o)]
+    sizes = [int(np.prod(s)) for _, s in oracle.qwen3_weight_layout(cfg_o)]
+    Wo = W.copy()
+    off = 0
+    for n, sz in zip(names, sizes):
+        if "norm" not in n:
+            Wo[off:off + sz] = W16[off:off + sz]
+        off += sz
+    pr = oracle.qwen3_prompt(cfg_o, 37, seed=4)
+    steps = 12
+    to, mo, lo = orc.qwen3_generate(cfg_o, Wo, pr, steps)
+    m = Qwen3(Qwen3Config(**kw), W, max_ctx=64, max_prompt=64, dtype=torch.float16)
+    assert m.embed.dtype == torch.float16 and m.kc.dtype == torch.float16
+    tg = m.generate(pr, steps)
+    print("oracle", to, "margins", np.round(mo, 4), "\ngpu   ", tg, flush=True)
+    m2 = Qwen3(Qwen3Config(**kw), W, max_ctx=64, max_prompt=64, dtype=torch.float16)
+    m2.prefill(pr)
+    torch.cuda.synchronize()
+    lg = m2.logits.float().cpu().numpy()[0]
+    rel = np.abs(lg - lo).max() / np.abs(lo).max()
+    print("fp16 first-step logits rel err", rel, flush=True)
+    assert rel <= 2e-2
+    assert np.array_equal(tg, to)
+    m3 = Qwen3(Qwen3Config(**kw), W, max_ctx=64, max_prompt=64, dtype=torch.float16)
+    assert np.array_equal(m3.generate(pr, steps, use_graph=False), tg)
+    # the matrices on the device are exactly yt::float16(w)
+    assert np.array_equal(m.embed.cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1),
+                          orc.f16_round(W[:sizes[0]]))

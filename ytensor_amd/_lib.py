@@ -75,6 +75,7 @@ SIGNATURES = {
     "ythip_yt_load": (_I, [_P, _I, _P, _I, _U64, _P]),
     "ythip_yt_load_many": (_I, [_P, _I, _P, _P, _P, _P, _P]),
     "ythip_yt_sync": (_I, [_P]),
+    "ythip_convert_host": (_I, [_I, _I, _P, _P, _L]),
     "ythip_yt_save": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(YtTensor), ctypes.c_char_p, _I, _P]),
 }
 

@@ -901,6 +901,22 @@ __attribute__((visibility("default"))) int ythip_yt_load_many(ythip_yt_file* f, 
     return 0;
 }
 
+__attribute__((visibility("default"))) int ythip_convert_host(int src_dtype, int dst_dtype, const void* src,
+                                                              void* dst, int64_t n) {
+    auto kind = [](int d) { return d == YTHIP_F32 ? SRC_F32 : d == YTHIP_BF16 ? SRC_BF16 : SRC_F16; };
+    auto ok = [](int d) { return d == YTHIP_F32 || d == YTHIP_F16 || d == YTHIP_BF16; };
+    if (!ok(src_dtype) || !ok(dst_dtype) || n < 0 || (n > 0 && (!src || !dst)))
+        return fail(YTHIP_EINVAL, "ythip_convert_host: bad arguments");
+    if (n == 0) return 0;
+    if (src_dtype == dst_dtype) {
+        std::memcpy(dst, src, static_cast<size_t>(n) * dst_size(dst_dtype));
+        return 0;
+    }
+    convert_parallel(kind(src_dtype), dst_dtype, static_cast<const unsigned char*>(src),
+                     static_cast<unsigned char*>(dst), static_cast<size_t>(n));
+    return 0;
+}
+
 __attribute__((visibility("default"))) int ythip_yt_sync(ythip_yt_file* f) {
     if (!f) return fail(YTHIP_EINVAL, "ythip_yt_sync: NULL file");
     return drain(f);

@@ -7,14 +7,16 @@ residual -> RMSNorm -> fused gate_up -> SwiGLU -> down projection + residual,
 then the final norm and the tied LM head, greedy selection.
 
 MI355X layout and execution:
-  * weights bf16 in HBM (qkv and gate_up fused as in the example's load(),
-    qwen3.cpp:326-349), norms fp32, embedding bf16 and reused as the LM head
-    unless the checkpoint has lm_head.weight; a .yt checkpoint loads straight
-    into this layout (Qwen3.from_yt);
-  * residual stream fp32; GEMM inputs bf16; the o/down projections write
-    fp32 straight into the residual with beta = 1 (residual add fused into
-    the GEMM epilogue); logits fp32;
-  * KV cache bf16 [layers][1, kv_heads, ctx, head_dim];
+  * weights in the model's 16-bit type (bf16 by default, fp16 with
+    dtype=torch.float16; rounded with the reference's yt::bfloat16 /
+    yt::float16 casts) in HBM, qkv and gate_up fused as in the example's
+    load() (qwen3.cpp:326-349); norms fp32; the embedding doubles as the LM
+    head unless the checkpoint has lm_head.weight; a .yt checkpoint loads
+    straight into this layout (Qwen3.from_yt);
+  * residual stream fp32; GEMM inputs in the 16-bit type; the o/down
+    projections write fp32 straight into the residual with beta = 1 (residual
+    add fused into the GEMM epilogue); logits fp32;
+  * KV cache in the 16-bit type, [layers][1, kv_heads, ctx, head_dim];
   * a decode step is 7 launches per layer (the RMSNorms ride in the qkv and
     gate_up GEMV prologues, SwiGLU in the down projection's, the final norm
     and the argmax in the LM head's) with no host-side value that changes
@@ -99,8 +101,11 @@ class Qwen3:
     """Greedy batch-1 generation on one GPU."""
 
     def __init__(self, cfg: Qwen3Config, weights, device="cuda", max_ctx: int | None = None,
-                 max_prompt: int = 512, fused: bool = True):
+                 max_prompt: int = 512, fused: bool = True, dtype: torch.dtype = torch.bfloat16):
+        if dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("the decoder runs its matrices, activations and KV cache in bfloat16 or float16")
         self.cfg = cfg
+        self.dtype = dtype  # matrices, GEMM inputs and KV cache; residual, norms and logits stay fp32
         self.fused = fused  # decode step with the fused GEMV prologues (same bits as the unfused path)
         self.dev = torch.device(device)
         self.max_ctx = min(cfg.max_pos, max_ctx or cfg.max_pos)
@@ -113,7 +118,7 @@ class Qwen3:
     def _upload(self, weights) -> None:
         """weights: flat fp32 array (numpy or torch) in weight_layout order, a
         dict name -> tensor, or the path of a .yt checkpoint (see _load_yt).
-        Matrices become bf16, norms stay fp32."""
+        Matrices become the model's 16-bit type, norms stay fp32."""
         cfg, dev = self.cfg, self.dev
         if isinstance(weights, (str, bytes)) or hasattr(weights, "__fspath__"):
             self._load_yt(weights)
@@ -132,7 +137,15 @@ class Qwen3:
             if flat.numel() != o:
                 raise ValueError(f"weight buffer has {flat.numel()} values, the layout needs {o}")
             get = lambda name, shp: flat[offs[name][0]:offs[name][0] + offs[name][1]].reshape(shp)
-        bf = lambda t: t.to(device=dev, dtype=torch.bfloat16).contiguous()
+        code = _lib.BF16 if self.dtype == torch.bfloat16 else _lib.F16
+
+        def bf(t):
+            # fp32 -> 16-bit on the host with the reference's cast (yt::bfloat16 / yt::float16)
+            src = np.ascontiguousarray(t.detach().cpu().numpy(), dtype=np.float32)
+            bits = np.empty(src.shape, np.uint16)
+            _lib.check(_lib.lib().ythip_convert_host(_lib.F32, code, src.ctypes.data, bits.ctypes.data, src.size),
+                       "ythip_convert_host")
+            return torch.from_numpy(bits.view(np.int16)).view(self.dtype).to(dev)
         f32 = lambda t: t.to(device=dev, dtype=torch.float32).contiguous()
         self.embed = bf(get("embed", (cfg.vocab, cfg.hidden)))
         self.layers = []
@@ -159,8 +172,8 @@ class Qwen3:
         304-363, 424-431) from a .yt checkpoint, straight into the device
         layout: q/k/v land in the row blocks of the fused qkv weight and
         gate/up in gate_up (the example's concat, 326-349, without a copy);
-        matrices are stored as bf16 (converted with the reference's cast when
-        the file holds another float type), norms as fp32. lm_head.weight is
+        matrices are stored in the model's 16-bit type (converted with the
+        reference's cast when the file holds another float type), norms as fp32. lm_head.weight is
         used when present, else the embedding (tied). Unlike the example, a
         missing tensor is an error rather than an empty weight."""
         from . import io as ytio
@@ -171,7 +184,7 @@ class Qwen3:
             raise FileNotFoundError(f"cannot open {path} as a .yt checkpoint")
         try:
             names = set(f.getTensorNames())
-            bf, fp = torch.bfloat16, torch.float32
+            bf, fp = self.dtype, torch.float32
             top = hf_names(cfg)
             need = [top["embed"], top["norm"]] + [n for i in range(cfg.layers) for n in hf_names(cfg, i).values()]
             missing = [n for n in need if n not in names]
@@ -227,7 +240,7 @@ class Qwen3:
     def _alloc(self) -> None:
         cfg, dev, P = self.cfg, self.dev, self.max_prompt
         H, nh, nkv, hd, I = cfg.hidden, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
-        bf, f32 = torch.bfloat16, torch.float32
+        bf, f32 = self.dtype, torch.float32
         self.x = torch.empty((P, H), dtype=f32, device=dev)
         self.h = torch.empty((P, H), dtype=bf, device=dev)
         self.qkv = torch.empty((P, (nh + 2 * nkv) * hd), dtype=bf, device=dev)
