@@ -313,8 +313,9 @@ def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=No
             "bytes_per_token": w_bytes + kv_bytes, "hbm_gbs": round(gbs, 1),
             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "tokens_generated": int(n_tokens),
             "distinct_tokens": int(len(set(toks.tolist()))),
-            "note": "batch 1, greedy, decode step = one HIP graph replay of 200 kernels "
-                    "(7 per layer: RMSNorm and SwiGLU fused into the GEMV prologues)"}
+            "note": "batch 1, greedy, decode step = one HIP graph replay of 171 kernels (6 per layer: "
+                    "RMSNorm and SwiGLU fused into the GEMV prologues, q/k norm + RoPE + cache append into "
+                    "the split-K attention kernel)"}
 
 
 def bench_yt_load(torch, dev, reps: int = 3) -> dict:

@@ -158,6 +158,31 @@ int ythip_attn_decode(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
                       float scale, void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * One decode step's attention for the Qwen3 layer with the q/k norm and RoPE
+ * fused in: the equivalent of ythip_rmsnorm_rope (S = 1, dev_pos) followed by
+ * ythip_attn_decode (kv_len = *dev_pos + 1), with the same bits:
+ *   qkv: the new token's projection row per batch entry (row b at qkv + b*ld_qkv),
+ *        q heads, then k heads, then v heads (example/qwen3/src/qwen3.cpp:233-248);
+ *   q, k <- RMSNorm (wq / wk, may be NULL) + RoPE at position p = *dev_pos (cos/sin
+ *        may be NULL); k and v are written to the cache row p (kv_str as for
+ *        ythip_attn_decode, K and V share it);
+ *   O[b, h] = softmax(scale * q . K[0..p]^T) . V[0..p]  (the q_len == 1 path,
+ *        src/kernel/avx2/flash_attention.inl:202-272).
+ * workspace: ythip_attn_decode_workspace_size(B, Hq, max_ctx, d) bytes. With
+ * O == NULL only the split-K partials are produced, in the workspace as
+ * fp32 [B][Hq][S][d + 2] = (running max m in log2 units, sum l, o[d]) per
+ * split, S = ythip_attn_decode_splits(B, Hq, max_ctx), for a caller that
+ * merges them itself.
+ * qkv rows, norm weights and cos/sin rows must be 16-byte aligned.
+ */
+int ythip_attn_decode_splits(int B, int Hq, int max_ctx);
+int ythip_attn_decode_rope(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
+                           const void* qkv, int64_t ld_qkv, const float* wq, const float* wk, float eps,
+                           const float* cos_tab, const float* sin_tab, int64_t ld_tab, const int32_t* dev_pos,
+                           void* Kc, void* Vc, const int64_t kv_str[3], void* O, const int64_t o_str[2],
+                           float scale, void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * Fused per-head RMSNorm + rotate-half RoPE on the fused qkv projection output,
  * scattering Q to [B,Hq,S,d] and K/V into cache rows cache_pos + s:
  *   qkv: rows of (Hq + 2*Hkv)*d elements, row (b*S + s) at qkv + (b*S+s)*ld_qkv;

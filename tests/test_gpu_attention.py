@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from conftest import rel_err
-from helpers import check16, dev_f32, host_f32, make_input
+from helpers import TORCH_DT, check16, dev_f32, host_f32, make_input
 
 pytestmark = pytest.mark.gpu
 
@@ -183,3 +183,48 @@ def test_single_visible_key_and_zero_query(orc, yt):
     g = host_f32(yt.scaled_dot_product_attention(dev_f32(Z), dev_f32(K), dev_f32(V), 0.0, mask="causal"))
     expect = np.cumsum(V[0, 0].astype(np.float64), axis=0) / np.arange(1, S + 1)[:, None]
     assert np.allclose(g[0, 0], expect, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("Hq,Hkv,d", [(16, 8, 128), (8, 8, 64), (16, 4, 128), (32, 4, 64)])
+def test_decode_attention_rope_equals_unfused(orc, yt, dtype, Hq, Hkv, d):
+    """ythip_attn_decode_rope == ythip_rmsnorm_rope (S = 1, dev_pos) followed
+    by ythip_attn_decode (kv_len = pos + 1): the same bits in the output, the
+    cache rows and (O == NULL) the split-K partials, over a run of positions
+    (the owner split moves across chunk boundaries)."""
+    rng = np.random.default_rng(Hq * 7 + d)
+    B, max_ctx = 2, 300
+    dt = TORCH_DT[dtype]
+    width = (Hq + 2 * Hkv) * d
+    cos, sin = orc.rope_tables(d, max_ctx, 1e6)
+    cos_d, sin_d = dev_f32(cos), dev_f32(sin)
+    wq = dev_f32((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
+    wk = dev_f32((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
+    kc = torch.zeros((B, Hkv, max_ctx, d), dtype=dt, device="cuda")
+    vc = torch.zeros_like(kc)
+    pre = torch.from_numpy(rng.standard_normal((B, Hkv, 100, d)).astype(np.float32)).to("cuda").to(dt)
+    kc[:, :, :100] = pre
+    vc[:, :, :100] = pre * 0.5
+    kc2, vc2, kc3, vc3 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    ws = torch.empty(yt.ops.decode_workspace_bytes(B, Hq, max_ctx, d), dtype=torch.uint8, device="cuda")
+    ws2 = torch.empty_like(ws)
+    ws3 = torch.empty_like(ws)
+    for pos in (100, 101, 149, 150, 151, 299):
+        qkv = torch.from_numpy(rng.standard_normal((B, width)).astype(np.float32)).to("cuda").to(dt)
+        p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        o_f = torch.empty((B, Hq, d), dtype=dt, device="cuda")
+        yt.ops.decode_attention_rope(qkv, Hq, Hkv, d, wq, wk, 1e-6, cos_d, sin_d, p, kc, vc, o_f, ws)
+        qd = torch.empty((B, Hq, 1, d), dtype=dt, device="cuda")
+        yt.rms_norm_rope(qkv.view(B, 1, width), Hq, Hkv, d, wq, wk, 1e-6, cos_d, sin_d, q_out=qd, k_out=kc2,
+                         v_out=vc2, dev_pos=p)
+        kvl = torch.full((B,), pos + 1, dtype=torch.int32, device="cuda")
+        o_u = yt.decode_attention(qd.view(B, Hq, d), kc2, vc2, kv_len=kvl, workspace=ws2)
+        torch.cuda.synchronize()
+        assert torch.equal(o_f, o_u), (dtype, pos)
+        assert torch.equal(kc, kc2) and torch.equal(vc, vc2), (dtype, pos)
+        # partials only (O == NULL): the workspace holds the unfused kernel's partials
+        yt.ops.decode_attention_rope(qkv, Hq, Hkv, d, wq, wk, 1e-6, cos_d, sin_d, p, kc3, vc3, None, ws3)
+        torch.cuda.synchronize()
+        nparts = B * Hq * yt.ops.decode_splits(B, Hq, max_ctx) * (d + 2) * 4
+        assert torch.equal(ws3[:nparts], ws2[:nparts]), (dtype, pos)
+        assert torch.equal(kc3, kc2) and torch.equal(vc3, vc2)

@@ -395,12 +395,53 @@ struct DecodeArgs {
     int B, Hq, Hkv, max_ctx, splits, chunk;
     float scale_log2;
     float* ws;  // [B, Hq, splits, D + 2]
+    // fused decode step (ythip_attn_decode_rope): the new token's q/k/v come
+    // from its qkv row; q and k get RMSNorm + RoPE at position *dev_pos, and
+    // k and v are appended to the cache there before the keys are read.
+    const void* qkv;
+    int64_t ld_qkv;
+    const float* wq;
+    const float* wk;
+    float eps;
+    const float* cos_tab;
+    const float* sin_tab;
+    int64_t ld_tab;
+    const int32_t* dev_pos;
+    int fused;
+    int direct;  // splits == 1 and O given: the split kernel writes O itself
 };
 
 constexpr int DEC_GMAX = 8;
 
+// Rounds 8 values to the storage type T and back (what a store and a reload give).
+template <class T>
+__device__ __forceinline__ void round8(float (&x)[8]) {
+    if constexpr (sizeof(typename T::raw) == 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t w = pack2<T>(x[2 * e], x[2 * e + 1]);
+            x[2 * e] = lo_as_f32(T{}, w);
+            x[2 * e + 1] = hi_as_f32(T{}, w);
+        }
+    }
+}
+
+template <class T>
+__device__ __forceinline__ void store8_raw(typename T::raw* p, const float (&x)[8]) {
+    if constexpr (sizeof(typename T::raw) == 2) {
+        *reinterpret_cast<u32x4*>(p) = u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(x[4], x[5]),
+                                             pack2<T>(x[6], x[7])};
+    } else {
+        reinterpret_cast<f32x4*>(p)[0] = f32x4{x[0], x[1], x[2], x[3]};
+        reinterpret_cast<f32x4*>(p)[1] = f32x4{x[4], x[5], x[6], x[7]};
+    }
+}
+
 // D = 8 * LPK (LPK lanes per key, 8 elements each); G query heads per kv head.
-template <class T, int D, int G>
+// FUSED: see DecodeArgs; the per-head RMSNorm / RoPE arithmetic is that of
+// norm_rope_kernel, so the fused step gives the same bits as
+// ythip_rmsnorm_rope followed by ythip_attn_decode.
+template <class T, int D, int G, bool FUSED>
 __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
     using raw = typename T::raw;
     constexpr int LPK = D / 8;          // lanes per key
@@ -409,18 +450,18 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int slot = tid / LPK, part = tid % LPK;
-    const int len = a.kv_len ? min(a.kv_len[b], a.max_ctx) : a.max_ctx;
     const int kbeg = split * a.chunk;
+    int len, pos = -1;
+    bool owner = false;  // FUSED: this workgroup's chunk holds the new token's position
+    if constexpr (FUSED) {
+        pos = a.dev_pos[0];
+        len = min(pos + 1, a.max_ctx);
+        owner = pos >= 0 && pos < a.max_ctx && pos >= kbeg && pos < kbeg + a.chunk;
+    } else {
+        len = a.kv_len ? min(a.kv_len[b], a.max_ctx) : a.max_ctx;
+    }
     const int kend = min(len, kbeg + a.chunk);
 
-    float q[G][8];
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        const int h = kvh * G + gi;
-        const raw* qp = static_cast<const raw*>(a.Q) + b * a.qs0 + h * a.qs1 + part * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) q[gi][e] = load_as_f32<T>(qp, e) * a.scale_log2;
-    }
     float m[G], l[G], o[G][8];
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
@@ -432,14 +473,16 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
     const raw* Kb = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1 + part * 8;
     const raw* Vb = static_cast<const raw*>(a.V) + b * a.ks0 + kvh * a.ks1 + part * 8;
 
-    for (int k0 = kbeg + slot; k0 < kend; k0 += SLOTS * UNR) {
-        float kx[UNR][8], vx[UNR][8];
-        bool ok[UNR];
+    // K/V of keys [k0, k0 + SLOTS * UNR) (this lane's 8 elements), clamped rows for
+    // keys past the end (loaded but never used)
+    float kx[UNR][8], vx[UNR][8];
+    bool ok[UNR];
+    auto load_batch = [&](int k0) {
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
             const int key = k0 + u * SLOTS;
             ok[u] = key < kend;
-            const int kk = ok[u] ? key : kbeg;  // clamped: loaded but never used
+            const int kk = ok[u] ? key : kbeg;
             const raw* kp = Kb + (int64_t)kk * a.ks2;
             const raw* vp = Vb + (int64_t)kk * a.ks2;
             if constexpr (sizeof(raw) == 2) {
@@ -463,6 +506,119 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
                     kx[u][e] = k_lo[e]; kx[u][e + 4] = k_hi[e];
                     vx[u][e] = v_lo[e]; vx[u][e + 4] = v_hi[e];
                 }
+            }
+        }
+    };
+    // The first batch is in flight while the query (and, fused, the new
+    // token's norm / RoPE) is prepared.
+    int k0 = kbeg + slot;
+    if (k0 < kend) load_batch(k0);
+
+    float q[G][8];
+    __shared__ float s_new[FUSED ? (G + 2) * D : 1];  // normed + roped q heads, then k, then v
+    if constexpr (FUSED) {
+        // norm_rope_kernel's arithmetic, one LPR-lane group per row
+        constexpr int HALF = D / 2, LPR = HALF / 8;
+        const int nrows = G + (owner ? 2 : 0);
+        if (tid < nrows * LPR) {
+            const int r = tid / LPR, j = tid % LPR;
+            const int head = r < G ? kvh * G + r : (r == G ? a.Hq + kvh : a.Hq + a.Hkv + kvh);
+            const raw* src = static_cast<const raw*>(a.qkv) + (int64_t)b * a.ld_qkv + (int64_t)head * D + 8 * j;
+            float x1[8], x2[8];
+            auto load8 = [&](const raw* p8, float (&x)[8]) {
+                if constexpr (sizeof(raw) == 2) {
+                    const u32x4 w4 = *reinterpret_cast<const u32x4*>(p8);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        x[2 * e] = lo_as_f32(T{}, w4[e]);
+                        x[2 * e + 1] = hi_as_f32(T{}, w4[e]);
+                    }
+                } else {
+                    const f32x4 lo = reinterpret_cast<const f32x4*>(p8)[0], hi = reinterpret_cast<const f32x4*>(p8)[1];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        x[e] = lo[e];
+                        x[e + 4] = hi[e];
+                    }
+                }
+            };
+            load8(src, x1);
+            load8(src + HALF, x2);
+            const float* w = r < G ? a.wq : (r == G ? a.wk : nullptr);
+            if (r <= G && w != nullptr) {
+                float ss = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = fmaf(x2[e], x2[e], fmaf(x1[e], x1[e], ss));
+#pragma unroll
+                for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+                const float den = sqrtf(ss / (float)D + a.eps);
+                const f32x4* w1 = reinterpret_cast<const f32x4*>(w + 8 * j);
+                const f32x4* w2 = reinterpret_cast<const f32x4*>(w + HALF + 8 * j);
+                const f32x4 wa = w1[0], wb = w1[1], wc = w2[0], wd = w2[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x1[e] = (x1[e] / den) * wa[e];
+                    x1[e + 4] = (x1[e + 4] / den) * wb[e];
+                    x2[e] = (x2[e] / den) * wc[e];
+                    x2[e + 4] = (x2[e + 4] / den) * wd[e];
+                }
+            }
+            if (r <= G && a.cos_tab != nullptr) {
+                const int64_t t = (int64_t)pos * a.ld_tab + 8 * j;
+                const f32x4 c0 = *reinterpret_cast<const f32x4*>(a.cos_tab + t);
+                const f32x4 c1 = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
+                const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.sin_tab + t);
+                const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.sin_tab + t + 4);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float c = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
+                    const float y1 = fmaf(x1[e], c, -(x2[e] * sn));
+                    const float y2 = fmaf(x2[e], c, x1[e] * sn);
+                    x1[e] = y1;
+                    x2[e] = y2;
+                }
+            }
+            round8<T>(x1);
+            round8<T>(x2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                s_new[r * D + 8 * j + e] = x1[e];
+                s_new[r * D + HALF + 8 * j + e] = x2[e];
+            }
+            if (r >= G) {  // append k (r == G) or v to the cache at `pos`
+                raw* dst = static_cast<raw*>(const_cast<void*>(r == G ? a.K : a.V)) + b * a.ks0 + kvh * a.ks1 +
+                           (int64_t)pos * a.ks2;
+                store8_raw<T>(dst + 8 * j, x1);
+                store8_raw<T>(dst + HALF + 8 * j, x2);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[gi][e] = s_new[gi * D + part * 8 + e] * a.scale_log2;
+    } else {
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const int h = kvh * G + gi;
+            const raw* qp = static_cast<const raw*>(a.Q) + b * a.qs0 + h * a.qs1 + part * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[gi][e] = load_as_f32<T>(qp, e) * a.scale_log2;
+        }
+    }
+
+    for (; k0 < kend; k0 += SLOTS * UNR) {
+        if constexpr (FUSED) {
+            if (owner) {  // the token appended above: its k / v from LDS, not the cache row
+#pragma unroll
+                for (int u = 0; u < UNR; ++u)
+                    if (k0 + u * SLOTS == pos) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            kx[u][e] = s_new[G * D + part * 8 + e];
+                            vx[u][e] = s_new[(G + 1) * D + part * 8 + e];
+                        }
+                    }
             }
         }
 #pragma unroll
@@ -499,6 +655,7 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
             }
             m[gi] = mx;
         }
+        if (k0 + SLOTS * UNR < kend) load_batch(k0 + SLOTS * UNR);
     }
 
     // Merge the SLOTS key slots of this workgroup: LDS holds per slot (m, l) and o.
@@ -530,6 +687,13 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
             }
         }
         const int h = kvh * G + gi;
+        if (a.direct) {
+            // one split: attn_decode_merge over a single partial is acc / L
+            // (its weight exp2(M - M) is exactly 1), stored straight away
+            const float out = L > 0.f ? acc / L : 0.f;
+            store_from_f32<T>(a.O, b * a.os0 + h * a.os1 + d, out);
+            continue;
+        }
         float* dst = ws + (((int64_t)b * a.Hq + h) * a.splits + split) * (D + 2);
         dst[2 + d] = acc;
         if (d == 0) {
@@ -637,9 +801,12 @@ int decode_splits(int B, int Hq, int max_ctx) {
 template <class T, int D, int G>
 hipError_t launch_decode_g(const DecodeArgs& a, hipStream_t s) {
     dim3 grid(a.splits, a.Hkv, a.B);
-    attn_decode_split<T, D, G><<<grid, 256, 0, s>>>(a);
+    if (a.fused)
+        attn_decode_split<T, D, G, true><<<grid, 256, 0, s>>>(a);
+    else
+        attn_decode_split<T, D, G, false><<<grid, 256, 0, s>>>(a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || a.O == nullptr || a.direct) return e;  // O == NULL: the caller merges the partials
     attn_decode_merge<T, D><<<dim3(a.Hq, a.B), D, 0, s>>>(a);
     return hipGetLastError();
 }
@@ -757,6 +924,62 @@ __attribute__((visibility("default"))) int ythip_attn_decode(int dtype, int B, i
     a.chunk = max_ctx > 0 ? (max_ctx + a.splits - 1) / a.splits : 0;
     a.scale_log2 = scale * LOG2E;
     a.ws = static_cast<float*>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case YTHIP_F32: return status_of(launch_decode<F32>(a, d, G, s));
+        case YTHIP_F16: return status_of(launch_decode<F16>(a, d, G, s));
+        default: return status_of(launch_decode<BF16>(a, d, G, s));
+    }
+}
+
+__attribute__((visibility("default"))) int ythip_attn_decode_splits(int B, int Hq, int max_ctx) {
+    if (B <= 0 || Hq <= 0 || max_ctx <= 0) return 0;
+    return decode_splits(B, Hq, max_ctx);
+}
+
+__attribute__((visibility("default"))) int ythip_attn_decode_rope(
+    int dtype, int B, int Hq, int Hkv, int d, int max_ctx, const void* qkv, int64_t ld_qkv, const float* wq,
+    const float* wk, float eps, const float* cos_tab, const float* sin_tab, int64_t ld_tab, const int32_t* dev_pos,
+    void* Kc, void* Vc, const int64_t kv_str[3], void* O, const int64_t o_str[2], float scale, void* workspace,
+    size_t ws_bytes, void* stream) {
+    const char* who = "ythip_attn_decode_rope";
+    if (B < 0 || Hq < 0 || Hkv < 0 || max_ctx <= 0) return fail(YTHIP_EINVAL, "%s: bad size", who);
+    if ((int64_t)B * Hq == 0) return 0;
+    if (Hkv == 0 || Hq % Hkv != 0) return fail(YTHIP_EINVAL, "%s: Hq=%d not a multiple of Hkv=%d", who, Hq, Hkv);
+    const int G = Hq / Hkv;
+    if (d != 64 && d != 128) return fail(YTHIP_EUNSUPPORTED, "%s: head dim %d (supported: 64, 128)", who, d);
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return fail(YTHIP_EUNSUPPORTED, "%s: group size %d (supported: 1, 2, 4, 8)", who, G);
+    if (!qkv || !dev_pos || !Kc || !Vc || !kv_str || (O && !o_str) || (cos_tab == nullptr) != (sin_tab == nullptr))
+        return fail(YTHIP_EINVAL, "%s: NULL pointer", who);
+    if (dtype != YTHIP_F32 && dtype != YTHIP_F16 && dtype != YTHIP_BF16)
+        return fail(YTHIP_EINVAL, "%s: invalid dtype %d", who, dtype);
+    const int es = dtype == YTHIP_F32 ? 4 : 2;
+    if (!al(Kc, 16) || !al(Vc, 16) || kv_str[0] % (16 / es) || kv_str[1] % (16 / es) || kv_str[2] % (16 / es) ||
+        !al(qkv, 16) || ld_qkv % (16 / es) || (wq && !al(wq, 16)) || (wk && !al(wk, 16)) ||
+        (cos_tab && (!al(cos_tab, 16) || !al(sin_tab, 16) || (ld_tab & 3))))
+        return fail(YTHIP_EUNSUPPORTED, "%s: qkv rows, K/V cache rows, norm weights and tables must be 16-byte aligned",
+                    who);
+    const size_t need = ythip_attn_decode_workspace_size(B, Hq, max_ctx, d);
+    if (workspace == nullptr || ws_bytes < need)
+        return fail(YTHIP_EINVAL, "%s: workspace of %zu bytes needed, %zu given", who, need, ws_bytes);
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)d);
+    DecodeArgs a{};
+    a.K = Kc; a.V = Vc; a.O = O;
+    if (O) {
+        a.os0 = o_str[0];
+        a.os1 = o_str[1];
+    }
+    a.ks0 = kv_str[0]; a.ks1 = kv_str[1]; a.ks2 = kv_str[2];
+    a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_ctx = max_ctx;
+    a.splits = decode_splits(B, Hq, max_ctx);
+    a.direct = O != nullptr && a.splits == 1;  // one split: no merge launch
+    a.chunk = (max_ctx + a.splits - 1) / a.splits;
+    a.scale_log2 = scale * LOG2E;
+    a.ws = static_cast<float*>(workspace);
+    a.qkv = qkv; a.ld_qkv = ld_qkv; a.wq = wq; a.wk = wk; a.eps = eps;
+    a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.ld_tab = ld_tab; a.dev_pos = dev_pos;
+    a.fused = 1;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (dtype) {
         case YTHIP_F32: return status_of(launch_decode<F32>(a, d, G, s));

@@ -364,6 +364,40 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out.reshape(q.shape)
 
 
+def decode_splits(B: int, Hq: int, max_ctx: int) -> int:
+    return int(_lib.lib().ythip_attn_decode_splits(B, Hq, max_ctx))
+
+
+def decode_attention_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torch.Tensor | None,
+                          wk: torch.Tensor | None, eps: float, cos: torch.Tensor | None, sin: torch.Tensor | None,
+                          dev_pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                          out: torch.Tensor | None, workspace: torch.Tensor, scale: float = 0.0):
+    """One decode step of a Qwen3 attention layer: the new token's qkv row
+    [B, (Hq + 2 Hkv) d] gets per-head RMSNorm + RoPE at position *dev_pos, k/v
+    are appended to the caches [B, Hkv, max_ctx, d] there, and out [B, Hq, d] =
+    attention over keys 0..*dev_pos -- the same bits as rms_norm_rope followed
+    by decode_attention. With out=None the result stays as split-K partials in
+    `workspace` (decode_workspace_bytes)."""
+    _dev(qkv, k_cache, v_cache, workspace, dev_pos)
+    B = qkv.shape[0]
+    ctx = k_cache.shape[2]
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share strides")
+    if qkv.shape[-1] != (Hq + 2 * Hkv) * d or qkv.stride(-1) != 1:
+        raise ValueError("qkv rows must hold (Hq + 2 Hkv) * d contiguous elements")
+    o3 = None if out is None else out.reshape(B, Hq, d)
+    st = _lib.lib().ythip_attn_decode_rope(
+        _code(qkv), B, Hq, Hkv, d, ctx, qkv.data_ptr(), qkv.stride(0),
+        None if wq is None else wq.data_ptr(), None if wk is None else wk.data_ptr(), float(eps),
+        None if cos is None else cos.data_ptr(), None if sin is None else sin.data_ptr(),
+        0 if cos is None else cos.stride(0), dev_pos.data_ptr(),
+        k_cache.data_ptr(), v_cache.data_ptr(), i64array(k_cache.stride()[:3]),
+        None if o3 is None else o3.data_ptr(), None if o3 is None else i64array(o3.stride()[:2]), float(scale),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream())
+    check(st, "ythip_attn_decode_rope")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # RMSNorm / RoPE
 # ---------------------------------------------------------------------------

@@ -17,9 +17,10 @@ MI355X layout and execution:
     projections write fp32 straight into the residual with beta = 1 (residual
     add fused into the GEMM epilogue); logits fp32;
   * KV cache in the 16-bit type, [layers][1, kv_heads, ctx, head_dim];
-  * a decode step is 7 launches per layer (the RMSNorms ride in the qkv and
-    gate_up GEMV prologues, SwiGLU in the down projection's, the final norm
-    and the argmax in the LM head's) with no host-side value that changes
+  * a decode step is 6 launches per layer (the RMSNorms ride in the qkv and
+    gate_up GEMV prologues, SwiGLU in the down projection's, q/k norm + RoPE +
+    cache append in the split-K attention kernel; the final norm and the argmax
+    ride in the LM head's) with no host-side value that changes
     between steps (token id and positions live in device memory), so it is
     captured once as a HIP graph and replayed per token.
 Every arithmetic operation runs in libythip.so; torch only allocates device
@@ -295,17 +296,18 @@ class Qwen3:
         ops.gemm(self.act[:S], L["down"].t(), x, beta=1.0)        # x += act . Wdown^T
 
     def _layer_decode_fused(self, i: int) -> None:
-        """One token through layer i in 7 launches: the RMSNorms ride in the
-        qkv / gate_up GEMV prologues and SwiGLU in the down projection's."""
+        """One token through layer i in 6 launches: the RMSNorms ride in the
+        qkv / gate_up GEMV prologues, SwiGLU in the down projection's, and the
+        q/k norm + RoPE and cache append in the split-K attention kernel."""
         cfg, L = self.cfg, self.layers[i]
         nh, nkv, hd = cfg.n_heads, cfg.n_kv, cfg.head_dim
         x = self.x[:1]
         kc, vc = self.kc[i], self.vc[i]
         ops.gemv_fused(x, L["qkv"], self.qkv[:1], "rmsnorm", L["n1"], cfg.eps)
-        ops.rms_norm_rope(self.qkv[:1].view(1, 1, -1), nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
-                          q_out=self.qd, k_out=kc, v_out=vc, dev_pos=self.state[1:2])
-        ops.decode_attention(self.qd.view(1, nh, hd), kc, vc, kv_len=self.state[2:3],
-                             out=self.attn[:1].view(1, nh, hd), workspace=self.ws)
+        # q/k norm + RoPE, the K/V append and split-K attention in one launch,
+        # then the merge of the splits
+        ops.decode_attention_rope(self.qkv[:1], nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
+                                  self.state[1:2], kc, vc, self.attn[:1].view(1, nh, hd), self.ws)
         ops.gemv_fused(self.attn[:1], L["o"], x, beta=1.0)                         # x += attn . Wo^T
         ops.gemv_fused(x, L["gu"], self.gu[:1], "rmsnorm", L["n2"], cfg.eps)
         ops.gemv_fused(self.gu[:1], L["down"], x, "swiglu", beta=1.0)             # x += swiglu . Wdown^T
