@@ -314,7 +314,7 @@ def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=No
             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "tokens_generated": int(n_tokens),
             "distinct_tokens": int(len(set(toks.tolist()))),
             "note": "batch 1, greedy, decode step = one HIP graph replay of 171 kernels (6 per layer: "
-                    "RMSNorm and SwiGLU fused into the GEMV prologues, q/k norm + RoPE + cache append into "
+                    "RMSNorm fused into the GEMV prologues, SwiGLU into the gate_up GEMV epilogue, q/k norm + RoPE + cache append into "
                     "the split-K attention kernel)"}
 
 

@@ -268,6 +268,21 @@ int ythip_gemv_fused(int prologue, int dtype_in, int dtype_out, int m, int n, in
                      float beta, float* argmax_parts, void* stream);
 
 /*
+ * The MLP's first half for M <= 16 rows, Qwen3MLP::forward up to the down
+ * projection (qwen3.cpp:193-200): the fused gate_up linear followed by the
+ * SwiGLU, C[m, i] = swish(g) * u with g = A'.W[i]^T and u = A'.W[inter + i]^T
+ * each rounded to dtype first (W = [gate rows | up rows], [2*inter][k], row
+ * stride ldw; C [m][inter], row stride ldc). prologue 0: A' = A (dtype rows);
+ * 1: A' = the rounded rmsNorm_ of fp32 rows A as in ythip_gemv_fused. The bits
+ * equal ythip_gemv_fused(prologue) into a [m][2*inter] buffer followed by
+ * ythip_silu_mul; the [m][2*inter] intermediate is never written. dtype is
+ * bf16 or fp16 (W and C); same alignment rules as ythip_gemv_fused.
+ */
+int ythip_gemv_swiglu(int prologue, int dtype, int m, int inter, int k, const void* A,
+                      int64_t lda, const float* norm_w, float eps, const void* W, int64_t ldw,
+                      void* C, int64_t ldc, void* stream);
+
+/*
  * Greedy selection from ythip_gemv_fused's per-tile pairs (n_parts tiles):
  * same result, tie rule and state update as ythip_argmax_step over the full
  * logits (qwen3.cpp:465-486, argmax as configs[4] specifies).

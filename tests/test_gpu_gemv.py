@@ -138,3 +138,43 @@ def test_gemv_argument_errors(yt, dev):
         yt.gemv_fused(a, w, out)  # more than 16 rows
     with pytest.raises(ValueError):
         yt.gemv_fused(a[:1], w, out[:1], "rmsnorm")  # needs fp32 A and a norm weight
+
+
+@pytest.mark.parametrize("m,inter,k", [(1, 3072, 1024), (3, 1000, 512), (16, 520, 256), (1, 12, 64)])
+@pytest.mark.parametrize("prologue", ["none", "rmsnorm"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemv_swiglu_epilogue_equals_unfused(orc, yt, dev, m, inter, k, prologue, dtype):
+    """gate_up linear + SwiGLU in one launch equals the linear into [m, 2I]
+    followed by silu_mul, bit for bit (I not a multiple of 8 included)."""
+    rng = np.random.default_rng(m * 31 + inter + k)
+    w = torch.from_numpy(rng.standard_normal((2 * inter, k)).astype(np.float32) * 0.05).to(dev).to(dtype)
+    if prologue == "rmsnorm":
+        a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32) * 3).to(dev)
+        nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(k)).astype(np.float32)).to(dev)
+    else:
+        a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev).to(dtype)
+        nw = None
+    out = torch.full((m, inter), 7.0, dtype=dtype, device=dev)
+    yt.gemv_swiglu(a, w, out, prologue, nw, 1e-6)
+    gu = torch.empty((m, 2 * inter), dtype=dtype, device=dev)
+    yt.gemv_fused(a, w, gu, prologue, nw, 1e-6)
+    act = torch.empty((m, inter), dtype=dtype, device=dev)
+    yt.silu_mul(gu, out=act)
+    torch.cuda.synchronize()
+    assert torch.equal(out, act)
+    # against float64 on the rounded gate/up values (the activation bar)
+    g, u = _f32(gu)[:, :inter].astype(np.float64), _f32(gu)[:, inter:].astype(np.float64)
+    ref = g / (1 + np.exp(-g)) * u
+    assert np.abs(_f32(out) - ref).max() <= 1e-2 * max(1.0, np.abs(ref).max())
+
+
+def test_gemv_swiglu_argument_errors(yt, dev):
+    w = torch.zeros((33, 64), dtype=torch.bfloat16, device=dev)
+    a = torch.zeros((1, 64), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        yt.gemv_swiglu(a, w, torch.zeros((1, 16), dtype=torch.bfloat16, device=dev))  # odd row count
+    w = torch.zeros((32, 64), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        yt.gemv_swiglu(a, w, torch.zeros((1, 16), dtype=torch.float32, device=dev))  # out dtype
+    with pytest.raises(ValueError):
+        yt.gemv_swiglu(a, w, torch.zeros((1, 16), dtype=torch.bfloat16, device=dev), "rmsnorm")  # fp32 A needed

@@ -303,7 +303,7 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <class T, class TO, int BM, int BN, int WM, int WN, bool NN, int STAGES>
+template <class T, class TO, int BM, int BN, int WM, int WN, bool NN, int STAGES, int BX = 0>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a) {
     using raw = typename T::raw;
     constexpr int THREADS = 64 * WM * WN;
@@ -321,8 +321,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 
     constexpr int PER = A_PT + B_PT;  // DMA instructions per thread per stage
     static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 2) * PER < 64, "pipeline depth");
+    // BX = 1: B gets a third stage (A keeps two), so B's DMA is issued two k steps
+    // before use; the 256 x 256 tile then fills exactly 160 KB of LDS.
+    static_assert(BX == 0 || (BX == 1 && STAGES == 2), "the extra B stage pairs with the double buffer");
 
-    __shared__ u32x4 sbuf[STAGES * (STA + STB)];
+    __shared__ u32x4 sbuf[STAGES * STA + (STAGES + BX) * STB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -338,7 +341,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
     const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b;
     const int KT = a.k / BK;
 
-    auto issue = [&](int kt, u32x4* sA, u32x4* sB) {
+    auto issue_a = [&](int kt, u32x4* sA) {
         const int k0 = kt * BK;
 #pragma unroll
         for (int i = 0; i < A_PT; ++i) {
@@ -348,6 +351,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
             const int row = min(m0 + r, a.m - 1);
             dma16_async(Ap + (int64_t)row * a.rsa + k0 + c * VEC, &sA[i * THREADS + wave * 64]);
         }
+    };
+    auto issue_b = [&](int kt, u32x4* sB) {
+        const int k0 = kt * BK;
 #pragma unroll
         for (int i = 0; i < B_PT; ++i) {
             const int slot = i * THREADS + wave * 64 + lane;
@@ -364,6 +370,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
             }
             dma16_async(g, &sB[i * THREADS + wave * 64]);
         }
+    };
+    auto issue = [&](int kt, u32x4* sA, u32x4* sB) {
+        issue_a(kt, sA);
+        issue_b(kt, sB);
     };
 
     f32x4 acc[FM][FN];
@@ -429,7 +439,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 
     u32x4* sA = sbuf;
     u32x4* sB = sbuf + STAGES * STA;
-    if constexpr (STAGES == 2) {
+    if constexpr (BX == 1) {
+        // A double-buffered, B triple-buffered. Issue order per iteration: A(kt+1),
+        // then B(kt+2); at the top of iteration kt only B(kt+1) may still be in flight
+        // behind A(kt) and B(kt) (vector-memory ops retire in order).
+        issue_a(0, sA);
+        issue_b(0, sB);
+        if (KT > 1) issue_b(1, sB + STB);
+        for (int kt = 0; kt < KT; ++kt) {
+            if (kt + 1 < KT) wait_vmcnt<B_PT>();
+            else wait_vmcnt<0>();
+            __syncthreads();  // stage kt is in LDS for every wave; stage kt-1 is consumed
+            if (kt + 1 < KT) issue_a(kt + 1, sA + ((kt + 1) & 1) * STA);
+            if (kt + 2 < KT) issue_b(kt + 2, sB + ((kt + 2) % 3) * STB);
+            compute(sA + (kt & 1) * STA, sB + (kt % 3) * STB);
+        }
+    } else if constexpr (STAGES == 2) {
         // Double buffer: DMA of step kt+1 overlaps the MFMAs of step kt.
         issue(0, sA, sB);
         wait_vmcnt<0>();

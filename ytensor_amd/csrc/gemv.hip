@@ -27,6 +27,7 @@
 // that the chip still has enough loads in flight.
 
 #include <cfloat>
+#include <type_traits>
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -50,7 +51,13 @@ __device__ __forceinline__ float silu_ref(float a) {
     return a * sig;
 }
 
-template <class T, class TO, int WAVES, int PRO>
+// EPI = 1 (SwiGLU epilogue): W holds 2n rows, gate rows [0, n) then up rows
+// [n, 2n); a workgroup covers 8 indices i, its MFMA columns 0-7 being gate rows
+// n0 + 0..7 and columns 8-15 the up rows of the same indices, so the epilogue
+// rounds both to the output type (the stored gate_up of the unfused sequence),
+// meets them with one lane exchange and writes swish(gate) * up (silu_mul_kernel's
+// arithmetic) to C [m][n].
+template <class T, class TO, int WAVES, int PRO, int EPI = 0>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     using raw = typename T::raw;
     constexpr int VEC = 16 / sizeof(raw);
@@ -59,14 +66,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     static_assert(PRO == 0 || sizeof(raw) == 2, "fused prologues are 16-bit");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * (EPI ? 8 : 16);
     const int bz = blockIdx.y;
     const int nsteps = (a.k + KSTEP - 1) / KSTEP;
     const int per_wave = (nsteps + WAVES - 1) / WAVES;
     const int s_begin = wave * per_wave, s_end = min(nsteps, s_begin + per_wave);
-    const bool arow = r < a.m, brow = n0 + r < a.n;
+    const bool arow = r < a.m;
+    bool brow;
+    int wrow;
+    if constexpr (EPI == 0) {
+        wrow = n0 + r;
+        brow = wrow < a.n;
+    } else {
+        brow = n0 + (r & 7) < a.n;
+        wrow = (r < 8 ? 0 : a.n) + n0 + (r & 7);
+    }
     const raw* __restrict__ wrp =
-        static_cast<const raw*>(a.W) + bz * a.sw_b + (int64_t)(brow ? n0 + r : 0) * a.ldw + g * VEC;
+        static_cast<const raw*>(a.W) + bz * a.sw_b + (int64_t)(brow ? wrow : 0) * a.ldw + g * VEC;
 
     auto load_w = [&](int s) -> u32x4 {
         const int k = s * KSTEP + g * VEC;
@@ -74,22 +90,63 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
             return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrp + (int64_t)s * KSTEP));
         return u32x4{0u, 0u, 0u, 0u};
     };
-    // The first round of weight loads goes out before the prologue's reduction.
+    // Latency plan: every global load the prologue and epilogue need is issued
+    // right after the first round of weight loads, before anything waits on
+    // memory, so the kernel pays about one memory round trip before the MFMAs.
     u32x4 fb[UNR];
 #pragma unroll
     for (int u = 0; u < UNR; ++u) fb[u] = load_w(s_begin + u);
 
+    using oraw = typename TO::raw;
+    oraw* crow = static_cast<oraw*>(a.C) + bz * a.sc_b + (int64_t)r * a.ldc;
+    float cold[4] = {0.f, 0.f, 0.f, 0.f};  // C for the beta term (wave 0 stores the result)
+    if (EPI == 0 && wave == 0 && arow && a.beta != 0.0f) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (n0 + 4 * g + j < a.n) cold[j] = load_as_f32<TO>(crow, n0 + 4 * g + j);
+    }
+
+    // Prologue operands of the first PJ elements of this thread (element e = tid + j * NT
+    // of the row-major m x k operand), held in registers.
+    constexpr int NT = 64 * WAVES;
+    constexpr int PJ = PRO == 2 ? 8 : 4;
+    const int total = a.m * a.k;
+    float p0[PJ], p1[PJ];
+    auto load_pro = [&](int e, float& x0, float& x1) {
+        const int row = e / a.k, col = e - row * a.k;
+        if constexpr (PRO == 1) {
+            x0 = static_cast<const float*>(a.A)[bz * a.sa_b + (int64_t)row * a.lda + col];
+            x1 = a.nw[col];
+        } else {
+            const raw* gp = static_cast<const raw*>(a.A) + bz * a.sa_b + (int64_t)row * a.lda;
+            x0 = load_as_f32<T>(gp, col);
+            x1 = load_as_f32<T>(gp, a.k + col);
+        }
+    };
+    if constexpr (PRO != 0) {
+#pragma unroll
+        for (int j = 0; j < PJ; ++j) {
+            p0[j] = p1[j] = 0.f;
+            if (tid + j * NT < total) load_pro(tid + j * NT, p0[j], p1[j]);
+        }
+    }
+
     __shared__ float s_part[GEMV_M][4];
     __shared__ float s_den[GEMV_M];
     if constexpr (PRO == 1) {
-        // rms_norm_kernel's reduction, row by row, on the first 256 threads.
+        // rms_norm_kernel's reduction, row by row, on the first 256 threads: the same
+        // sequential FMA order over i = t, t + 256, ... (the four loads of a group go
+        // out together; a zero term leaves the non-negative sum unchanged).
         const float* X = static_cast<const float*>(a.A) + bz * a.sa_b;
         for (int row = 0; row < a.m; ++row) {
             if (tid < 256) {
                 float ss = 0.f;
-                for (int i = tid; i < a.k; i += 256) {
-                    const float v = X[(int64_t)row * a.lda + i];
-                    ss = fmaf(v, v, ss);
+                for (int i = tid; i < a.k; i += 1024) {
+                    float x[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[j] = i + 256 * j < a.k ? X[(int64_t)row * a.lda + i + 256 * j] : 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) ss = fmaf(x[j], x[j], ss);
                 }
                 ss = wave_sum(ss);
                 if (lane == 0) s_part[row][wave] = ss;
@@ -108,18 +165,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     extern __shared__ u32x4 gemv_lds[];  // dynamic: m * k 16-bit values
     raw* sAp = reinterpret_cast<raw*>(gemv_lds);
     if constexpr (PRO != 0) {
-        const int total = a.m * a.k;
-        for (int e = tid; e < total; e += 64 * WAVES) {
-            const int row = e / a.k, col = e - row * a.k;
+        auto finish = [&](int e, float x0, float x1) {
             float y;
-            if constexpr (PRO == 1) {
-                const float* xr = static_cast<const float*>(a.A) + bz * a.sa_b + (int64_t)row * a.lda;
-                y = (xr[col] / s_den[row]) * a.nw[col];
-            } else {
-                const raw* gp = static_cast<const raw*>(a.A) + bz * a.sa_b + (int64_t)row * a.lda;
-                y = silu_ref(load_as_f32<T>(gp, col)) * load_as_f32<T>(gp, a.k + col);
-            }
+            if constexpr (PRO == 1) y = (x0 / s_den[e / a.k]) * x1;
+            else y = silu_ref(x0) * x1;
             sAp[e] = static_cast<raw>(pack2<T>(y, 0.0f) & 0xffffu);
+        };
+#pragma unroll
+        for (int j = 0; j < PJ; ++j)
+            if (tid + j * NT < total) finish(tid + j * NT, p0[j], p1[j]);
+        for (int e = tid + PJ * NT; e < total; e += NT) {
+            float x0, x1;
+            load_pro(e, x0, x1);
+            finish(e, x0, x1);
         }
         __syncthreads();
     }
@@ -154,17 +212,28 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     f32x4 t = red[0][lane];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) t += red[w][lane];
-    using oraw = typename TO::raw;
+    if constexpr (EPI == 1) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float val = a.alpha * t[j];
+            if constexpr (std::is_same<TO, BF16>::value) val = bf16_bits_to_f32(f32_to_bf16_bits(val));
+            if constexpr (std::is_same<TO, F16>::value) val = f16_bits_to_f32(f32_to_f16_bits(val));
+            const float up = __shfl_xor(val, 32, 64);  // lane group g + 2 holds the up rows
+            const int i = n0 + 4 * g + j;
+            if (g < 2 && arow && i < a.n) store_from_f32<TO>(crow, i, silu_ref(val) * up);
+        }
+        return;
+    }
     float v[4];
-    oraw* crow = static_cast<oraw*>(a.C) + bz * a.sc_b + (int64_t)r * a.ldc;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int n = n0 + 4 * g + j;
         v[j] = a.alpha * t[j];
         if (arow && n < a.n) {
-            if (a.beta != 0.0f) v[j] += a.beta * load_as_f32<TO>(crow, n);
+            if (a.beta != 0.0f) v[j] += a.beta * cold[j];
             store_from_f32<TO>(crow, n, v[j]);
-            if constexpr (sizeof(oraw) == 2) v[j] = load_as_f32<TO>(crow, n);  // the value as stored
+            if constexpr (std::is_same<TO, BF16>::value) v[j] = bf16_bits_to_f32(f32_to_bf16_bits(v[j]));  // as stored
+            if constexpr (std::is_same<TO, F16>::value) v[j] = f16_bits_to_f32(f32_to_f16_bits(v[j]));
         }
     }
     if (a.amax != nullptr && bz == 0) {
@@ -229,19 +298,33 @@ __global__ __launch_bounds__(1024) void argmax_finish_kernel(const float* parts,
 
 namespace {
 
-template <class T, class TO, int PRO>
+// Waves per column tile. The kernel holds ~90 VGPRs (5 waves per SIMD, 20 per
+// CU), so a 16-wave workgroup is alone on its CU: 16 waves while the grid fits
+// the 256 CUs in one round (more loads in flight per tile), 8 waves (two
+// workgroups per CU) beyond that. Depends only on the tile count, so a fused
+// call and the unfused sequence it replaces sum the k partials alike.
+inline bool gemv_wide(int64_t tiles) { return tiles <= 256; }
+
+template <class T, class TO, int PRO, int EPI = 0>
 hipError_t launch_gemv_t(const GemvArgs& a, int batch, hipStream_t s) {
-    const int tiles = (a.n + 15) / 16;
-    // fewer than ~2 column tiles per CU: more waves per tile to keep loads in flight
+    const int tiles = EPI ? (a.n + 7) / 8 : (a.n + 15) / 16;
     const size_t lds = PRO == 0 ? 0 : (size_t)a.m * a.k * sizeof(typename T::raw);
-    if ((int64_t)tiles * batch < 512)
-        gemv_kernel<T, TO, 16, PRO><<<dim3(tiles, batch), 1024, lds, s>>>(a);
+    if (gemv_wide((int64_t)tiles * batch))
+        gemv_kernel<T, TO, 16, PRO, EPI><<<dim3(tiles, batch), 1024, lds, s>>>(a);
     else
-        gemv_kernel<T, TO, 8, PRO><<<dim3(tiles, batch), 512, lds, s>>>(a);
+        gemv_kernel<T, TO, 8, PRO, EPI><<<dim3(tiles, batch), 512, lds, s>>>(a);
     return hipGetLastError();
 }
 
 }  // namespace
+
+int gemv_swiglu_dispatch(int prologue, int dtype, const GemvArgs& a, hipStream_t s) {
+    if (dtype == YTHIP_BF16)
+        return status_of(prologue ? launch_gemv_t<BF16, BF16, 1, 1>(a, 1, s) : launch_gemv_t<BF16, BF16, 0, 1>(a, 1, s));
+    if (dtype == YTHIP_F16)
+        return status_of(prologue ? launch_gemv_t<F16, F16, 1, 1>(a, 1, s) : launch_gemv_t<F16, F16, 0, 1>(a, 1, s));
+    return fail(YTHIP_EUNSUPPORTED, "ythip_gemv_swiglu: weights and output must be bf16 or fp16");
+}
 
 int gemv_dispatch(int prologue, int dtype_in, int dtype_out, const GemvArgs& a, int batch, hipStream_t s) {
 #define YTHIP_GEMV(TI, TOUT)                                                          \
@@ -298,6 +381,33 @@ __attribute__((visibility("default"))) int ythip_gemv_fused(int prologue, int dt
     a.m = m; a.n = n; a.k = k; a.alpha = alpha; a.beta = beta;
     a.amax = argmax_parts;
     return gemv_dispatch(prologue, dtype_in, dtype_out, a, 1, static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int ythip_gemv_swiglu(int prologue, int dtype, int m, int inter, int k,
+                                                             const void* A, int64_t lda, const float* norm_w,
+                                                             float eps, const void* W, int64_t ldw, void* C,
+                                                             int64_t ldc, void* stream) {
+    if (prologue < 0 || prologue > 1) return fail(YTHIP_EINVAL, "ythip_gemv_swiglu: prologue %d", prologue);
+    if (m < 0 || inter < 0 || k < 0) return fail(YTHIP_EINVAL, "ythip_gemv_swiglu: negative size");
+    if (m > GEMV_M) return fail(YTHIP_EUNSUPPORTED, "ythip_gemv_swiglu: m = %d (at most %d rows)", m, GEMV_M);
+    if (m == 0 || inter == 0) return 0;
+    if (!A || !W || !C) return fail(YTHIP_EINVAL, "ythip_gemv_swiglu: NULL A, W or C");
+    if (dtype != YTHIP_BF16 && dtype != YTHIP_F16)
+        return fail(YTHIP_EUNSUPPORTED, "ythip_gemv_swiglu: weights and output must be bf16 or fp16");
+    if (prologue == 1 && norm_w == nullptr) return fail(YTHIP_EINVAL, "ythip_gemv_swiglu: the RMSNorm prologue needs norm_w");
+    if (k % 8 || ldw % 8 || (prologue == 1 ? lda % 4 : lda % 8) || lda < k || ldw < k ||
+        (reinterpret_cast<uintptr_t>(A) % 16) || (reinterpret_cast<uintptr_t>(W) % 16) ||
+        (prologue == 1 && (reinterpret_cast<uintptr_t>(norm_w) % 16)))
+        return fail(YTHIP_EUNSUPPORTED, "ythip_gemv_swiglu: rows of A/W must be 16-byte aligned and k a multiple of 8");
+    if (ldc < inter) return fail(YTHIP_EINVAL, "ythip_gemv_swiglu: ldc < inter");
+    if (prologue != 0 && (int64_t)m * k * 2 > GEMV_LDS_MAX)
+        return fail(YTHIP_EUNSUPPORTED, "ythip_gemv_swiglu: m * k = %lld exceeds the %d-byte operand staging",
+                    (long long)m * k, GEMV_LDS_MAX);
+    GemvArgs a{};
+    a.A = A; a.lda = lda; a.nw = norm_w; a.eps = eps;
+    a.W = W; a.ldw = ldw; a.C = C; a.ldc = ldc;
+    a.m = m; a.n = inter; a.k = k; a.alpha = 1.0f; a.beta = 0.0f;
+    return gemv_swiglu_dispatch(prologue, dtype, a, static_cast<hipStream_t>(stream));
 }
 
 __attribute__((visibility("default"))) int ythip_argmax_finish(const float* parts, int n_parts, int32_t* token,

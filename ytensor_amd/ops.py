@@ -551,6 +551,41 @@ def gemv_fused(a: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, prologu
     return out
 
 
+def gemv_swiglu(a: torch.Tensor, gate_up: torch.Tensor, out: torch.Tensor, prologue: str = "none",
+                norm_weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
+    """Qwen3MLP's gate_up linear + SwiGLU for at most 16 rows (qwen3.cpp:193-200):
+    out [m, I] = silu(A' @ gate.T) * (A' @ up.T), gate_up = [gate | up] ([2I, K], the
+    fused weight), both products rounded to the weight type first. prologue "none":
+    A' = a [m, K]; "rmsnorm": A' = rms_norm(a fp32 [m, K], norm_weight, eps). Same
+    bits as gemv_fused into a [m, 2I] buffer followed by silu_mul."""
+    _dev(a, gate_up, out)
+    if prologue not in ("none", "rmsnorm"):
+        raise ValueError("prologue must be 'none' or 'rmsnorm'")
+    pro = GEMV_PROLOGUE[prologue]
+    n2, k = gate_up.shape
+    if n2 % 2:
+        raise ValueError("gate_up must have an even number of rows ([gate | up])")
+    inter = n2 // 2
+    a2 = a.reshape(-1, a.shape[-1])
+    o2 = out.reshape(-1, out.shape[-1])
+    m = a2.shape[0]
+    if o2.shape != (m, inter) or a2.shape[1] != k:
+        raise ValueError(f"a must be [m, {k}] and out [m, {inter}]")
+    if gate_up.stride(1) != 1 or a2.stride(1) != 1 or o2.stride(1) != 1:
+        raise ValueError("gemv_swiglu needs unit column strides")
+    if out.dtype != gate_up.dtype:
+        raise ValueError("out must have the weight's dtype")
+    if a.dtype != (torch.float32 if pro == 1 else gate_up.dtype):
+        raise ValueError(f"A has the wrong dtype for prologue {prologue!r}")
+    if pro == 1 and (norm_weight is None or norm_weight.dtype != torch.float32):
+        raise ValueError("the rmsnorm prologue needs an fp32 norm_weight")
+    check(_lib.lib().ythip_gemv_swiglu(pro, _code(gate_up), m, inter, k, a2.data_ptr(), a2.stride(0),
+                                       None if norm_weight is None else norm_weight.data_ptr(), float(eps),
+                                       gate_up.data_ptr(), gate_up.stride(0), o2.data_ptr(), o2.stride(0),
+                                       _stream()), "ythip_gemv_swiglu")
+    return out
+
+
 def argmax_finish(parts: torch.Tensor, n_parts: int, token: torch.Tensor, history: torch.Tensor | None = None,
                   state: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy token from gemv_fused's per-tile (max, index) pairs; as argmax_step."""

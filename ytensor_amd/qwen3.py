@@ -18,7 +18,7 @@ MI355X layout and execution:
     add fused into the GEMM epilogue); logits fp32;
   * KV cache in the 16-bit type, [layers][1, kv_heads, ctx, head_dim];
   * a decode step is 6 launches per layer (the RMSNorms ride in the qkv and
-    gate_up GEMV prologues, SwiGLU in the down projection's, q/k norm + RoPE +
+    gate_up GEMV prologues, SwiGLU in the gate_up GEMV's epilogue, q/k norm + RoPE +
     cache append in the split-K attention kernel; the final norm and the argmax
     ride in the LM head's) with no host-side value that changes
     between steps (token id and positions live in device memory), so it is
@@ -297,8 +297,10 @@ class Qwen3:
 
     def _layer_decode_fused(self, i: int) -> None:
         """One token through layer i in 6 launches: the RMSNorms ride in the
-        qkv / gate_up GEMV prologues, SwiGLU in the down projection's, and the
-        q/k norm + RoPE and cache append in the split-K attention kernel."""
+        qkv / gate_up GEMV prologues, SwiGLU in the gate_up GEMV's epilogue (each
+        activation computed once, by the workgroup that owns its gate and up
+        rows), and the q/k norm + RoPE and cache append in the split-K attention
+        kernel."""
         cfg, L = self.cfg, self.layers[i]
         nh, nkv, hd = cfg.n_heads, cfg.n_kv, cfg.head_dim
         x = self.x[:1]
@@ -309,8 +311,8 @@ class Qwen3:
         ops.decode_attention_rope(self.qkv[:1], nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
                                   self.state[1:2], kc, vc, self.attn[:1].view(1, nh, hd), self.ws)
         ops.gemv_fused(self.attn[:1], L["o"], x, beta=1.0)                         # x += attn . Wo^T
-        ops.gemv_fused(x, L["gu"], self.gu[:1], "rmsnorm", L["n2"], cfg.eps)
-        ops.gemv_fused(self.gu[:1], L["down"], x, "swiglu", beta=1.0)             # x += swiglu . Wdown^T
+        ops.gemv_swiglu(x, L["gu"], self.act[:1], "rmsnorm", L["n2"], cfg.eps)    # act = swiglu(norm(x) . Wgu^T)
+        ops.gemv_fused(self.act[:1], L["down"], x, beta=1.0)                      # x += act . Wdown^T
 
     def _head(self, S: int) -> None:
         if S == 1 and self.fused:
