@@ -278,6 +278,23 @@ int ythip_gemv_fused(int prologue, int dtype_in, int dtype_out, int m, int n, in
  * ythip_silu_mul; the [m][2*inter] intermediate is never written. dtype is
  * bf16 or fp16 (W and C); same alignment rules as ythip_gemv_fused.
  */
+/*
+ * The attention output projection of a decode step with the split-K merge as
+ * its operand prologue (Qwen3Attention::forward's linear(attn3, o_proj) after
+ * the q_len == 1 attention, qwen3.cpp:254-268; the merge is the combine of
+ * src/kernel/avx2/flash_attention.inl:202-272's per-block softmax state):
+ *   A'[b, h*hd + d] = sum_s 2^(m_s - M) o_s[d] / sum_s 2^(m_s - M) l_s, rounded
+ *   to dtype, over the partials ythip_attn_decode_rope(O = NULL) leaves in its
+ *   workspace (fp32 [m][hq][splits][hd + 2], row stride ld_part floats;
+ *   splits = ythip_attn_decode_splits), then
+ *   C[m, n] = alpha * A' . W[n, hq*hd]^T + beta * C   (dtype W, dtype_out C).
+ * Same bits as the merge inside ythip_attn_decode_rope(O given) followed by
+ * ythip_gemv_fused(prologue 0). The attention output is never written.
+ */
+int ythip_gemv_attn_merge(int dtype, int dtype_out, int m, int n, int hq, int hd, int splits,
+                          const float* partials, int64_t ld_part, const void* W, int64_t ldw,
+                          void* C, int64_t ldc, float alpha, float beta, void* stream);
+
 int ythip_gemv_swiglu(int prologue, int dtype, int m, int inter, int k, const void* A,
                       int64_t lda, const float* norm_w, float eps, const void* W, int64_t ldw,
                       void* C, int64_t ldc, void* stream);

@@ -228,3 +228,46 @@ def test_decode_attention_rope_equals_unfused(orc, yt, dtype, Hq, Hkv, d):
         nparts = B * Hq * yt.ops.decode_splits(B, Hq, max_ctx) * (d + 2) * 4
         assert torch.equal(ws3[:nparts], ws2[:nparts]), (dtype, pos)
         assert torch.equal(kc3, kc2) and torch.equal(vc3, vc2)
+
+
+@pytest.mark.parametrize("dtype,out_dtype", [("bf16", torch.float32), ("bf16", torch.bfloat16), ("f16", torch.float32)])
+@pytest.mark.parametrize("B,Hq,Hkv,d,max_ctx", [(1, 16, 8, 128, 1000), (3, 8, 2, 64, 300), (2, 16, 8, 128, 40)])
+def test_gemv_attn_merge_equals_merge_then_gemv(yt, dtype, out_dtype, B, Hq, Hkv, d, max_ctx):
+    """The o projection with the split-K merge as its prologue equals the merged
+    attention output (decode_attention_rope with O) fed to gemv_fused, bit for
+    bit, including positions where some splits hold no key (m = -inf)."""
+    rng = np.random.default_rng(B * 100 + Hq + d + max_ctx)
+    dt = TORCH_DT[dtype]
+    width = (Hq + 2 * Hkv) * d
+    N = 320
+    kc = torch.from_numpy(rng.standard_normal((B, Hkv, max_ctx, d)).astype(np.float32)).to("cuda").to(dt)
+    vc = torch.from_numpy(rng.standard_normal((B, Hkv, max_ctx, d)).astype(np.float32)).to("cuda").to(dt)
+    w = torch.from_numpy(rng.standard_normal((N, Hq * d)).astype(np.float32) * 0.05).to("cuda").to(dt)
+    ws = torch.empty(yt.ops.decode_workspace_bytes(B, Hq, max_ctx, d), dtype=torch.uint8, device="cuda")
+    splits = yt.ops.decode_splits(B, Hq, max_ctx)
+    for pos in sorted({0, 1, max_ctx // 3, max_ctx - 1}):
+        qkv = torch.from_numpy(rng.standard_normal((B, width)).astype(np.float32)).to("cuda").to(dt)
+        p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        base = torch.from_numpy(rng.standard_normal((B, N)).astype(np.float32)).to("cuda").to(out_dtype)
+        attn = torch.empty((B, Hq, d), dtype=dt, device="cuda")
+        k1, v1 = kc.clone(), vc.clone()
+        yt.ops.decode_attention_rope(qkv, Hq, Hkv, d, None, None, 1e-6, None, None, p, k1, v1, attn, ws)
+        want = base.clone()
+        yt.gemv_fused(attn.view(B, Hq * d), w, want, alpha=0.5, beta=1.0)
+        k2, v2 = kc.clone(), vc.clone()
+        yt.ops.decode_attention_rope(qkv, Hq, Hkv, d, None, None, 1e-6, None, None, p, k2, v2, None, ws)
+        got = base.clone()
+        yt.gemv_attn_merge(ws, B, Hq, d, max_ctx, w, got, alpha=0.5, beta=1.0)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (pos, splits)
+        assert torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
+def test_gemv_attn_merge_argument_errors(yt):
+    w = torch.zeros((32, 2048), dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros((1, 32), dtype=torch.float32, device="cuda")
+    ws = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):
+        yt.gemv_attn_merge(ws, 1, 16, 128, 1000, w, out)  # workspace too small
+    with pytest.raises(ValueError):
+        yt.gemv_attn_merge(ws, 1, 8, 128, 1000, w, out)  # weight width != Hq * d

@@ -14,6 +14,7 @@ from .ops import (  # noqa: F401
     embedding,
     gemm,
     gemm_masked,
+    gemv_attn_merge,
     gemv_fused,
     gemv_swiglu,
     linear,
@@ -35,5 +36,5 @@ def load():
 __all__ = [
     "YthipError", "lib", "gemm", "matmul", "linear", "scaled_dot_product_attention",
     "decode_attention", "rms_norm", "rms_norm_rope", "silu_mul", "embedding", "argmax_step",
-    "gemv_fused", "gemv_swiglu", "argmax_finish", "io", "masked_matmul", "gemm_masked",
+    "gemv_fused", "gemv_swiglu", "gemv_attn_merge", "argmax_finish", "io", "masked_matmul", "gemm_masked",
 ]

@@ -35,6 +35,10 @@
 namespace ythip {
 
 constexpr int GEMV_M = 16;
+// Single-row GEMVs up to this many output rows run gemv_row_kernel (every
+// decode-step linear); wider ones (the LM head) keep the MFMA-reducer kernel,
+// whose 16-column tiles amortise the per-workgroup prologue better.
+constexpr int GEMV_ROW_MAX_N = 32768;
 constexpr int GEMV_LDS_MAX = 64 * 1024;  // bytes of the staged A' (prologues 1 and 2)
 
 
@@ -51,6 +55,212 @@ __device__ __forceinline__ float silu_ref(float a) {
     return a * sig;
 }
 
+// Operand prologues of the decode GEMVs: build A' [m][k] (16-bit, row-major) in
+// the dynamic LDS. load() issues the prologue's global loads into registers and
+// runs BEFORE the weight loads: vector-memory loads retire in issue order, so
+// the prologue's first wait then covers only its own (small, cache-resident)
+// inputs and its arithmetic overlaps the weight stream. build() does the
+// arithmetic (loading directly whatever did not fit in the registers) and ends
+// with a barrier. All NT threads of the workgroup take part.
+//   PRO 1: RMSNorm of fp32 rows (rms_norm_kernel's arithmetic and order);
+//   PRO 2: swish(gate) * up of 16-bit rows [gate | up] (silu_mul_kernel's);
+//   PRO 3: the split-K decode merge (attn_decode_merge's): per (row, head) the
+//          max M of the splits' m, weights w_s = 2^(m_s - M) (-inf marks a split
+//          merge skips) and L = sum w_s l_s, then o = sum_s w_s o_s[d] / L.
+template <class T, int NT, int PRO>
+struct GemvPrologue {
+    using raw = typename T::raw;
+    static constexpr bool EW = PRO == 1 || PRO == 2;  // elementwise prologues
+    static constexpr int PJ = PRO == 2 ? 8 : 4;        // elements per thread held in registers
+    static constexpr int MS = 8;                       // merge: splits held in registers
+    float p0[EW ? PJ : 1], p1[EW ? PJ : 1];
+    float xr[PRO == 1 ? 4 : 1];                        // RMSNorm: first reduction group of row 0
+    float opre[PRO == 3 ? 2 : 1][PRO == 3 ? MS : 1];   // merge: o of this thread's 2 elements
+    float mreg[PRO == 3 ? MS : 1], lreg[PRO == 3 ? MS : 1];
+
+    __device__ __forceinline__ void load_elem(const GemvArgs& a, int bz, int e, float& x0, float& x1) const {
+        const int row = e / a.k, col = e - row * a.k;
+        if constexpr (PRO == 1) {
+            x0 = static_cast<const float*>(a.A)[bz * a.sa_b + (int64_t)row * a.lda + col];
+            x1 = a.nw[col];
+        } else {
+            const raw* gp = static_cast<const raw*>(a.A) + bz * a.sa_b + (int64_t)row * a.lda;
+            x0 = load_as_f32<T>(gp, col);
+            x1 = load_as_f32<T>(gp, a.k + col);
+        }
+    }
+    __device__ __forceinline__ const float* merge_src(const GemvArgs& a, int bz, int e) const {
+        const int row = e / a.k, col = e - row * a.k;
+        const int h = col / a.hd, d = col - h * a.hd;
+        return static_cast<const float*>(a.A) + bz * a.sa_b + (int64_t)row * a.lda +
+               (int64_t)h * a.splits * (a.hd + 2) + 2 + d;
+    }
+    __device__ __forceinline__ const float* merge_msrc(const GemvArgs& a, int bz, int rh) const {
+        return static_cast<const float*>(a.A) + bz * a.sa_b + (int64_t)(rh / a.hq) * a.lda +
+               (int64_t)(rh % a.hq) * a.splits * (a.hd + 2);
+    }
+
+    __device__ __forceinline__ void load(const GemvArgs& a, int bz) {
+        const int tid = threadIdx.x, total = a.m * a.k;
+        if constexpr (EW) {
+#pragma unroll
+            for (int j = 0; j < PJ; ++j) {
+                p0[j] = p1[j] = 0.f;
+                if (tid + j * NT < total) load_elem(a, bz, tid + j * NT, p0[j], p1[j]);
+            }
+        }
+        if constexpr (PRO == 1) {
+            const float* X = static_cast<const float*>(a.A) + bz * a.sa_b;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xr[j] = (tid < 256 && tid + 256 * j < a.k) ? X[tid + 256 * j] : 0.f;
+        }
+        if constexpr (PRO == 3) {
+            const int S = a.splits, stride = a.hd + 2;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int e = tid + j * NT;
+                const float* src = merge_src(a, bz, e < total ? e : 0);
+#pragma unroll
+                for (int q = 0; q < MS; ++q) opre[j][q] = (e < total && q < S) ? src[q * stride] : 0.f;
+            }
+            const bool owner = tid < a.m * a.hq;
+            const float* msrc = merge_msrc(a, bz, owner ? tid : 0);
+#pragma unroll
+            for (int q = 0; q < MS; ++q) {
+                mreg[q] = (owner && q < S) ? msrc[q * stride] : -INFINITY;
+                lreg[q] = (owner && q < S) ? msrc[q * stride + 1] : 0.f;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void build(const GemvArgs& a, int bz, raw* sAp) {
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, total = a.m * a.k;
+        if constexpr (PRO == 1) {
+            __shared__ float s_part[GEMV_M][4];
+            __shared__ float s_den[GEMV_M];
+            // rms_norm_kernel's reduction, row by row, on the first 256 threads: the
+            // sequential FMA order over i = t, t + 256, ...; a zero term leaves the
+            // non-negative sum unchanged.
+            const float* X = static_cast<const float*>(a.A) + bz * a.sa_b;
+            for (int row = 0; row < a.m; ++row) {
+                if (tid < 256) {
+                    float ss = 0.f;
+                    for (int i = tid; i < a.k; i += 1024) {
+                        float x[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            x[j] = (row == 0 && i == tid) ? xr[j]
+                                                          : (i + 256 * j < a.k ? X[(int64_t)row * a.lda + i + 256 * j] : 0.f);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) ss = fmaf(x[j], x[j], ss);
+                    }
+                    ss = wave_sum(ss);
+                    if (lane == 0) s_part[row][wave] = ss;
+                }
+            }
+            __syncthreads();
+            if (tid < a.m) {
+                const float tot = (s_part[tid][0] + s_part[tid][1]) + (s_part[tid][2] + s_part[tid][3]);
+                s_den[tid] = sqrtf(tot / (float)a.k + a.eps);
+            }
+            __syncthreads();
+            auto finish = [&](int e, float x0, float x1) {
+                const float y = (x0 / s_den[e / a.k]) * x1;
+                sAp[e] = static_cast<raw>(pack2<T>(y, 0.0f) & 0xffffu);
+            };
+#pragma unroll
+            for (int j = 0; j < PJ; ++j)
+                if (tid + j * NT < total) finish(tid + j * NT, p0[j], p1[j]);
+            for (int e = tid + PJ * NT; e < total; e += NT) {
+                float x0, x1;
+                load_elem(a, bz, e, x0, x1);
+                finish(e, x0, x1);
+            }
+            __syncthreads();
+        }
+        if constexpr (PRO == 2) {
+            auto finish = [&](int e, float x0, float x1) {
+                const float y = silu_ref(x0) * x1;
+                sAp[e] = static_cast<raw>(pack2<T>(y, 0.0f) & 0xffffu);
+            };
+#pragma unroll
+            for (int j = 0; j < PJ; ++j)
+                if (tid + j * NT < total) finish(tid + j * NT, p0[j], p1[j]);
+            for (int e = tid + PJ * NT; e < total; e += NT) {
+                float x0, x1;
+                load_elem(a, bz, e, x0, x1);
+                finish(e, x0, x1);
+            }
+            __syncthreads();
+        }
+        if constexpr (PRO == 3) {
+            const int S = a.splits, hs = a.hq * S, stride = a.hd + 2;
+            float* s_w = reinterpret_cast<float*>(sAp + ((total + 7) & ~7));
+            float* s_L = s_w + a.m * hs;
+            if (tid < a.m * a.hq) {  // this thread owns (row, head) rh = tid
+                const float* msrc = merge_msrc(a, bz, tid);
+                float M = -INFINITY;
+#pragma unroll
+                for (int q = 0; q < MS; ++q)
+                    if (q < S) M = fmaxf(M, mreg[q]);
+                for (int q = MS; q < S; ++q) M = fmaxf(M, msrc[q * stride]);
+                float L = 0.f;
+                float* w = s_w + tid * S;
+#pragma unroll
+                for (int q = 0; q < MS; ++q) {
+                    if (q < S) {
+                        float ws = -INFINITY;
+                        if (M != -INFINITY && mreg[q] != -INFINITY) {
+                            ws = exp2f(mreg[q] - M);
+                            L = fmaf(lreg[q], ws, L);
+                        }
+                        w[q] = ws;
+                    }
+                }
+                for (int q = MS; q < S; ++q) {
+                    const float ms = msrc[q * stride];
+                    float ws = -INFINITY;
+                    if (M != -INFINITY && ms != -INFINITY) {
+                        ws = exp2f(ms - M);
+                        L = fmaf(msrc[q * stride + 1], ws, L);
+                    }
+                    w[q] = ws;
+                }
+                s_L[tid] = L;
+            }
+            __syncthreads();
+            // pre: the element's first MS partial values, in registers (or not)
+            auto merge_one = [&](int e, const float (&pre)[MS], bool have_pre) {
+                const int row = e / a.k, col = e - row * a.k;
+                const int rh = row * a.hq + col / a.hd;
+                const float* src = merge_src(a, bz, e);
+                const float* w = s_w + rh * S;
+                float acc = 0.f;
+#pragma unroll
+                for (int q = 0; q < MS; ++q) {
+                    if (q < S) {
+                        const float ws = w[q];
+                        const float o = have_pre ? pre[q] : src[q * stride];
+                        if (ws != -INFINITY) acc = fmaf(o, ws, acc);
+                    }
+                }
+                for (int q = MS; q < S; ++q) {
+                    const float ws = w[q];
+                    if (ws != -INFINITY) acc = fmaf(src[q * stride], ws, acc);
+                }
+                const float L = s_L[rh];
+                const float y = L > 0.f ? acc / L : 0.f;
+                sAp[e] = static_cast<raw>(pack2<T>(y, 0.0f) & 0xffffu);
+            };
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (tid + j * NT < total) merge_one(tid + j * NT, opre[j], true);
+            for (int e = tid + 2 * NT; e < total; e += NT) merge_one(e, opre[0], false);
+            __syncthreads();
+        }
+    }
+};
+
 // EPI = 1 (SwiGLU epilogue): W holds 2n rows, gate rows [0, n) then up rows
 // [n, 2n); a workgroup covers 8 indices i, its MFMA columns 0-7 being gate rows
 // n0 + 0..7 and columns 8-15 the up rows of the same indices, so the epilogue
@@ -64,6 +274,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     constexpr int KSTEP = 4 * VEC;  // k covered by one MFMA chunk across the 4 lane groups
     constexpr int UNR = 8;
     static_assert(PRO == 0 || sizeof(raw) == 2, "fused prologues are 16-bit");
+    static_assert(EPI == 0 || PRO <= 1, "the SwiGLU epilogue takes prologue 0 or 1");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.x * (EPI ? 8 : 16);
@@ -90,9 +301,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
             return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrp + (int64_t)s * KSTEP));
         return u32x4{0u, 0u, 0u, 0u};
     };
-    // Latency plan: every global load the prologue and epilogue need is issued
-    // right after the first round of weight loads, before anything waits on
-    // memory, so the kernel pays about one memory round trip before the MFMAs.
+    // Latency plan: the prologue's loads, then the first round of weight loads,
+    // then the epilogue's, all before anything waits on memory.
+    GemvPrologue<T, 64 * WAVES, PRO> pro;
+    if constexpr (PRO != 0) pro.load(a, bz);
     u32x4 fb[UNR];
 #pragma unroll
     for (int u = 0; u < UNR; ++u) fb[u] = load_w(s_begin + u);
@@ -106,81 +318,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
             if (n0 + 4 * g + j < a.n) cold[j] = load_as_f32<TO>(crow, n0 + 4 * g + j);
     }
 
-    // Prologue operands of the first PJ elements of this thread (element e = tid + j * NT
-    // of the row-major m x k operand), held in registers.
-    constexpr int NT = 64 * WAVES;
-    constexpr int PJ = PRO == 2 ? 8 : 4;
-    const int total = a.m * a.k;
-    float p0[PJ], p1[PJ];
-    auto load_pro = [&](int e, float& x0, float& x1) {
-        const int row = e / a.k, col = e - row * a.k;
-        if constexpr (PRO == 1) {
-            x0 = static_cast<const float*>(a.A)[bz * a.sa_b + (int64_t)row * a.lda + col];
-            x1 = a.nw[col];
-        } else {
-            const raw* gp = static_cast<const raw*>(a.A) + bz * a.sa_b + (int64_t)row * a.lda;
-            x0 = load_as_f32<T>(gp, col);
-            x1 = load_as_f32<T>(gp, a.k + col);
-        }
-    };
-    if constexpr (PRO != 0) {
-#pragma unroll
-        for (int j = 0; j < PJ; ++j) {
-            p0[j] = p1[j] = 0.f;
-            if (tid + j * NT < total) load_pro(tid + j * NT, p0[j], p1[j]);
-        }
-    }
-
-    __shared__ float s_part[GEMV_M][4];
-    __shared__ float s_den[GEMV_M];
-    if constexpr (PRO == 1) {
-        // rms_norm_kernel's reduction, row by row, on the first 256 threads: the same
-        // sequential FMA order over i = t, t + 256, ... (the four loads of a group go
-        // out together; a zero term leaves the non-negative sum unchanged).
-        const float* X = static_cast<const float*>(a.A) + bz * a.sa_b;
-        for (int row = 0; row < a.m; ++row) {
-            if (tid < 256) {
-                float ss = 0.f;
-                for (int i = tid; i < a.k; i += 1024) {
-                    float x[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) x[j] = i + 256 * j < a.k ? X[(int64_t)row * a.lda + i + 256 * j] : 0.f;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) ss = fmaf(x[j], x[j], ss);
-                }
-                ss = wave_sum(ss);
-                if (lane == 0) s_part[row][wave] = ss;
-            }
-        }
-        __syncthreads();
-        if (tid < a.m) {
-            const float tot = (s_part[tid][0] + s_part[tid][1]) + (s_part[tid][2] + s_part[tid][3]);
-            s_den[tid] = sqrtf(tot / (float)a.k + a.eps);
-        }
-        __syncthreads();
-    }
-    // Prologues 1 and 2 build A' [m][k] once per workgroup in LDS (every thread
-    // takes whole elements, so no lane idles on the m < 16 padding rows), then the
-    // waves read their operand chunks from there.
-    extern __shared__ u32x4 gemv_lds[];  // dynamic: m * k 16-bit values
+    extern __shared__ u32x4 gemv_lds[];  // dynamic: m * k 16-bit values (+ prologue 3's tables)
     raw* sAp = reinterpret_cast<raw*>(gemv_lds);
-    if constexpr (PRO != 0) {
-        auto finish = [&](int e, float x0, float x1) {
-            float y;
-            if constexpr (PRO == 1) y = (x0 / s_den[e / a.k]) * x1;
-            else y = silu_ref(x0) * x1;
-            sAp[e] = static_cast<raw>(pack2<T>(y, 0.0f) & 0xffffu);
-        };
-#pragma unroll
-        for (int j = 0; j < PJ; ++j)
-            if (tid + j * NT < total) finish(tid + j * NT, p0[j], p1[j]);
-        for (int e = tid + PJ * NT; e < total; e += NT) {
-            float x0, x1;
-            load_pro(e, x0, x1);
-            finish(e, x0, x1);
-        }
-        __syncthreads();
-    }
+    if constexpr (PRO != 0) pro.build(a, bz, sAp);
 
     // A operand chunk s of this lane: 8 (16-bit) or 4 (fp32) k values of row r.
     auto load_a = [&](int s) -> u32x4 {
@@ -258,6 +398,190 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     }
 }
 
+// Sum over the 64 lanes with DPP row operations (quad swaps, half-row and row
+// mirrors, then the row broadcasts of gfx9): the total lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float dpp_sum_to_lane63(float v) {
+    v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+    v = dpp_add<0x140, 0xf>(v);  // row_mirror
+    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// 16 bytes of 16-bit weights . 16 bytes of the 16-bit operand, fp32 accumulate
+// (v_dot2_f32_bf16 / v_dot2_f32_f16: the products are exact in fp32).
+__device__ __forceinline__ float dot8(BF16, u32x4 w, u32x4 x, float acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        // element copies first: hipcc (clang 22) folds a bit_cast of a vector
+        // element expression to element 0
+        const uint32_t we = w[e], xe = x[e];
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, we), __builtin_bit_cast(bf16x2_t, xe), acc,
+                                              false);
+    }
+    return acc;
+}
+__device__ __forceinline__ float dot8(F16, u32x4 w, u32x4 x, float acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t we = w[e], xe = x[e];  // see dot8(BF16, ...)
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, we), __builtin_bit_cast(f16x2_t, xe), acc, false);
+    }
+    return acc;
+}
+__device__ __forceinline__ float dot8(F32, u32x4 w, u32x4 x, float acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = fmaf(__uint_as_float(w[e]), __uint_as_float(x[e]), acc);
+    return acc;
+}
+
+// Decode GEMV for ONE activation row (m == 1), the shape of every decode-step
+// linear. A wave owns RPW whole weight rows: lane l takes the 16-byte chunks
+// c = l, l + 64, ... of a row, so one load instruction reads 1 KB of one row
+// (full 128-byte lines, unlike the MFMA layout's 64-byte pieces of 16 rows),
+// all chunks of a round go out before any is used, and the row's dot product
+// is the lane's in-order partial followed by one DPP wave sum. Each row is
+// computed entirely inside one wave in a fixed order, so its bits do not
+// depend on the workgroup shape, the prologue or the epilogue: a fused call
+// and the unfused sequence it replaces agree bit for bit.
+//   EPI 0: C[n] = alpha * dot + beta * C; optional per-workgroup (max, index)
+//          pairs for the LM-head argmax (WAVES * RPW rows per workgroup).
+//   EPI 1: RPW = 2, rows (i, n + i) of W = [gate | up]; C[i] = swish(g) * u with
+//          g, u rounded to TO first (silu_mul_kernel after a 16-bit gate_up).
+template <class T, class TO, int WAVES, int RPW, int PRO, int EPI>
+__global__ __launch_bounds__(64 * WAVES) void gemv_row_kernel(GemvArgs a) {
+    using raw = typename T::raw;
+    constexpr int VEC = 16 / sizeof(raw);
+    // chunks per lane per round (16-wave workgroups hold fewer: 128 VGPRs a lane)
+    constexpr int CPL = (sizeof(raw) == 2 && WAVES < 16) ? 8 : 4;
+    static_assert(PRO == 0 || sizeof(raw) == 2, "fused prologues are 16-bit");
+    static_assert(EPI == 0 || (RPW == 2 && PRO <= 1), "the SwiGLU epilogue pairs a gate and an up row");
+    static_assert(PRO == 0 || WAVES >= 4, "the RMSNorm prologue reduces on 256 threads");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch = a.k / VEC;
+    int rows[RPW];
+    bool rok[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        if constexpr (EPI == 1) {
+            const int i = blockIdx.x * WAVES + wave;
+            rok[j] = i < a.n;
+            rows[j] = j == 0 ? i : a.n + i;
+        } else {
+            rows[j] = (blockIdx.x * WAVES + wave) * RPW + j;
+            rok[j] = rows[j] < a.n;
+        }
+    }
+    const raw* Wp = static_cast<const raw*>(a.W);
+    auto load_round = [&](int c0, u32x4 (&w)[RPW][CPL]) {
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) {
+            const raw* wr = Wp + (int64_t)(rok[j] ? rows[j] : 0) * a.ldw;
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) {
+                const int c = c0 + lane + 64 * u;
+                w[j][u] = (rok[j] && c < nch) ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr) + c)
+                                              : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    GemvPrologue<T, 64 * WAVES, PRO> pro;  // its loads go out first (see GemvPrologue)
+    if constexpr (PRO != 0) pro.load(a, 0);
+    u32x4 w[RPW][CPL];
+    load_round(0, w);
+
+    using oraw = typename TO::raw;
+    oraw* Cp = static_cast<oraw*>(a.C);
+    float cold[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) cold[j] = (EPI == 0 && a.beta != 0.0f && rok[j]) ? load_as_f32<TO>(Cp, rows[j]) : 0.f;
+
+    extern __shared__ u32x4 gemv_lds[];
+    raw* sAp = reinterpret_cast<raw*>(gemv_lds);
+    auto load_x = [&](int c) -> u32x4 {
+        if (c >= nch) return u32x4{0u, 0u, 0u, 0u};
+        if constexpr (PRO == 0) return reinterpret_cast<const u32x4*>(a.A)[c];
+        else return reinterpret_cast<const u32x4*>(sAp)[c];
+    };
+    u32x4 x[CPL];
+    if constexpr (PRO == 0) {
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) x[u] = load_x(lane + 64 * u);
+    } else {
+        pro.build(a, 0, sAp);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) x[u] = load_x(lane + 64 * u);
+    }
+
+    float acc[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
+    for (int c0 = 0;;) {
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) acc[j] = dot8(T{}, w[j][u], x[u], acc[j]);
+        c0 += 64 * CPL;
+        if (c0 >= nch) break;
+        load_round(c0, w);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) x[u] = load_x(c0 + lane + 64 * u);
+    }
+    float tot[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) tot[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dpp_sum_to_lane63(acc[j])), 63));
+
+    if constexpr (EPI == 1) {
+        float g = a.alpha * tot[0], u = a.alpha * tot[1];
+        if constexpr (std::is_same<TO, BF16>::value) {
+            g = bf16_bits_to_f32(f32_to_bf16_bits(g));
+            u = bf16_bits_to_f32(f32_to_bf16_bits(u));
+        }
+        if constexpr (std::is_same<TO, F16>::value) {
+            g = f16_bits_to_f32(f32_to_f16_bits(g));
+            u = f16_bits_to_f32(f32_to_f16_bits(u));
+        }
+        if (lane == 0 && rok[0]) store_from_f32<TO>(Cp, rows[0], silu_ref(g) * u);
+        return;
+    }
+    float v[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        v[j] = a.alpha * tot[j];
+        if (a.beta != 0.0f) v[j] += a.beta * cold[j];
+        if (lane == 0 && rok[j]) store_from_f32<TO>(Cp, rows[j], v[j]);
+        if constexpr (std::is_same<TO, BF16>::value) v[j] = bf16_bits_to_f32(f32_to_bf16_bits(v[j]));  // as stored
+        if constexpr (std::is_same<TO, F16>::value) v[j] = f16_bits_to_f32(f32_to_f16_bits(v[j]));
+    }
+    if (a.amax != nullptr) {
+        // the workgroup's rows: lowest index wins ties, NaN never wins
+        float best = -INFINITY;
+        int idx = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+            if (rok[j] && (v[j] > best || (v[j] == best && rows[j] < idx))) { best = v[j]; idx = rows[j]; }
+        __shared__ float s_best[WAVES];
+        __shared__ int s_idx[WAVES];
+        if (lane == 0) {
+            s_best[wave] = best;
+            s_idx[wave] = idx;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w2 = 1; w2 < WAVES; ++w2)
+                if (s_best[w2] > best || (s_best[w2] == best && s_idx[w2] < idx)) { best = s_best[w2]; idx = s_idx[w2]; }
+            a.amax[2 * blockIdx.x] = best;
+            a.amax[2 * blockIdx.x + 1] = __int_as_float(idx);
+        }
+    }
+}
+
 // Final greedy step over the per-tile (max, index) pairs; same tie rule and
 // state update as argmax_step_kernel.
 __global__ __launch_bounds__(1024) void argmax_finish_kernel(const float* parts, int n_parts, int32_t* token,
@@ -305,10 +629,30 @@ namespace {
 // call and the unfused sequence it replaces sum the k partials alike.
 inline bool gemv_wide(int64_t tiles) { return tiles <= 256; }
 
+template <class T, class TO, int WAVES, int RPW, int PRO, int EPI>
+hipError_t launch_row_t(const GemvArgs& a, size_t lds, hipStream_t s) {
+    const int per_wg = EPI ? WAVES : WAVES * RPW;
+    gemv_row_kernel<T, TO, WAVES, RPW, PRO, EPI><<<(a.n + per_wg - 1) / per_wg, 64 * WAVES, lds, s>>>(a);
+    return hipGetLastError();
+}
+
 template <class T, class TO, int PRO, int EPI = 0>
 hipError_t launch_gemv_t(const GemvArgs& a, int batch, hipStream_t s) {
+    if (a.m == 1 && batch == 1 && a.n <= GEMV_ROW_MAX_N) {
+        // One activation row: the row-per-wave kernel, whose bits do not depend on
+        // the workgroup shape, so each variant takes the shape measured fastest on
+        // the decode shapes: 4 rows per workgroup without a prologue; 16 waves
+        // where a prologue is built once per workgroup (fewer copies of it) or the
+        // argmax wants 16-row tiles; 16 gate/up pairs with the SwiGLU epilogue.
+        size_t lds = PRO == 0 ? 0 : (size_t)a.k * sizeof(typename T::raw);
+        if (PRO == 3) lds = ((size_t)a.k + 7) / 8 * 16 + ((size_t)a.hq * a.splits + (size_t)a.hq) * 4;
+        if constexpr (EPI == 1) return launch_row_t<T, TO, 16, 2, PRO, 1>(a, lds, s);
+        if (PRO != 0 || a.amax != nullptr) return launch_row_t<T, TO, 16, 1, PRO, 0>(a, lds, s);
+        return launch_row_t<T, TO, 4, 1, PRO, 0>(a, lds, s);
+    }
     const int tiles = EPI ? (a.n + 7) / 8 : (a.n + 15) / 16;
-    const size_t lds = PRO == 0 ? 0 : (size_t)a.m * a.k * sizeof(typename T::raw);
+    size_t lds = PRO == 0 ? 0 : (size_t)a.m * a.k * sizeof(typename T::raw);
+    if (PRO == 3) lds = ((size_t)a.m * a.k + 7) / 8 * 16 + ((size_t)a.m * a.hq * a.splits + (size_t)a.m * a.hq) * 4;
     if (gemv_wide((int64_t)tiles * batch))
         gemv_kernel<T, TO, 16, PRO, EPI><<<dim3(tiles, batch), 1024, lds, s>>>(a);
     else
@@ -317,6 +661,14 @@ hipError_t launch_gemv_t(const GemvArgs& a, int batch, hipStream_t s) {
 }
 
 }  // namespace
+
+int gemv_merge_dispatch(int dtype_in, int dtype_out, const GemvArgs& a, hipStream_t s) {
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_BF16) return status_of(launch_gemv_t<BF16, BF16, 3>(a, 1, s));
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_F32) return status_of(launch_gemv_t<BF16, F32, 3>(a, 1, s));
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F16) return status_of(launch_gemv_t<F16, F16, 3>(a, 1, s));
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F32) return status_of(launch_gemv_t<F16, F32, 3>(a, 1, s));
+    return fail(YTHIP_EUNSUPPORTED, "ythip_gemv_attn_merge: unsupported dtype/dtype_out %d/%d", dtype_in, dtype_out);
+}
 
 int gemv_swiglu_dispatch(int prologue, int dtype, const GemvArgs& a, hipStream_t s) {
     if (dtype == YTHIP_BF16)
@@ -408,6 +760,33 @@ __attribute__((visibility("default"))) int ythip_gemv_swiglu(int prologue, int d
     a.W = W; a.ldw = ldw; a.C = C; a.ldc = ldc;
     a.m = m; a.n = inter; a.k = k; a.alpha = 1.0f; a.beta = 0.0f;
     return gemv_swiglu_dispatch(prologue, dtype, a, static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int ythip_gemv_attn_merge(int dtype, int dtype_out, int m, int n, int hq,
+                                                                 int hd, int splits, const float* partials,
+                                                                 int64_t ld_part, const void* W, int64_t ldw, void* C,
+                                                                 int64_t ldc, float alpha, float beta, void* stream) {
+    const char* who = "ythip_gemv_attn_merge";
+    if (m < 0 || n < 0 || hq < 0 || hd <= 0 || splits <= 0) return fail(YTHIP_EINVAL, "%s: bad size", who);
+    if (m > GEMV_M) return fail(YTHIP_EUNSUPPORTED, "%s: m = %d (at most %d rows)", who, m, GEMV_M);
+    if (m == 0 || n == 0 || hq == 0) return 0;
+    if (!partials || !W || !C) return fail(YTHIP_EINVAL, "%s: NULL partials, W or C", who);
+    const int64_t k = (int64_t)hq * hd;
+    if (hd % 8 || ldw % 8 || ldw < k || (reinterpret_cast<uintptr_t>(W) % 16) ||
+        (reinterpret_cast<uintptr_t>(partials) % 4))
+        return fail(YTHIP_EUNSUPPORTED, "%s: W rows must be 16-byte aligned and hd a multiple of 8", who);
+    if (ld_part < (int64_t)hq * splits * (hd + 2)) return fail(YTHIP_EINVAL, "%s: ld_part too small", who);
+    if (ldc < n) return fail(YTHIP_EINVAL, "%s: ldc < n", who);
+    const int64_t lds = (m * k + 7) / 8 * 16 + ((int64_t)m * hq * splits + (int64_t)m * hq) * 4;
+    if (lds > GEMV_LDS_MAX)
+        return fail(YTHIP_EUNSUPPORTED, "%s: m * hq * hd = %lld with %d splits exceeds the %d-byte staging", who,
+                    (long long)(m * k), splits, GEMV_LDS_MAX);
+    GemvArgs a{};
+    a.A = partials; a.lda = ld_part;
+    a.W = W; a.ldw = ldw; a.C = C; a.ldc = ldc;
+    a.m = m; a.n = n; a.k = (int)k; a.alpha = alpha; a.beta = beta;
+    a.hq = hq; a.hd = hd; a.splits = splits;
+    return gemv_merge_dispatch(dtype, dtype_out, a, static_cast<hipStream_t>(stream));
 }
 
 __attribute__((visibility("default"))) int ythip_argmax_finish(const float* parts, int n_parts, int32_t* token,

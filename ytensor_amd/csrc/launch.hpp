@@ -35,6 +35,7 @@ struct GemvArgs {
     int m, n, k;
     float alpha, beta;
     float* amax;  // optional: per 16-column tile (max, index) of row 0
+    int hq, hd, splits;  // prologue 3: A = split-K decode partials [m][hq][splits][hd + 2]
 };
 
 int gemv_dispatch(int prologue, int dtype_in, int dtype_out, const GemvArgs& a, int batch, hipStream_t s);

@@ -551,6 +551,29 @@ def gemv_fused(a: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, prologu
     return out
 
 
+def gemv_attn_merge(workspace: torch.Tensor, B: int, Hq: int, d: int, max_ctx: int, weight: torch.Tensor,
+                    out: torch.Tensor, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """Decode-step o projection straight from the split-K partials that
+    decode_attention_rope(out=None) left in `workspace`: out [B, N] = alpha *
+    merge(partials) @ weight.T + beta * out, weight [N, Hq*d]. Same bits as
+    decode_attention_rope(out=attn) followed by gemv_fused(attn, weight, out)."""
+    _dev(workspace, weight, out)
+    splits = decode_splits(B, Hq, max_ctx)
+    n, k = weight.shape
+    if k != Hq * d:
+        raise ValueError(f"weight must be [N, {Hq * d}]")
+    o2 = out.reshape(-1, out.shape[-1])
+    if o2.shape != (B, n) or o2.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError(f"out must be [{B}, {n}] with unit column stride")
+    ld = Hq * splits * (d + 2)
+    if workspace.numel() * workspace.element_size() < B * ld * 4:
+        raise ValueError("workspace smaller than the partials")
+    check(_lib.lib().ythip_gemv_attn_merge(_code(weight), _code(out), B, n, Hq, d, splits, workspace.data_ptr(), ld,
+                                           weight.data_ptr(), weight.stride(0), o2.data_ptr(), o2.stride(0),
+                                           float(alpha), float(beta), _stream()), "ythip_gemv_attn_merge")
+    return out
+
+
 def gemv_swiglu(a: torch.Tensor, gate_up: torch.Tensor, out: torch.Tensor, prologue: str = "none",
                 norm_weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
     """Qwen3MLP's gate_up linear + SwiGLU for at most 16 rows (qwen3.cpp:193-200):

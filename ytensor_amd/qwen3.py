@@ -306,11 +306,12 @@ class Qwen3:
         x = self.x[:1]
         kc, vc = self.kc[i], self.vc[i]
         ops.gemv_fused(x, L["qkv"], self.qkv[:1], "rmsnorm", L["n1"], cfg.eps)
-        # q/k norm + RoPE, the K/V append and split-K attention in one launch,
-        # then the merge of the splits
+        # q/k norm + RoPE, the K/V append and split-K attention in one launch
+        # (partials in the workspace), then the merge of the splits as the o
+        # projection's prologue
         ops.decode_attention_rope(self.qkv[:1], nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
-                                  self.state[1:2], kc, vc, self.attn[:1].view(1, nh, hd), self.ws)
-        ops.gemv_fused(self.attn[:1], L["o"], x, beta=1.0)                         # x += attn . Wo^T
+                                  self.state[1:2], kc, vc, None, self.ws)
+        ops.gemv_attn_merge(self.ws, 1, nh, hd, self.max_ctx, L["o"], x, beta=1.0)  # x += attn . Wo^T
         ops.gemv_swiglu(x, L["gu"], self.act[:1], "rmsnorm", L["n2"], cfg.eps)    # act = swiglu(norm(x) . Wgu^T)
         ops.gemv_fused(self.act[:1], L["down"], x, beta=1.0)                      # x += act . Wdown^T
 
