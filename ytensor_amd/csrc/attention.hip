@@ -441,11 +441,13 @@ __device__ __forceinline__ void store8_raw(typename T::raw* p, const float (&x)[
 // FUSED: see DecodeArgs; the per-head RMSNorm / RoPE arithmetic is that of
 // norm_rope_kernel, so the fused step gives the same bits as
 // ythip_rmsnorm_rope followed by ythip_attn_decode.
-template <class T, int D, int G, bool FUSED>
-__global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
+// NTH threads per workgroup: 512 (twice the keys in flight, so a split of up to
+// 128 keys is one batch) when the grid is too small to cover the CUs.
+template <class T, int D, int G, bool FUSED, int NTH>
+__global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     using raw = typename T::raw;
     constexpr int LPK = D / 8;          // lanes per key
-    constexpr int SLOTS = 256 / LPK;    // keys in flight per workgroup
+    constexpr int SLOTS = NTH / LPK;    // keys in flight per workgroup
     constexpr int UNR = 4;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
@@ -672,7 +674,7 @@ __global__ __launch_bounds__(256) void attn_decode_split(DecodeArgs a) {
     }
     __syncthreads();
     float* ws = a.ws;
-    for (int idx = tid; idx < G * D; idx += 256) {
+    for (int idx = tid; idx < G * D; idx += NTH) {
         const int gi = idx / D, d = idx % D;
         float M = -INFINITY;
         for (int sl = 0; sl < SLOTS; ++sl) M = fmaxf(M, s_ml[sl][gi][0]);
@@ -798,13 +800,26 @@ int decode_splits(int B, int Hq, int max_ctx) {
     return s;
 }
 
+// The workgroup size is a function of the launch shape only, so the fused and
+// the unfused decode paths produce the same partials.
+inline bool decode_wide(int B, int Hkv, int splits, int G, int D) {
+    return (int64_t)B * Hkv * splits < 256 && (int64_t)(512 / (D / 8)) * G * D * 4 <= 64 * 1024;
+}
+
 template <class T, int D, int G>
 hipError_t launch_decode_g(const DecodeArgs& a, hipStream_t s) {
     dim3 grid(a.splits, a.Hkv, a.B);
-    if (a.fused)
-        attn_decode_split<T, D, G, true><<<grid, 256, 0, s>>>(a);
-    else
-        attn_decode_split<T, D, G, false><<<grid, 256, 0, s>>>(a);
+    const bool wide = decode_wide(a.B, a.Hkv, a.splits, G, D);
+    if constexpr ((512 / (D / 8)) * G * D * 4 <= 64 * 1024) {
+        if (wide) {
+            if (a.fused) attn_decode_split<T, D, G, true, 512><<<grid, 512, 0, s>>>(a);
+            else attn_decode_split<T, D, G, false, 512><<<grid, 512, 0, s>>>(a);
+        }
+    }
+    if (!wide) {
+        if (a.fused) attn_decode_split<T, D, G, true, 256><<<grid, 256, 0, s>>>(a);
+        else attn_decode_split<T, D, G, false, 256><<<grid, 256, 0, s>>>(a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.O == nullptr || a.direct) return e;  // O == NULL: the caller merges the partials
     attn_decode_merge<T, D><<<dim3(a.Hq, a.B), D, 0, s>>>(a);
