@@ -522,7 +522,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 // Skinny GEMM, M <= 16 (the decode GEMVs: x [1..16, K] . W^T). HBM-bound on
 // the weight stream, so the design goal is bytes in flight, not MFMA reuse.
 //   NT (W^T, the `linear` layout): gemv_kernel in gemv.hip.
-//   NN (B [K][N] row-major): VALU; lane = one output column, coalesced 2-byte
+//   NN (B [K][N] row-major): VALU; M == 1 in gemv_nn_kernel (16-byte chunks
+//   of 8 k-rows per load), else lane = one output column, coalesced 2-byte
 //   row loads, 8 waves split K, LDS reduction.
 // ---------------------------------------------------------------------------
 constexpr int SKINNY_M = 16;
@@ -578,6 +579,79 @@ __global__ __launch_bounds__(64 * SKINNY_WAVES) void gemm_skinny_nn_kernel(GemmA
         if (a.beta != 0.0f) v += a.beta * load_as_f32<TO>(crow, n);
         store_from_f32<TO>(crow, n, v);
     }
+}
+
+// M == 1 with row-major B [K][N] (the configs' weight layout): a workgroup owns
+// CPR * VEC consecutive columns (CPR 16-byte chunks of a k-row); its 16 waves
+// split K, and within a wave lane (r, c) = (lane / CPR, lane % CPR) reads chunk c
+// of k-rows r, r + 64/CPR, ... (all of a wave's loads issued before the first
+// use). CPR is chosen so the grid covers the CUs: narrower column tiles read
+// shorter row pieces but keep more CUs streaming. Per lane VEC fp32 partials in
+// k order, a butterfly over the row lanes, then a fixed-order sum of the 16
+// waves' partials in LDS.
+template <class T, class TO, int CPR>
+__global__ __launch_bounds__(1024) void gemv_nn_kernel(GemmArgs a) {
+    using raw = typename T::raw;
+    constexpr int VEC = 16 / sizeof(raw), WAVES = 16, UNR = 8, RPI = 64 / CPR;  // k-rows per load
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane % CPR, r = lane / CPR;
+    const int n0 = blockIdx.x * CPR * VEC;
+    const int bz = blockIdx.y;
+    const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
+    const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b + n0 + c * VEC;
+    const bool col = n0 + c * VEC < a.n;  // the host guarantees n % VEC == 0
+    const int kper = ((a.k + WAVES - 1) / WAVES + RPI - 1) / RPI * RPI;
+    const int kb = wave * kper, ke = min(a.k, kb + kper);
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int k0 = kb; k0 < ke; k0 += RPI * UNR) {
+        u32x4 w[UNR];
+        float x[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int kk = k0 + RPI * u + r;
+            const bool ok = col && kk < ke;
+            w[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Bp + (int64_t)kk * a.rsb))
+                      : u32x4{0u, 0u, 0u, 0u};
+            x[u] = kk < ke ? load_as_f32<T>(Ap, kk) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            if constexpr (sizeof(raw) == 2) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t we = w[u][e];
+                    acc[2 * e] = fmaf(x[u], lo_as_f32(T{}, we), acc[2 * e]);
+                    acc[2 * e + 1] = fmaf(x[u], hi_as_f32(T{}, we), acc[2 * e + 1]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = fmaf(x[u], __uint_as_float(w[u][e]), acc[e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = CPR; off < 64; off <<= 1)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
+    __shared__ float red[WAVES][CPR * VEC];
+    if (r == 0) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) red[wave][c * VEC + e] = acc[e];
+    }
+    __syncthreads();
+    if (tid >= CPR * VEC) return;
+    const int n = n0 + tid;
+    if (n >= a.n) return;
+    float t = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < WAVES; ++w2) t += red[w2][tid];
+    using oraw = typename TO::raw;
+    oraw* crow = static_cast<oraw*>(a.C) + bz * a.sc_b;
+    float v = a.alpha * t;
+    if (a.beta != 0.0f) v += a.beta * load_as_f32<TO>(crow, n);
+    store_from_f32<TO>(crow, n, v);
 }
 
 // Any-stride fallback: one output per thread, fp32 accumulation in k order.
@@ -725,6 +799,16 @@ int gemm_typed(int batch, int m, int n, int k, const void* A, int64_t sa_b, int6
                 v.sa_b = sa_b; v.sw_b = sb_b; v.sc_b = sc_b;
                 v.m = m; v.n = n; v.k = k; v.alpha = alpha; v.beta = beta;
                 return gemv_dispatch(0, T::code, TO::code, v, batch, s);
+            }
+            if (m == 1 && (n % VEC) == 0 && (rsb % VEC) == 0 && (sb_b % VEC) == 0 && aligned(B, 16)) {
+                auto tiles = [&](int cpr) { return (int64_t)((n + cpr * VEC - 1) / (cpr * VEC)) * batch; };
+                if (tiles(8) >= 96)
+                    gemv_nn_kernel<T, TO, 8><<<dim3((n + 8 * VEC - 1) / (8 * VEC), batch), 1024, 0, s>>>(g);
+                else if (tiles(4) >= 96)
+                    gemv_nn_kernel<T, TO, 4><<<dim3((n + 4 * VEC - 1) / (4 * VEC), batch), 1024, 0, s>>>(g);
+                else
+                    gemv_nn_kernel<T, TO, 2><<<dim3((n + 2 * VEC - 1) / (2 * VEC), batch), 1024, 0, s>>>(g);
+                return status_of(hipGetLastError());
             }
             gemm_skinny_nn_kernel<T, TO><<<dim3((n + 63) / 64, batch), 64 * SKINNY_WAVES, 0, s>>>(g);
             return status_of(hipGetLastError());

@@ -35,10 +35,10 @@
 namespace ythip {
 
 constexpr int GEMV_M = 16;
-// Single-row GEMVs up to this many output rows run gemv_row_kernel (every
-// decode-step linear); wider ones (the LM head) keep the MFMA-reducer kernel,
-// whose 16-column tiles amortise the per-workgroup prologue better.
-constexpr int GEMV_ROW_MAX_N = 32768;
+// Single-row GEMVs wider than this (the LM head) give each wave 4 weight rows:
+// more bytes in flight per wave and a quarter of the workgroups (and of the
+// prologue copies) -- measured 50 us against 97 us for the 151936 x 1024 head.
+constexpr int GEMV_WIDE_N = 32768;
 constexpr int GEMV_LDS_MAX = 64 * 1024;  // bytes of the staged A' (prologues 1 and 2)
 
 
@@ -454,12 +454,13 @@ __device__ __forceinline__ float dot8(F32, u32x4 w, u32x4 x, float acc) {
 //          pairs for the LM-head argmax (WAVES * RPW rows per workgroup).
 //   EPI 1: RPW = 2, rows (i, n + i) of W = [gate | up]; C[i] = swish(g) * u with
 //          g, u rounded to TO first (silu_mul_kernel after a 16-bit gate_up).
-template <class T, class TO, int WAVES, int RPW, int PRO, int EPI>
+template <class T, class TO, int WAVES, int RPW, int PRO, int EPI, int CPL_ = 0>
 __global__ __launch_bounds__(64 * WAVES) void gemv_row_kernel(GemvArgs a) {
     using raw = typename T::raw;
     constexpr int VEC = 16 / sizeof(raw);
-    // chunks per lane per round (16-wave workgroups hold fewer: 128 VGPRs a lane)
-    constexpr int CPL = (sizeof(raw) == 2 && WAVES < 16) ? 8 : 4;
+    // chunks per lane per round (16-wave workgroups hold fewer: 128 VGPRs a lane);
+    // the lane's chunk order, hence the bits, is the same for any CPL
+    constexpr int CPL = CPL_ ? CPL_ : ((sizeof(raw) == 2 && WAVES < 16) ? 8 : 4);
     static_assert(PRO == 0 || sizeof(raw) == 2, "fused prologues are 16-bit");
     static_assert(EPI == 0 || (RPW == 2 && PRO <= 1), "the SwiGLU epilogue pairs a gate and an up row");
     static_assert(PRO == 0 || WAVES >= 4, "the RMSNorm prologue reduces on 256 threads");
@@ -629,16 +630,16 @@ namespace {
 // call and the unfused sequence it replaces sum the k partials alike.
 inline bool gemv_wide(int64_t tiles) { return tiles <= 256; }
 
-template <class T, class TO, int WAVES, int RPW, int PRO, int EPI>
+template <class T, class TO, int WAVES, int RPW, int PRO, int EPI, int CPL = 0>
 hipError_t launch_row_t(const GemvArgs& a, size_t lds, hipStream_t s) {
     const int per_wg = EPI ? WAVES : WAVES * RPW;
-    gemv_row_kernel<T, TO, WAVES, RPW, PRO, EPI><<<(a.n + per_wg - 1) / per_wg, 64 * WAVES, lds, s>>>(a);
+    gemv_row_kernel<T, TO, WAVES, RPW, PRO, EPI, CPL><<<(a.n + per_wg - 1) / per_wg, 64 * WAVES, lds, s>>>(a);
     return hipGetLastError();
 }
 
 template <class T, class TO, int PRO, int EPI = 0>
 hipError_t launch_gemv_t(const GemvArgs& a, int batch, hipStream_t s) {
-    if (a.m == 1 && batch == 1 && a.n <= GEMV_ROW_MAX_N) {
+    if (a.m == 1 && batch == 1) {
         // One activation row: the row-per-wave kernel, whose bits do not depend on
         // the workgroup shape, so each variant takes the shape measured fastest on
         // the decode shapes: 4 rows per workgroup without a prologue; 16 waves
@@ -647,6 +648,10 @@ hipError_t launch_gemv_t(const GemvArgs& a, int batch, hipStream_t s) {
         size_t lds = PRO == 0 ? 0 : (size_t)a.k * sizeof(typename T::raw);
         if (PRO == 3) lds = ((size_t)a.k + 7) / 8 * 16 + ((size_t)a.hq * a.splits + (size_t)a.hq) * 4;
         if constexpr (EPI == 1) return launch_row_t<T, TO, 16, 2, PRO, 1>(a, lds, s);
+        if (a.n > GEMV_WIDE_N) {
+            if (a.k / (16 / (int)sizeof(typename T::raw)) <= 128) return launch_row_t<T, TO, 4, 4, PRO, 0, 2>(a, lds, s);
+            return launch_row_t<T, TO, 4, 4, PRO, 0, 4>(a, lds, s);
+        }
         if (PRO != 0 || a.amax != nullptr) return launch_row_t<T, TO, 16, 1, PRO, 0>(a, lds, s);
         return launch_row_t<T, TO, 4, 1, PRO, 0>(a, lds, s);
     }
