@@ -234,12 +234,16 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) v[kt][r] = s[qt][kt][r];
             }
+            // IEEE maximum (NaN-propagating) instead of fmaxf: gfx950's v_maximum3_f32
+            // takes the MFMA results as they are, where fmaxf first canonicalises
+            // every input (one extra VALU op per score); same value for any non-NaN row
             float mx = -INFINITY;
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
-                mx = fmaxf(mx, fmaxf(fmaxf(v[kt][0], v[kt][1]), fmaxf(v[kt][2], v[kt][3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, v[kt][r]);
+            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 16, 64));
+            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32, 64));
             // move the reference point only when the block max is far above it
             const bool move = (m[qt] == -INFINITY) ? (mx != -INFINITY) : ((mx - m[qt]) * c > LAZY);
             const float m_new = move ? mx : m[qt];
