@@ -313,9 +313,10 @@ def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=No
             "bytes_per_token": w_bytes + kv_bytes, "hbm_gbs": round(gbs, 1),
             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "tokens_generated": int(n_tokens),
             "distinct_tokens": int(len(set(toks.tolist()))),
-            "note": "batch 1, greedy, decode step = one HIP graph replay of 171 kernels (6 per layer: "
-                    "RMSNorm fused into the GEMV prologues, SwiGLU into the gate_up GEMV epilogue, q/k norm + RoPE + cache append into "
-                    "the split-K attention kernel)"}
+            "note": "batch 1, greedy, decode step = one HIP graph replay of 143 kernels (5 per layer: "
+                    "RMSNorm fused into the GEMV prologues, SwiGLU into the gate_up GEMV epilogue, q/k norm + "
+                    "RoPE + cache append into the split-K attention kernel, the split merge into the o "
+                    "projection's prologue)"}
 
 
 def bench_yt_load(torch, dev, reps: int = 3) -> dict:

@@ -17,10 +17,11 @@ MI355X layout and execution:
     projections write fp32 straight into the residual with beta = 1 (residual
     add fused into the GEMM epilogue); logits fp32;
   * KV cache in the 16-bit type, [layers][1, kv_heads, ctx, head_dim];
-  * a decode step is 6 launches per layer (the RMSNorms ride in the qkv and
+  * a decode step is 5 launches per layer (the RMSNorms ride in the qkv and
     gate_up GEMV prologues, SwiGLU in the gate_up GEMV's epilogue, q/k norm + RoPE +
-    cache append in the split-K attention kernel; the final norm and the argmax
-    ride in the LM head's) with no host-side value that changes
+    cache append in the split-K attention kernel, the merge of its splits in the
+    o projection's prologue; the final norm and the argmax ride in the LM
+    head's) with no host-side value that changes
     between steps (token id and positions live in device memory), so it is
     captured once as a HIP graph and replayed per token.
 Every arithmetic operation runs in libythip.so; torch only allocates device
@@ -296,11 +297,11 @@ class Qwen3:
         ops.gemm(self.act[:S], L["down"].t(), x, beta=1.0)        # x += act . Wdown^T
 
     def _layer_decode_fused(self, i: int) -> None:
-        """One token through layer i in 6 launches: the RMSNorms ride in the
+        """One token through layer i in 5 launches: the RMSNorms ride in the
         qkv / gate_up GEMV prologues, SwiGLU in the gate_up GEMV's epilogue (each
         activation computed once, by the workgroup that owns its gate and up
-        rows), and the q/k norm + RoPE and cache append in the split-K attention
-        kernel."""
+        rows), the q/k norm + RoPE and cache append in the split-K attention
+        kernel, and the merge of the splits in the o projection's prologue."""
         cfg, L = self.cfg, self.layers[i]
         nh, nkv, hd = cfg.n_heads, cfg.n_kv, cfg.head_dim
         x = self.x[:1]
