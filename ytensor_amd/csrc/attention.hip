@@ -515,8 +515,42 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
             }
         }
     };
-    // The first batch is in flight while the query (and, fused, the new
-    // token's norm / RoPE) is prepared.
+    // Fused: the new token's rows are loaded first, then the first K/V batch goes
+    // out, then the norm / RoPE runs while the batch is in flight. (Vector-memory
+    // loads retire in issue order: loading the rows after the batch would make
+    // their first wait cover the whole batch.)
+    constexpr int HALF = D / 2, LPR = HALF / 8;
+    constexpr int RW = sizeof(raw) == 2 ? 1 : 2;  // u32x4 per 8 elements
+    const int nrows = FUSED ? G + (owner ? 2 : 0) : 0;
+    const bool prow = FUSED && tid < nrows * LPR;
+    const int pr = tid / LPR, pj = tid % LPR;
+    u32x4 r1[RW], r2[RW];
+    f32x4 wv[4], cs[4];
+    if constexpr (FUSED) {
+        if (prow) {
+            const int head = pr < G ? kvh * G + pr : (pr == G ? a.Hq + kvh : a.Hq + a.Hkv + kvh);
+            const raw* src = static_cast<const raw*>(a.qkv) + (int64_t)b * a.ld_qkv + (int64_t)head * D + 8 * pj;
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                r1[i] = reinterpret_cast<const u32x4*>(src)[i];
+                r2[i] = reinterpret_cast<const u32x4*>(src + HALF)[i];
+            }
+            const float* w = pr < G ? a.wq : (pr == G ? a.wk : nullptr);
+            if (pr <= G && w != nullptr) {
+                wv[0] = reinterpret_cast<const f32x4*>(w + 8 * pj)[0];
+                wv[1] = reinterpret_cast<const f32x4*>(w + 8 * pj)[1];
+                wv[2] = reinterpret_cast<const f32x4*>(w + HALF + 8 * pj)[0];
+                wv[3] = reinterpret_cast<const f32x4*>(w + HALF + 8 * pj)[1];
+            }
+            if (pr <= G && a.cos_tab != nullptr) {
+                const int64_t t = (int64_t)pos * a.ld_tab + 8 * pj;
+                cs[0] = *reinterpret_cast<const f32x4*>(a.cos_tab + t);
+                cs[1] = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
+                cs[2] = *reinterpret_cast<const f32x4*>(a.sin_tab + t);
+                cs[3] = *reinterpret_cast<const f32x4*>(a.sin_tab + t + 4);
+            }
+        }
+    }
     int k0 = kbeg + slot;
     if (k0 < kend) load_batch(k0);
 
@@ -524,32 +558,27 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     __shared__ float s_new[FUSED ? (G + 2) * D : 1];  // normed + roped q heads, then k, then v
     if constexpr (FUSED) {
         // norm_rope_kernel's arithmetic, one LPR-lane group per row
-        constexpr int HALF = D / 2, LPR = HALF / 8;
-        const int nrows = G + (owner ? 2 : 0);
-        if (tid < nrows * LPR) {
-            const int r = tid / LPR, j = tid % LPR;
-            const int head = r < G ? kvh * G + r : (r == G ? a.Hq + kvh : a.Hq + a.Hkv + kvh);
-            const raw* src = static_cast<const raw*>(a.qkv) + (int64_t)b * a.ld_qkv + (int64_t)head * D + 8 * j;
+        if (prow) {
+            const int r = pr, j = pj;
             float x1[8], x2[8];
-            auto load8 = [&](const raw* p8, float (&x)[8]) {
+            auto unpack8 = [&](const u32x4 (&rw)[RW], float (&x)[8]) {
                 if constexpr (sizeof(raw) == 2) {
-                    const u32x4 w4 = *reinterpret_cast<const u32x4*>(p8);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        x[2 * e] = lo_as_f32(T{}, w4[e]);
-                        x[2 * e + 1] = hi_as_f32(T{}, w4[e]);
+                        const uint32_t we = rw[0][e];
+                        x[2 * e] = lo_as_f32(T{}, we);
+                        x[2 * e + 1] = hi_as_f32(T{}, we);
                     }
                 } else {
-                    const f32x4 lo = reinterpret_cast<const f32x4*>(p8)[0], hi = reinterpret_cast<const f32x4*>(p8)[1];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        x[e] = lo[e];
-                        x[e + 4] = hi[e];
+                        x[e] = __uint_as_float(rw[0][e]);
+                        x[e + 4] = __uint_as_float(rw[RW - 1][e]);
                     }
                 }
             };
-            load8(src, x1);
-            load8(src + HALF, x2);
+            unpack8(r1, x1);
+            unpack8(r2, x2);
             const float* w = r < G ? a.wq : (r == G ? a.wk : nullptr);
             if (r <= G && w != nullptr) {
                 float ss = 0.f;
@@ -558,9 +587,7 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
 #pragma unroll
                 for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
                 const float den = sqrtf(ss / (float)D + a.eps);
-                const f32x4* w1 = reinterpret_cast<const f32x4*>(w + 8 * j);
-                const f32x4* w2 = reinterpret_cast<const f32x4*>(w + HALF + 8 * j);
-                const f32x4 wa = w1[0], wb = w1[1], wc = w2[0], wd = w2[1];
+                const f32x4 wa = wv[0], wb = wv[1], wc = wv[2], wd = wv[3];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     x1[e] = (x1[e] / den) * wa[e];
@@ -570,11 +597,7 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
                 }
             }
             if (r <= G && a.cos_tab != nullptr) {
-                const int64_t t = (int64_t)pos * a.ld_tab + 8 * j;
-                const f32x4 c0 = *reinterpret_cast<const f32x4*>(a.cos_tab + t);
-                const f32x4 c1 = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
-                const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.sin_tab + t);
-                const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.sin_tab + t + 4);
+                const f32x4 c0 = cs[0], c1 = cs[1], s0 = cs[2], s1 = cs[3];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float c = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
