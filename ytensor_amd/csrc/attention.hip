@@ -700,19 +700,52 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
         for (int e = 0; e < 8; ++e) s_o[slot][gi][part * 8 + e] = o[gi][e];
     }
     __syncthreads();
+    // NTH = 512 (32 slots): slot weights once per (head, slot) -- one wave per head,
+    // lane = slot, the max and the weighted l as wave reductions (a slot that saw
+    // no key has m = -inf and o = 0, so weight 0 drops it) -- so the per-element
+    // loop is a plain FMA chain. NTH = 256 (16 slots, long splits) keeps the
+    // per-element loop, which measured faster there.
+    static_assert(SLOTS <= 64, "one lane per slot");
+    __shared__ float s_w[NTH == 512 ? G : 1][SLOTS];
+    __shared__ float s_ML[G][2];
+    if constexpr (NTH == 512) {
+        for (int t = tid; t < G * 64; t += NTH) {
+            const int gi = t / 64, sl = t % 64;
+            const float ms = sl < SLOTS ? s_ml[sl][gi][0] : -INFINITY;
+            float M = ms;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+            const float w = (M != -INFINITY && ms != -INFINITY) ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
+            const float L = wave_sum(sl < SLOTS ? s_ml[sl][gi][1] * w : 0.f);
+            if (sl < SLOTS) s_w[gi][sl] = w;
+            if (sl == 0) {
+                s_ML[gi][0] = M;
+                s_ML[gi][1] = L;
+            }
+        }
+        __syncthreads();
+    }
     float* ws = a.ws;
     for (int idx = tid; idx < G * D; idx += NTH) {
         const int gi = idx / D, d = idx % D;
-        float M = -INFINITY;
-        for (int sl = 0; sl < SLOTS; ++sl) M = fmaxf(M, s_ml[sl][gi][0]);
-        float L = 0.f, acc = 0.f;
-        if (M != -INFINITY) {
-            for (int sl = 0; sl < SLOTS; ++sl) {
-                const float ms = s_ml[sl][gi][0];
-                if (ms == -INFINITY) continue;
-                const float w = __builtin_amdgcn_exp2f(ms - M);
-                L = fmaf(s_ml[sl][gi][1], w, L);
-                acc = fmaf(s_o[sl][gi][d], w, acc);
+        float M, L, acc = 0.f;
+        if constexpr (NTH == 512) {
+            M = s_ML[gi][0];
+            L = s_ML[gi][1];
+#pragma unroll
+            for (int sl = 0; sl < SLOTS; ++sl) acc = fmaf(s_o[sl][gi][d], s_w[gi][sl], acc);
+        } else {
+            M = -INFINITY;
+            L = 0.f;
+            for (int sl = 0; sl < SLOTS; ++sl) M = fmaxf(M, s_ml[sl][gi][0]);
+            if (M != -INFINITY) {
+                for (int sl = 0; sl < SLOTS; ++sl) {
+                    const float ms = s_ml[sl][gi][0];
+                    if (ms == -INFINITY) continue;
+                    const float w = __builtin_amdgcn_exp2f(ms - M);
+                    L = fmaf(s_ml[sl][gi][1], w, L);
+                    acc = fmaf(s_o[sl][gi][d], w, acc);
+                }
             }
         }
         const int h = kvh * G + gi;
