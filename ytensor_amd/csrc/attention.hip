@@ -712,11 +712,9 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
         for (int t = tid; t < G * 64; t += NTH) {
             const int gi = t / 64, sl = t % 64;
             const float ms = sl < SLOTS ? s_ml[sl][gi][0] : -INFINITY;
-            float M = ms;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+            const float M = lane63(dpp_max_to_lane63(ms));
             const float w = (M != -INFINITY && ms != -INFINITY) ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
-            const float L = wave_sum(sl < SLOTS ? s_ml[sl][gi][1] * w : 0.f);
+            const float L = lane63(dpp_sum_to_lane63(sl < SLOTS ? s_ml[sl][gi][1] * w : 0.f));
             if (sl < SLOTS) s_w[gi][sl] = w;
             if (sl == 0) {
                 s_ML[gi][0] = M;

@@ -154,6 +154,38 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Sum / max over the 64 lanes with DPP row operations (quad swaps, half-row and
+// row mirrors, then the row broadcasts of gfx9): the result lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max(float v) {
+    const int ninf = __float_as_int(-INFINITY);  // rows the broadcast skips see -inf
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), CTRL, ROW_MASK, 0xf, false)));
+}
+__device__ __forceinline__ float dpp_sum_to_lane63(float v) {
+    v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+    v = dpp_add<0x140, 0xf>(v);  // row_mirror
+    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+__device__ __forceinline__ float dpp_max_to_lane63(float v) {
+    v = dpp_max<0xb1, 0xf>(v);
+    v = dpp_max<0x4e, 0xf>(v);
+    v = dpp_max<0x141, 0xf>(v);
+    v = dpp_max<0x140, 0xf>(v);
+    v = dpp_max<0x142, 0xa>(v);
+    v = dpp_max<0x143, 0xc>(v);
+    return v;
+}
+// The lane-63 result as a wave-uniform value.
+__device__ __forceinline__ float lane63(float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)); }
+
 // Compile-time loop: f(std::integral_constant<int, i>) for i in [B, E).
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F&& f) {

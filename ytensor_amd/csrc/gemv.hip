@@ -398,22 +398,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     }
 }
 
-// Sum over the 64 lanes with DPP row operations (quad swaps, half-row and row
-// mirrors, then the row broadcasts of gfx9): the total lands in lane 63.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add(float v) {
-    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
-}
-__device__ __forceinline__ float dpp_sum_to_lane63(float v) {
-    v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
-    v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
-    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
-    v = dpp_add<0x140, 0xf>(v);  // row_mirror
-    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
-    v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
-    return v;
-}
-
 // 16 bytes of 16-bit weights . 16 bytes of the 16-bit operand, fp32 accumulate
 // (v_dot2_f32_bf16 / v_dot2_f32_f16: the products are exact in fp32).
 __device__ __forceinline__ float dot8(BF16, u32x4 w, u32x4 x, float acc) {
