@@ -480,7 +480,11 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     const raw* Vb = static_cast<const raw*>(a.V) + b * a.ks0 + kvh * a.ks1 + part * 8;
 
     // K/V of keys [k0, k0 + SLOTS * UNR) (this lane's 8 elements), clamped rows for
-    // keys past the end (loaded but never used)
+    // keys past the end (loaded but never used). The batch stays in its raw form
+    // until the key loop unpacks it: converting right after the loads would make
+    // the kernel wait for the batch there, before the work it is meant to overlap.
+    constexpr int KW = sizeof(raw) == 2 ? 1 : 2;  // u32x4 per 8 elements
+    u32x4 kr[UNR][KW], vr[UNR][KW];
     float kx[UNR][8], vx[UNR][8];
     bool ok[UNR];
     auto load_batch = [&](int k0) {
@@ -491,26 +495,33 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
             const int kk = ok[u] ? key : kbeg;
             const raw* kp = Kb + (int64_t)kk * a.ks2;
             const raw* vp = Vb + (int64_t)kk * a.ks2;
-            if constexpr (sizeof(raw) == 2) {
+#pragma unroll
+            for (int i = 0; i < KW; ++i) {
                 // streamed once: non-temporal loads (measured ~10% more HBM read rate)
-                const u32x4 kw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp));
-                const u32x4 vw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp));
+                kr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp) + i);
+                vr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp) + i);
+            }
+        }
+    };
+    auto unpack_batch = [&]() {
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            if constexpr (sizeof(raw) == 2) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    kx[u][2 * e] = lo_as_f32(T{}, kw[e]);
-                    kx[u][2 * e + 1] = hi_as_f32(T{}, kw[e]);
-                    vx[u][2 * e] = lo_as_f32(T{}, vw[e]);
-                    vx[u][2 * e + 1] = hi_as_f32(T{}, vw[e]);
+                    const uint32_t kw = kr[u][0][e], vw = vr[u][0][e];
+                    kx[u][2 * e] = lo_as_f32(T{}, kw);
+                    kx[u][2 * e + 1] = hi_as_f32(T{}, kw);
+                    vx[u][2 * e] = lo_as_f32(T{}, vw);
+                    vx[u][2 * e + 1] = hi_as_f32(T{}, vw);
                 }
             } else {
-                const f32x4 k_lo = *reinterpret_cast<const f32x4*>(kp);
-                const f32x4 k_hi = *reinterpret_cast<const f32x4*>(kp + 4);
-                const f32x4 v_lo = *reinterpret_cast<const f32x4*>(vp);
-                const f32x4 v_hi = *reinterpret_cast<const f32x4*>(vp + 4);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    kx[u][e] = k_lo[e]; kx[u][e + 4] = k_hi[e];
-                    vx[u][e] = v_lo[e]; vx[u][e + 4] = v_hi[e];
+                    kx[u][e] = __uint_as_float(kr[u][0][e]);
+                    kx[u][e + 4] = __uint_as_float(kr[u][1][e]);
+                    vx[u][e] = __uint_as_float(vr[u][0][e]);
+                    vx[u][e + 4] = __uint_as_float(vr[u][1][e]);
                 }
             }
         }
@@ -551,8 +562,11 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
             }
         }
     }
+    // issued unconditionally (rows past the end are clamped and masked): a branch
+    // around the loads would make the compiler's wait before the prologue
+    // arithmetic cover the batch as well
     int k0 = kbeg + slot;
-    if (k0 < kend) load_batch(k0);
+    load_batch(k0);
 
     float q[G][8];
     __shared__ float s_new[FUSED ? (G + 2) * D : 1];  // normed + roped q heads, then k, then v
@@ -637,6 +651,7 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     }
 
     for (; k0 < kend; k0 += SLOTS * UNR) {
+        unpack_batch();
         if constexpr (FUSED) {
             if (owner) {  // the token appended above: its k / v from LDS, not the cache row
 #pragma unroll
