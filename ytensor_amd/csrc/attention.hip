@@ -674,8 +674,7 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
                 float sv = 0.f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) sv = fmaf(q[gi][e], kx[u][e], sv);
-#pragma unroll
-                for (int w = LPK / 2; w >= 1; w >>= 1) sv += __shfl_xor(sv, w, LPK);
+                sv = dpp_sum_group<LPK>(sv);
                 sc[u] = ok[u] ? sv : -INFINITY;
                 mx = fmaxf(mx, sc[u]);
             }

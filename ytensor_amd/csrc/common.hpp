@@ -183,6 +183,22 @@ __device__ __forceinline__ float dpp_max_to_lane63(float v) {
     v = dpp_max<0x143, 0xc>(v);
     return v;
 }
+// Sum over aligned groups of N = 8 or 16 lanes, every lane of a group getting
+// its group's total (DPP: quad swaps, half-row mirror, then a rotate by 8 within
+// the 16-lane row).
+template <int N>
+__device__ __forceinline__ float dpp_sum_group(float v) {
+    static_assert(N == 8 || N == 16, "8- or 16-lane groups");
+    auto dpp = [](float x, auto ctrl) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+    };
+    v += dpp(v, std::integral_constant<int, 0xb1>{});   // quad_perm [1,0,3,2]
+    v += dpp(v, std::integral_constant<int, 0x4e>{});   // quad_perm [2,3,0,1]
+    v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+    if constexpr (N == 16) v += dpp(v, std::integral_constant<int, 0x128>{});  // row_ror:8
+    return v;
+}
+
 // The lane-63 result as a wave-uniform value.
 __device__ __forceinline__ float lane63(float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)); }
 
