@@ -70,11 +70,11 @@ struct AttnArgs {
 // the linear id is remapped so each XCD walks a contiguous range of
 // (kv head, query block) pairs -- one KV head's K/V stays in one XCD's L2 --
 // and, for causal masks, the longest query blocks start first.
-template <class T, int D, int MODE, int GH, int QT>
+template <class T, int D, int MODE, int GH, int QT, int NKT = 4>
 __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     using raw = typename T::raw;
     constexpr int THREADS = 256 * GH;
-    constexpr int WQ = 16 * QT, BQ = 4 * WQ, BKV = 64;  // QT 16-query tiles per wave
+    constexpr int WQ = 16 * QT, BQ = 4 * WQ, BKV = 16 * NKT;  // QT 16-query tiles per wave, NKT 16-key tiles per block
     constexpr int KCH = D / 8;    // 16-byte chunks per K/V row
     constexpr int DT = D / 16;    // output d tiles
     constexpr int KS = D / 32;    // d steps of the score MFMA
@@ -181,18 +181,18 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         }
     };
 
-    f32x4 s[QT][4];
+    f32x4 s[QT][NKT];
     // S^T = K . Q^T for block kb (K stage kb & 1).
     auto qk = [&](int kb) {
         const u32x4* cK = sK + (kb & 1) * STG;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int kt = 0; kt < NKT; ++kt) s[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
+            for (int kt = 0; kt < NKT; ++kt) {
                 const int key = kt * 16 + l16;
                 const u32x4 kf = cK[key * KCH + ((ks * 4 + g) ^ (key & KMASK))];
 #pragma unroll
@@ -204,16 +204,16 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     auto softmax_pv = [&](int kb) {
         const int k0 = kb * BKV;
         const bool need_mask = (MODE == 2) || (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off);
-        u32x4 pk[QT][2];
+        u32x4 pk[QT][NKT / 2];
         bool rescale = false;
         float alpha[QT];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             const int qa = q0 + qt * 16 + l16;
-            float v[4][4];
+            float v[NKT][4];
             if (need_mask) {
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
+                for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         float x = s[qt][kt][r];
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
                     }
             } else {
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
+                for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) v[kt][r] = s[qt][kt][r];
             }
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
             // every input (one extra VALU op per score); same value for any non-NaN row
             float mx = -INFINITY;
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, v[kt][r]);
             mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 16, 64));
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
             rescale |= move;
             float sum = 0.f;
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     v[kt][r] = __builtin_amdgcn_exp2f(fmaf(v[kt][r], c, -mc));
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
             l[qt] = fmaf(l[qt], alpha[qt], sum);
             m[qt] = m_new;
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
+            for (int kk = 0; kk < NKT / 2; ++kk) {
                 pk[qt][kk] = u32x4{pack2<T>(v[2 * kk][0], v[2 * kk][1]), pack2<T>(v[2 * kk][2], v[2 * kk][3]),
                                    pack2<T>(v[2 * kk + 1][0], v[2 * kk + 1][1]),
                                    pack2<T>(v[2 * kk + 1][2], v[2 * kk + 1][3])};
@@ -276,7 +276,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         }
         const u32x4* cV = sV + (kb & 1) * STG;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < NKT / 2; ++kk) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 u32x4 vf;
@@ -804,14 +804,14 @@ namespace {
 
 bool al(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
-template <class T, int D, int GH, int QT>
+template <class T, int D, int GH, int QT, int NKT = 4>
 hipError_t launch_prefill_gh(AttnArgs a, int mode, hipStream_t s) {
     constexpr int BQ = 64 * QT;
     a.nqb = (a.Sq + BQ - 1) / BQ;
     dim3 grid(a.nqb * a.B * a.Hq / GH);
-    if (mode == 0) attn_fwd_mfma<T, D, 0, GH, QT><<<grid, 256 * GH, 0, s>>>(a);
-    else if (mode == 1) attn_fwd_mfma<T, D, 1, GH, QT><<<grid, 256 * GH, 0, s>>>(a);
-    else attn_fwd_mfma<T, D, 2, GH, QT><<<grid, 256 * GH, 0, s>>>(a);
+    if (mode == 0) attn_fwd_mfma<T, D, 0, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
+    else if (mode == 1) attn_fwd_mfma<T, D, 1, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
+    else attn_fwd_mfma<T, D, 2, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -820,7 +820,7 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     // Two query heads per workgroup (K/V staged once for both) when the GQA
     // group size is even and the paired grid still covers the 256 CUs twice.
     const int64_t paired = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq / 2;
-    if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) return launch_prefill_gh<T, D, 2, 2>(a, mode, s);
+    if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) return launch_prefill_gh<T, D, 2, 2, 8>(a, mode, s);
     // Short sequences: 16 queries per wave doubles the workgroups (two per CU)
     // and halves the per-block work on the longest causal row's serial chain.
     const int64_t wgs = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq;
