@@ -457,6 +457,35 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     const int tid = threadIdx.x;
     const int slot = tid / LPK, part = tid % LPK;
     const int kbeg = split * a.chunk;
+    // Fused: the new token's q rows (and its k / v rows, used by the workgroup that
+    // owns the position) and the norm weights are loaded before anything else,
+    // in parallel with the position read; the RoPE rows follow once the position
+    // is known, then the first K/V batch. (Vector-memory loads retire in issue
+    // order: loading the rows after the batch would make their wait cover it.)
+    constexpr int HALF = D / 2, LPR = HALF / 8;
+    constexpr int RW = sizeof(raw) == 2 ? 1 : 2;  // u32x4 per 8 elements
+    const bool prow = FUSED && tid < (G + 2) * LPR;
+    const int pr = tid / LPR, pj = tid % LPR;
+    u32x4 r1[RW], r2[RW];
+    f32x4 wv[4], cs[4];
+    if constexpr (FUSED) {
+        if (prow) {
+            const int head = pr < G ? kvh * G + pr : (pr == G ? a.Hq + kvh : a.Hq + a.Hkv + kvh);
+            const raw* src = static_cast<const raw*>(a.qkv) + (int64_t)b * a.ld_qkv + (int64_t)head * D + 8 * pj;
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                r1[i] = reinterpret_cast<const u32x4*>(src)[i];
+                r2[i] = reinterpret_cast<const u32x4*>(src + HALF)[i];
+            }
+            const float* w = pr < G ? a.wq : (pr == G ? a.wk : nullptr);
+            if (pr <= G && w != nullptr) {
+                wv[0] = reinterpret_cast<const f32x4*>(w + 8 * pj)[0];
+                wv[1] = reinterpret_cast<const f32x4*>(w + 8 * pj)[1];
+                wv[2] = reinterpret_cast<const f32x4*>(w + HALF + 8 * pj)[0];
+                wv[3] = reinterpret_cast<const f32x4*>(w + HALF + 8 * pj)[1];
+            }
+        }
+    }
     int len, pos = -1;
     bool owner = false;  // FUSED: this workgroup's chunk holds the new token's position
     if constexpr (FUSED) {
@@ -526,40 +555,14 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
             }
         }
     };
-    // Fused: the new token's rows are loaded first, then the first K/V batch goes
-    // out, then the norm / RoPE runs while the batch is in flight. (Vector-memory
-    // loads retire in issue order: loading the rows after the batch would make
-    // their first wait cover the whole batch.)
-    constexpr int HALF = D / 2, LPR = HALF / 8;
-    constexpr int RW = sizeof(raw) == 2 ? 1 : 2;  // u32x4 per 8 elements
-    const int nrows = FUSED ? G + (owner ? 2 : 0) : 0;
-    const bool prow = FUSED && tid < nrows * LPR;
-    const int pr = tid / LPR, pj = tid % LPR;
-    u32x4 r1[RW], r2[RW];
-    f32x4 wv[4], cs[4];
+    // Fused: the RoPE rows of the position, then the first K/V batch.
     if constexpr (FUSED) {
-        if (prow) {
-            const int head = pr < G ? kvh * G + pr : (pr == G ? a.Hq + kvh : a.Hq + a.Hkv + kvh);
-            const raw* src = static_cast<const raw*>(a.qkv) + (int64_t)b * a.ld_qkv + (int64_t)head * D + 8 * pj;
-#pragma unroll
-            for (int i = 0; i < RW; ++i) {
-                r1[i] = reinterpret_cast<const u32x4*>(src)[i];
-                r2[i] = reinterpret_cast<const u32x4*>(src + HALF)[i];
-            }
-            const float* w = pr < G ? a.wq : (pr == G ? a.wk : nullptr);
-            if (pr <= G && w != nullptr) {
-                wv[0] = reinterpret_cast<const f32x4*>(w + 8 * pj)[0];
-                wv[1] = reinterpret_cast<const f32x4*>(w + 8 * pj)[1];
-                wv[2] = reinterpret_cast<const f32x4*>(w + HALF + 8 * pj)[0];
-                wv[3] = reinterpret_cast<const f32x4*>(w + HALF + 8 * pj)[1];
-            }
-            if (pr <= G && a.cos_tab != nullptr) {
-                const int64_t t = (int64_t)pos * a.ld_tab + 8 * pj;
-                cs[0] = *reinterpret_cast<const f32x4*>(a.cos_tab + t);
-                cs[1] = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
-                cs[2] = *reinterpret_cast<const f32x4*>(a.sin_tab + t);
-                cs[3] = *reinterpret_cast<const f32x4*>(a.sin_tab + t + 4);
-            }
+        if (prow && pr <= G && a.cos_tab != nullptr) {
+            const int64_t t = (int64_t)pos * a.ld_tab + 8 * pj;
+            cs[0] = *reinterpret_cast<const f32x4*>(a.cos_tab + t);
+            cs[1] = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
+            cs[2] = *reinterpret_cast<const f32x4*>(a.sin_tab + t);
+            cs[3] = *reinterpret_cast<const f32x4*>(a.sin_tab + t + 4);
         }
     }
     // issued unconditionally (rows past the end are clamped and masked): a branch
@@ -571,8 +574,9 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     float q[G][8];
     __shared__ float s_new[FUSED ? (G + 2) * D : 1];  // normed + roped q heads, then k, then v
     if constexpr (FUSED) {
-        // norm_rope_kernel's arithmetic, one LPR-lane group per row
-        if (prow) {
+        // norm_rope_kernel's arithmetic, one LPR-lane group per row (k / v rows only
+        // in the workgroup that owns the position)
+        if (prow && (pr < G || owner)) {
             const int r = pr, j = pj;
             float x1[8], x2[8];
             auto unpack8 = [&](const u32x4 (&rw)[RW], float (&x)[8]) {
