@@ -781,20 +781,38 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     }
 }
 
-template <class T, int D>
+// One workgroup per (head, batch), one thread per d. The splits' m and l go
+// through LDS and every o_s[d] is loaded up front (splits <= DEC_MAX_SPLITS),
+// so the merge pays one memory round trip; the arithmetic is the sequential
+// log-sum-exp combine over s = 0, 1, ... (the order the o projection's merge
+// prologue reproduces).
+constexpr int DEC_MAX_SPLITS = 64;
+template <class T, int D, int MAXS>  // MAXS >= splits: 8 or DEC_MAX_SPLITS
 __global__ __launch_bounds__(D) void attn_decode_merge(DecodeArgs a) {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const float* src = a.ws + ((int64_t)b * a.Hq + h) * a.splits * (D + 2);
+    const int S = a.splits;
+    __shared__ float s_m[MAXS], s_l[MAXS];
+    for (int q = d; q < S; q += D) {
+        s_m[q] = src[q * (D + 2)];
+        s_l[q] = src[q * (D + 2) + 1];
+    }
+    float ov[MAXS];
+#pragma unroll
+    for (int q = 0; q < MAXS; ++q) ov[q] = q < S ? src[q * (D + 2) + 2 + d] : 0.f;
+    __syncthreads();
     float M = -INFINITY;
-    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, src[s * (D + 2)]);
+    for (int q = 0; q < S; ++q) M = fmaxf(M, s_m[q]);
     float L = 0.f, acc = 0.f;
     if (M != -INFINITY) {
-        for (int s = 0; s < a.splits; ++s) {
-            const float ms = src[s * (D + 2)];
-            if (ms == -INFINITY) continue;
-            const float w = exp2f(ms - M);
-            L = fmaf(src[s * (D + 2) + 1], w, L);
-            acc = fmaf(src[s * (D + 2) + 2 + d], w, acc);
+#pragma unroll
+        for (int q = 0; q < MAXS; ++q) {
+            const float ms = q < S ? s_m[q] : -INFINITY;
+            if (ms != -INFINITY) {
+                const float w = exp2f(ms - M);
+                L = fmaf(s_l[q], w, L);
+                acc = fmaf(ov[q], w, acc);
+            }
         }
     }
     const float out = L > 0.f ? acc / L : 0.f;
@@ -871,7 +889,7 @@ int decode_splits(int B, int Hq, int max_ctx) {
     int s = (1024 + bh - 1) / bh;
     const int by_len = (max_ctx + 127) / 128;
     if (s > by_len) s = by_len;
-    if (s > 64) s = 64;
+    if (s > DEC_MAX_SPLITS) s = DEC_MAX_SPLITS;  // the merge holds one register per split
     if (s < 1) s = 1;
     return s;
 }
@@ -898,7 +916,8 @@ hipError_t launch_decode_g(const DecodeArgs& a, hipStream_t s) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.O == nullptr || a.direct) return e;  // O == NULL: the caller merges the partials
-    attn_decode_merge<T, D><<<dim3(a.Hq, a.B), D, 0, s>>>(a);
+    if (a.splits <= 8) attn_decode_merge<T, D, 8><<<dim3(a.Hq, a.B), D, 0, s>>>(a);
+    else attn_decode_merge<T, D, DEC_MAX_SPLITS><<<dim3(a.Hq, a.B), D, 0, s>>>(a);
     return hipGetLastError();
 }
 
