@@ -789,31 +789,35 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
 constexpr int DEC_MAX_SPLITS = 64;
 template <class T, int D, int MAXS>  // MAXS >= splits: 8 or DEC_MAX_SPLITS
 __global__ __launch_bounds__(D) void attn_decode_merge(DecodeArgs a) {
+    static_assert(MAXS <= D, "one thread stages each split's m and l");
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const float* src = a.ws + ((int64_t)b * a.Hq + h) * a.splits * (D + 2);
     const int S = a.splits;
-    __shared__ float s_m[MAXS], s_l[MAXS];
-    for (int q = d; q < S; q += D) {
-        s_m[q] = src[q * (D + 2)];
-        s_l[q] = src[q * (D + 2) + 1];
-    }
+    __shared__ float s_m[D], s_l[D];  // every thread stores (no branch to sink loads into)
+    // Every load is issued before the first wait, m and l first: indices past
+    // the last split re-read it (their values are unused), so no load sits
+    // behind a branch and the waits count down split by split.
+    const float* ml = src + min(d, S - 1) * (D + 2);
+    const float mv = ml[0], lv = ml[1];
     float ov[MAXS];
 #pragma unroll
-    for (int q = 0; q < MAXS; ++q) ov[q] = q < S ? src[q * (D + 2) + 2 + d] : 0.f;
+    for (int q = 0; q < MAXS; ++q) ov[q] = src[min(q, S - 1) * (D + 2) + 2 + d];
+    s_m[d] = d < S ? mv : -INFINITY;
+    s_l[d] = lv;
     __syncthreads();
     float M = -INFINITY;
-    for (int q = 0; q < S; ++q) M = fmaxf(M, s_m[q]);
-    float L = 0.f, acc = 0.f;
-    if (M != -INFINITY) {
 #pragma unroll
-        for (int q = 0; q < MAXS; ++q) {
-            const float ms = q < S ? s_m[q] : -INFINITY;
-            if (ms != -INFINITY) {
-                const float w = exp2f(ms - M);
-                L = fmaf(s_l[q], w, L);
-                acc = fmaf(ov[q], w, acc);
-            }
-        }
+    for (int q = 0; q < MAXS; ++q) M = fmaxf(M, s_m[q]);
+    // Empty splits (m = -inf, also the padding) get weight 0: every split
+    // writes finite l and o, so their terms add exact zeros and the result
+    // has the bits of skipping them in the sequential combine.
+    float L = 0.f, acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < MAXS; ++q) {
+        const float ms = s_m[q];
+        const float w = ms != -INFINITY ? exp2f(ms - M) : 0.f;
+        L = fmaf(s_l[q], w, L);
+        acc = fmaf(ov[q], w, acc);
     }
     const float out = L > 0.f ? acc / L : 0.f;
     store_from_f32<T>(a.O, b * a.os0 + h * a.os1 + d, out);
