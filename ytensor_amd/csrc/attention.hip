@@ -112,6 +112,11 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     const raw* Kp = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1;
     const raw* Vp = static_cast<const raw*>(a.V) + b * a.vs0 + kvh * a.vs1;
 
+    // Q is pre-scaled by scale*log2(e) and rounded back to T (relative error
+    // 2^-9 per element, about 1e-3 on p): the scores then leave the MFMA in
+    // log2 units, and since the accumulator starts at -m they leave it as
+    // s - m, so p = exp2(s - m) costs one exp per score and no multiply.
+    const float c = a.scale_log2;
     u32x4 qf[QT][KS];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -120,6 +125,11 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         for (int ks = 0; ks < KS; ++ks) {
             u32x4 v = {0u, 0u, 0u, 0u};
             if (q < a.Sq) v = *reinterpret_cast<const u32x4*>(Qp + (int64_t)q * a.qs2 + ks * 32 + g * 8);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t w2 = v[e];
+                v[e] = pack2<T>(lo_as_f32(T{}, w2) * c, hi_as_f32(T{}, w2) * c);
+            }
             qf[qt][ks] = v;
         }
     }
@@ -128,18 +138,24 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     int kv_end = a.Skv;
     if (MODE == 1) kv_end = min(a.Skv, qb * BQ + BQ + off);
     const int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;
-    const float c = a.scale_log2;
 
-    // m is the reference point of the exponentials (raw score units). It moves
-    // only when a block's max exceeds it by more than 2^8 in probability, so the
-    // O rescale is rare; p = 2^((s - m) c) <= 2^8 stays far from any overflow and
-    // the final O / l is independent of m.
+    // m is the reference point of the exponentials (log2 units), set by the
+    // first block with a visible key and moved only when a block's max exceeds
+    // it by more than 2^8 in probability, so the O rescale is rare; p = 2^(s - m)
+    // <= 2^8 stays far from any overflow and the final O / l is independent of m.
+    // l is the fourth MFMA output next to O: ones . P^T sums the packed p of
+    // every key (the same rounded p that multiplies V), one result per query.
     constexpr float LAZY = 8.0f;
-    float m[QT], l[QT];
+    constexpr uint32_t ONE2 = std::is_same_v<T, BF16> ? 0x3F803F80u : 0x3C003C00u;
+    const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
+    float m[QT];
+    bool mset[QT];
+    f32x4 lsum[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        m[qt] = -INFINITY;
-        l[qt] = 0.f;
+        m[qt] = 0.f;
+        mset[qt] = false;
+        lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     f32x4 o[QT][DT];
 #pragma unroll
@@ -182,13 +198,13 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     };
 
     f32x4 s[QT][NKT];
-    // S^T = K . Q^T for block kb (K stage kb & 1).
+    // S^T - m = K . Q^T - m for block kb (K stage kb & 1).
     auto qk = [&](int kb) {
         const u32x4* cK = sK + (kb & 1) * STG;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt) s[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int kt = 0; kt < NKT; ++kt) s[qt][kt] = f32x4{-m[qt], -m[qt], -m[qt], -m[qt]};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
@@ -222,9 +238,9 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
                         if (MODE == 1) vis = vis && (key <= qa + off);
                         if (MODE == 2 && vis && qa < a.Sq) {
                             if (a.mask != nullptr) vis = a.mask[(int64_t)qa * a.mask_ld + key] != 0;
-                            // bias is added after scaling: fold it into raw units
+                            // bias is added after scaling: log2 units, like the scores
                             if (vis && a.bias != nullptr)
-                                x += a.bias[(int64_t)qa * a.brs + (int64_t)key * a.bcs] * LOG2E / c;
+                                x += a.bias[(int64_t)qa * a.brs + (int64_t)key * a.bcs] * LOG2E;
                         }
                         v[kt][r] = vis ? x : -INFINITY;
                     }
@@ -244,22 +260,25 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
                 for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, v[kt][r]);
             mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 16, 64));
             mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32, 64));
-            // move the reference point only when the block max is far above it
-            const bool move = (m[qt] == -INFINITY) ? (mx != -INFINITY) : ((mx - m[qt]) * c > LAZY);
-            const float m_new = move ? mx : m[qt];
-            const float mc = (m_new == -INFINITY) ? 0.f : m_new * c;
-            alpha[qt] = move ? __builtin_amdgcn_exp2f(m[qt] * c - mc) : 1.0f;
-            rescale |= move;
-            float sum = 0.f;
+            // mx is relative to m. Set m on the first visible block, afterwards
+            // move it only when the block max is far above it.
+            const bool move = mset[qt] ? (mx > LAZY) : (mx != -INFINITY);
+            const float delta = move ? mx : 0.f;
+            const bool moved = move && mset[qt];  // O and l hold terms to rescale
+            alpha[qt] = moved ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
+            rescale |= moved;
+            m[qt] += delta;
+            mset[qt] = mset[qt] || move;
+            if (__ballot(move) != 0) {
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[kt][r] -= delta;
+            }
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    v[kt][r] = __builtin_amdgcn_exp2f(fmaf(v[kt][r], c, -mc));
-                    sum += v[kt][r];
-                }
-            l[qt] = fmaf(l[qt], alpha[qt], sum);
-            m[qt] = m_new;
+                for (int r = 0; r < 4; ++r) v[kt][r] = __builtin_amdgcn_exp2f(v[kt][r]);
 #pragma unroll
             for (int kk = 0; kk < NKT / 2; ++kk) {
                 pk[qt][kk] = u32x4{pack2<T>(v[2 * kk][0], v[2 * kk][1]), pack2<T>(v[2 * kk][2], v[2 * kk][3]),
@@ -270,9 +289,11 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         // O *= alpha only when some lane's reference point moved in this block.
         if (__ballot(rescale) != 0) {
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt)
+            for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha[qt];
+                lsum[qt] *= alpha[qt];
+            }
         }
         const u32x4* cV = sV + (kb & 1) * STG;
 #pragma unroll
@@ -291,6 +312,8 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_chunk(T{}, vf, pk[qt][kk], o[qt][dt]);
             }
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) lsum[qt] = mfma_chunk(T{}, ones, pk[qt][kk], lsum[qt]);
         }
     };
     // Wave-uniform: does block kb hold any key visible to this wave's queries?
@@ -313,9 +336,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     raw* Op = static_cast<raw*>(a.O) + b * a.os0 + h * a.os1;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        float L = l[qt];
-        L += __shfl_xor(L, 16, 64);
-        L += __shfl_xor(L, 32, 64);
+        const float L = lsum[qt][0];
         const float inv = L > 0.f ? 1.0f / L : 0.f;
         const int q = q0 + qt * 16 + l16;
         if (q >= a.Sq) continue;
