@@ -89,17 +89,37 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
             reinterpret_cast<f32x4*>(p)[1] = f32x4{x[4], x[5], x[6], x[7]};
         }
     };
+    // Every load is issued before the first use (the row, then its norm
+    // weights, then its table row): vector loads retire in order, so the
+    // weights and the cached tables arrive behind the row instead of costing a
+    // round trip each after the reduction. v rows load them too (unused).
     load8(src, x1);
     load8(src + HALF, x2);
+    const bool is_q = h < a.Hq, is_k = !is_q && h < a.Hq + a.Hkv;
+    const float* w = is_q ? a.wq : a.wk;
+    f32x4 wa = {}, wb = {}, wc = {}, wd = {};
+    if (w != nullptr) {
+        const f32x4* w1 = reinterpret_cast<const f32x4*>(w + 8 * j);
+        const f32x4* w2 = reinterpret_cast<const f32x4*>(w + HALF + 8 * j);
+        wa = w1[0];
+        wb = w1[1];
+        wc = w2[0];
+        wd = w2[1];
+    }
+    f32x4 c0 = {}, c1 = {}, s0 = {}, s1 = {};
+    if (a.cos_tab != nullptr) {
+        const int64_t t = (int64_t)(pos0 + s) * a.ld_tab + 8 * j;
+        c0 = *reinterpret_cast<const f32x4*>(a.cos_tab + t);
+        c1 = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
+        s0 = *reinterpret_cast<const f32x4*>(a.sin_tab + t);
+        s1 = *reinterpret_cast<const f32x4*>(a.sin_tab + t + 4);
+    }
 
     raw* dst;
-    const float* w = nullptr;
-    if (h < a.Hq) {
+    if (is_q) {
         dst = static_cast<raw*>(a.q) + b * a.qs0 + h * a.qs1 + s * a.qs2;
-        w = a.wq;
-    } else if (h < a.Hq + a.Hkv) {
+    } else if (is_k) {
         dst = static_cast<raw*>(a.k) + b * a.ks0 + (h - a.Hq) * a.ks1 + (int64_t)(cache_pos + s) * a.ks2;
-        w = a.wk;
     } else {
         if (a.v == nullptr) return;
         dst = static_cast<raw*>(a.v) + b * a.vs0 + (h - a.Hq - a.Hkv) * a.vs1 + (int64_t)(cache_pos + s) * a.vs2;
@@ -115,9 +135,6 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
 #pragma unroll
         for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
         const float den = sqrtf(ss / (float)D + a.eps);
-        const f32x4* w1 = reinterpret_cast<const f32x4*>(w + 8 * j);
-        const f32x4* w2 = reinterpret_cast<const f32x4*>(w + HALF + 8 * j);
-        const f32x4 wa = w1[0], wb = w1[1], wc = w2[0], wd = w2[1];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             x1[e] = (x1[e] / den) * wa[e];
@@ -127,9 +144,6 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
         }
     }
     if (a.cos_tab != nullptr) {
-        const int64_t t = (int64_t)(pos0 + s) * a.ld_tab + 8 * j;
-        const f32x4 c0 = *reinterpret_cast<const f32x4*>(a.cos_tab + t), c1 = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.sin_tab + t), s1 = *reinterpret_cast<const f32x4*>(a.sin_tab + t + 4);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const float c = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
