@@ -131,6 +131,36 @@ def test_qwen3_small_fp16_end_to_end(orc):
 
 
 @pytest.mark.gpu
+def test_qwen3_prefill_graph_equals_eager(orc):
+    """The captured prefill (one HIP graph per prompt length, replayed) gives
+    the eager prefill's bits: logits, residual stream, KV caches and the first
+    token, for three prompts of one length through the same graph with eager
+    work between the replays, and the decode that follows is unchanged."""
+    import torch
+
+    from ytensor_amd.qwen3 import Qwen3, Qwen3Config
+    cfg_o = oracle.Qwen3Config(**SMALL)
+    W = _small_weights(orc, cfg_o)
+    a = Qwen3(Qwen3Config(**SMALL), W, max_ctx=64, max_prompt=64)
+    b = Qwen3(Qwen3Config(**SMALL), W, max_ctx=64, max_prompt=64)
+    for seed in (6, 7, 8):
+        pr = oracle.qwen3_prompt(cfg_o, 29, seed=seed)
+        a.prefill(pr, use_graph=True)
+        b.prefill(pr)
+        torch.cuda.synchronize()
+        P = len(pr)
+        assert torch.equal(a.logits, b.logits), seed
+        assert torch.equal(a.x[:P], b.x[:P]), seed
+        assert torch.equal(a.kc[:, :, :, :P], b.kc[:, :, :, :P]) and torch.equal(a.vc[:, :, :, :P], b.vc[:, :, :, :P])
+        assert torch.equal(a.history[:1], b.history[:1]) and torch.equal(a.state, b.state), seed
+    assert len(a.prefill_graphs) == 1
+    pr = oracle.qwen3_prompt(cfg_o, 29, seed=9)
+    a.prefill(pr, use_graph=True)
+    ta = a.generate(pr, 8)  # the prefill graph again, then the decode graph
+    assert np.array_equal(ta, b.generate(pr, 8, use_graph=False))
+
+
+@pytest.mark.gpu
 def test_qwen3_fused_decode_equals_unfused(orc):
     """The fused decode step (GEMV prologues, one-kernel attention with q/k
     norm + RoPE + cache append + merge) gives the same bits as the unfused

@@ -115,6 +115,7 @@ class Qwen3:
         self._upload(weights)
         self._alloc()
         self.graph = None
+        self.prefill_graphs = {}  # prompt length -> captured prefill
 
     # ---------------------------------------------------------------- weights
     def _upload(self, weights) -> None:
@@ -327,18 +328,33 @@ class Qwen3:
         ops.gemm(self.hf, self.lm_head.t(), self.logits)           # LM head (tied by default), fp32 logits
         ops.argmax_step(self.logits, self.token, self.history, self.state)
 
-    def prefill(self, prompt) -> None:
-        """Run the prompt; the first generated token lands in history[0]."""
+    def _prefill_body(self, P: int) -> None:
+        ops.embedding(self.embed, self.ids[:P], self.x[:P])
+        for i in range(self.cfg.layers):
+            self._layer(i, P, 0, decode=False)
+        self._head(P)
+
+    def prefill(self, prompt, use_graph: bool = False) -> None:
+        """Run the prompt; the first generated token lands in history[0].
+
+        With use_graph the prompt's launches (embedding, every layer, head) are
+        captured once per prompt length as a HIP graph and replayed: the token
+        ids and the decode state are device buffers written before the replay,
+        so one capture serves every prompt of that length with the eager
+        path's bits."""
         P = len(prompt)
         if P > self.max_prompt or P >= self.max_ctx:
             raise ValueError(f"prompt of {P} tokens exceeds max_prompt={self.max_prompt} / max_ctx={self.max_ctx}")
         self.ids[:P].copy_(torch.as_tensor(np.asarray(prompt, dtype=np.int32)))
         # state after the head's argmax: generated = 1, position = P, kv_len = P + 1
         self.state.copy_(torch.tensor([0, P - 1, P], dtype=torch.int32))
-        ops.embedding(self.embed, self.ids[:P], self.x[:P])
-        for i in range(self.cfg.layers):
-            self._layer(i, P, 0, decode=False)
-        self._head(P)
+        if use_graph:
+            g = self.prefill_graphs.get(P)
+            if g is None:
+                g = self.prefill_graphs[P] = self._capture(lambda: self._prefill_body(P))
+            g.replay()
+        else:
+            self._prefill_body(P)
         self.prompt_len = P
 
     def _decode_step(self) -> None:
@@ -347,20 +363,26 @@ class Qwen3:
             self._layer(i, 1, 0, decode=True)
         self._head(1)
 
-    def capture(self) -> None:
-        """Capture one decode step as a HIP graph (replayed per token)."""
+    @staticmethod
+    def _capture(fn) -> "torch.cuda.CUDAGraph":
+        """Record fn's launches as a HIP graph (nothing executes while capturing)."""
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(side):
             with torch.cuda.graph(g, stream=side):
-                self._decode_step()
+                fn()
         torch.cuda.current_stream().wait_stream(side)
-        self.graph = g
+        return g
+
+    def capture(self) -> None:
+        """Capture one decode step as a HIP graph (replayed per token)."""
+        self.graph = self._capture(self._decode_step)
 
     def generate(self, prompt, n_tokens: int, use_graph: bool = True) -> np.ndarray:
-        """Greedy: prompt forward, then n_tokens - 1 decode steps. Returns the tokens."""
-        self.prefill(prompt)
+        """Greedy: prompt forward, then n_tokens - 1 decode steps. Returns the tokens.
+        use_graph replays captured graphs for both (one prefill graph per prompt length)."""
+        self.prefill(prompt, use_graph=use_graph)
         if len(prompt) + n_tokens > self.max_ctx:
             raise ValueError("max_ctx too small for prompt + generated tokens")
         if use_graph and self.graph is None:
