@@ -145,6 +145,36 @@ def test_batched_and_alpha_beta(orc, yt, dtype):
         assert rel_err(g[b], r) <= tol
 
 
+# Grids with fewer 64 x 64 tiles than CUs split each tile's k loop over 2 or 4
+# wave groups of one workgroup (bf16/fp16: k/64 steps, fp32: k/32): (130, 200,
+# 512) bf16 -> 2 groups, fp32 -> 4; (96, 192, 1024) -> 4; (64, 100, 256) fp32 -> 2.
+KSPLIT_SHAPES = [(130, 200, 512), (96, 192, 1024), (64, 100, 256), (1000, 1000, 2048)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("layout", ["NN", "NT"])
+@pytest.mark.parametrize("shape", KSPLIT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_split_k_groups_alpha_beta(orc, yt, shape, layout, dtype):
+    """Short grids (k split inside the workgroup), batched, alpha/beta into an fp32 C."""
+    M, N, K = shape
+    Bt = 2
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    A = rng.standard_normal((Bt, M, K)).astype(np.float32)
+    W = rng.standard_normal((Bt, K, N) if layout == "NN" else (Bt, N, K)).astype(np.float32)
+    C0 = rng.standard_normal((Bt, M, N)).astype(np.float32)
+    Ad, Ah = make_input(orc, A, dtype)
+    Wd, Wh = make_input(orc, W, dtype)
+    out = torch.from_numpy(C0).cuda()
+    yt.gemm(Ad, Wd if layout == "NN" else Wd.transpose(1, 2), out, alpha=0.5, beta=0.25)
+    g = host_f32(out)
+    for b in range(Bt):
+        r = orc.sgemm(Ah[b], Wh[b], b_trans=(layout == "NT"), alpha=0.5, beta=0.25, C=C0[b])
+        if dtype == "f32":
+            assert rel_err(g[b], r) <= REL_F32, (b, rel_err(g[b], r))
+        else:
+            _check16(orc, g[b], r, dtype, False, f"{shape} {layout} {dtype} batch {b}")
+
+
 def test_strided_operands_use_fallback(orc, yt):
     """Transposed A (csa != 1) and a column-major C go through the any-stride kernel."""
     rng = np.random.default_rng(5)

@@ -303,10 +303,15 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <class T, class TO, int BM, int BN, int WM, int WN, bool NN, int STAGES, int BX = 0>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a) {
+// KSPLIT > 1: KSPLIT groups of WM x WN waves share the tile, group g runs the
+// k steps [g*KT, (g+1)*KT) through its own LDS ring, and group 0 adds the other
+// groups' accumulators (through LDS, in group order) before the epilogue. For
+// grids with fewer tiles than CUs, where a tile's serial k loop is the critical
+// path.
+template <class T, class TO, int BM, int BN, int WM, int WN, bool NN, int STAGES, int KSPLIT = 1>
+__global__ __launch_bounds__(64 * WM * WN * KSPLIT) void gemm_mfma_dma_kernel(GemmArgs a) {
     using raw = typename T::raw;
-    constexpr int THREADS = 64 * WM * WN;
+    constexpr int THREADS = 64 * WM * WN;  // threads per k group
     constexpr int VEC = 16 / sizeof(raw);
     constexpr int BK = 8 * VEC;
     constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -321,13 +326,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 
     constexpr int PER = A_PT + B_PT;  // DMA instructions per thread per stage
     static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 2) * PER < 64, "pipeline depth");
-    // BX = 1: B gets a third stage (A keeps two), so B's DMA is issued two k steps
-    // before use; the 256 x 256 tile then fills exactly 160 KB of LDS.
-    static_assert(BX == 0 || (BX == 1 && STAGES == 2), "the extra B stage pairs with the double buffer");
+    constexpr int GSLOTS = STAGES * (STA + STB);  // 16-byte LDS slots per k group
+    static_assert((KSPLIT - 1) * THREADS * FM * FN * 4 * 4 <= KSPLIT * GSLOTS * 16, "reduction fits the rings");
 
-    __shared__ u32x4 sbuf[STAGES * STA + (STAGES + BX) * STB];
+    __shared__ u32x4 sbuf[KSPLIT * GSLOTS];
 
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x % THREADS;
+    const int grp = threadIdx.x / THREADS;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -339,10 +344,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
     const int bz = blockIdx.y;
     const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
     const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b;
-    const int KT = a.k / BK;
+    const int KT = a.k / BK / KSPLIT;  // k steps per group (the host checks divisibility)
+    const int kbase = grp * KT;
 
     auto issue_a = [&](int kt, u32x4* sA) {
-        const int k0 = kt * BK;
+        const int k0 = (kbase + kt) * BK;
 #pragma unroll
         for (int i = 0; i < A_PT; ++i) {
             const int slot = i * THREADS + wave * 64 + lane;
@@ -353,7 +359,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
         }
     };
     auto issue_b = [&](int kt, u32x4* sB) {
-        const int k0 = kt * BK;
+        const int k0 = (kbase + kt) * BK;
 #pragma unroll
         for (int i = 0; i < B_PT; ++i) {
             const int slot = i * THREADS + wave * 64 + lane;
@@ -437,24 +443,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
         });
     };
 
-    u32x4* sA = sbuf;
-    u32x4* sB = sbuf + STAGES * STA;
-    if constexpr (BX == 1) {
-        // A double-buffered, B triple-buffered. Issue order per iteration: A(kt+1),
-        // then B(kt+2); at the top of iteration kt only B(kt+1) may still be in flight
-        // behind A(kt) and B(kt) (vector-memory ops retire in order).
-        issue_a(0, sA);
-        issue_b(0, sB);
-        if (KT > 1) issue_b(1, sB + STB);
-        for (int kt = 0; kt < KT; ++kt) {
-            if (kt + 1 < KT) wait_vmcnt<B_PT>();
-            else wait_vmcnt<0>();
-            __syncthreads();  // stage kt is in LDS for every wave; stage kt-1 is consumed
-            if (kt + 1 < KT) issue_a(kt + 1, sA + ((kt + 1) & 1) * STA);
-            if (kt + 2 < KT) issue_b(kt + 2, sB + ((kt + 2) % 3) * STB);
-            compute(sA + (kt & 1) * STA, sB + (kt % 3) * STB);
-        }
-    } else if constexpr (STAGES == 2) {
+    u32x4* sA = sbuf + grp * GSLOTS;
+    u32x4* sB = sA + STAGES * STA;
+    if constexpr (STAGES == 2) {
         // Double buffer: DMA of step kt+1 overlaps the MFMAs of step kt.
         issue(0, sA, sB);
         wait_vmcnt<0>();
@@ -482,6 +473,32 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
         if (nxt < KT) issue(nxt, sA + (nxt % STAGES) * STA, sB + (nxt % STAGES) * STB);
         compute(sA + (kt % STAGES) * STA, sB + (kt % STAGES) * STB);
     }
+    }
+    if constexpr (KSPLIT > 1) {
+        __syncthreads();  // every group is done with its ring
+        float* red = reinterpret_cast<float*>(sbuf);
+        constexpr int NACC = FM * FN * 4;
+        if (grp > 0) {
+            float* dst = red + (grp - 1) * THREADS * NACC;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) dst[((i * FN + j) * 4 + r) * THREADS + tid] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int g2 = 1; g2 < KSPLIT; ++g2) {
+            const float* src = red + (g2 - 1) * THREADS * NACC;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] += src[((i * FN + j) * 4 + r) * THREADS + tid];
+        }
     }
 
     using oraw = typename TO::raw;
@@ -711,20 +728,20 @@ hipError_t launch_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <class T, class TO, int BM, int BN, int WM, int WN, int STAGES>
+template <class T, class TO, int BM, int BN, int WM, int WN, int STAGES, int KSPLIT = 1>
 hipError_t launch_dma_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s) {
     GemmArgs a = a0;
     a.tiles_m = (a.m + BM - 1) / BM;
     a.tiles_n = (a.n + BN - 1) / BN;
     dim3 grid(a.tiles_m * a.tiles_n, batch);
-    dim3 block(64 * WM * WN);
+    dim3 block(64 * WM * WN * KSPLIT);
     if constexpr (sizeof(typename T::raw) == 2) {
         if (nn) {
-            gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, true, STAGES><<<grid, block, 0, s>>>(a);
+            gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, true, STAGES, KSPLIT><<<grid, block, 0, s>>>(a);
             return hipGetLastError();
         }
     }
-    gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, false, STAGES><<<grid, block, 0, s>>>(a);
+    gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, false, STAGES, KSPLIT><<<grid, block, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -740,6 +757,12 @@ hipError_t launch_dma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
     if (tiles(256, 256) >= 192) return launch_dma_tile<T, TO, 256, 256, 2, 4, 2>(a, nn, batch, s);
     if (tiles(128, 128) >= 384) return launch_dma_tile<T, TO, 128, 128, 2, 2, 2>(a, nn, batch, s);
     if (tiles(64, 64) >= 768) return launch_dma_tile<T, TO, 64, 64, 2, 2, 2>(a, nn, batch, s);
+    // Fewer 64 x 64 tiles than CUs: split each tile's k loop over 2 or 4 wave
+    // groups of one workgroup (at least 4 k steps each), so the serial chain per
+    // tile shortens while the workgroup still has a CU to itself.
+    const int kt = a.k / (128 / (int)sizeof(typename T::raw));
+    if (tiles(64, 64) < 256 && kt % 4 == 0 && kt >= 16) return launch_dma_tile<T, TO, 64, 64, 2, 2, 2, 4>(a, nn, batch, s);
+    if (tiles(64, 64) < 256 && kt % 2 == 0 && kt >= 8) return launch_dma_tile<T, TO, 64, 64, 2, 2, 4, 2>(a, nn, batch, s);
     return launch_dma_tile<T, TO, 64, 64, 2, 2, 4>(a, nn, batch, s);
 }
 
