@@ -443,22 +443,16 @@ def main() -> int:
         for _ in range(20):
             ops.gemm(A, B, C)
         torch.cuda.synchronize()
-    ms = time_launches(lambda: ops.gemm(A, B, C), args.steps, args.warmup, torch)
-    tflops = flops / (ms * 1e-3) / 1e12
-    traffic = read_traffic(TRAFFIC_FILE)
-    roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                "kernel": "gemm_mfma_dma_kernel<BF16,BF16,256,256,2,4,NN=true>",
-                "algorithmic_flops_per_launch": flops, "avg_launch_ms": round(ms, 5)}
 
     if want("gemm") and not args.quick:
         Wt = (torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16)
+        ms_nn = time_launches(lambda: ops.gemm(A, B, C), args.steps, args.warmup, torch)
         ms_nt = time_launches(lambda: ops.gemm(A, Wt.t(), C), args.steps, args.warmup, torch)
         ms_torch = time_launches(lambda: torch.matmul(A, B, out=C), args.steps, args.warmup, torch)
         A16, B16, C16 = A.to(torch.float16), B.to(torch.float16), torch.empty_like(C, dtype=torch.float16)
         ms_f16 = time_launches(lambda: ops.gemm(A16, B16, C16), args.steps, args.warmup, torch)
         del A16, B16, C16
-        sections["gemm_4096_bf16"] = {"NN_tflops": round(tflops, 2), "NT_tflops": round(flops / ms_nt / 1e9, 2),
+        sections["gemm_4096_bf16"] = {"NN_tflops": round(flops / ms_nn / 1e9, 2), "NT_tflops": round(flops / ms_nt / 1e9, 2),
                                       "torch_hipblaslt_NN_tflops": round(flops / ms_torch / 1e9, 2),
                                       "NN_fp16_tflops": round(flops / ms_f16 / 1e9, 2)}
         del Wt
@@ -597,6 +591,14 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     # ---- the timed headline region: exactly K steps, synchronised both sides ----
+    # The sections above end with host-side work (checkpoint I/O, CPU timing),
+    # during which the GPU idles and its clocks drop: settle them again with
+    # 0.5 s of the same GEMM (untimed), as before the kernel measurement.
+    t_end = time.perf_counter() + 0.5
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            ops.gemm(A, B, C)
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         ops.gemm(A, B, C)
     torch.cuda.synchronize()
@@ -607,6 +609,17 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
     value = flops / (ms_step * 1e-3) / 1e12
+
+    # Roofline of the headline kernel, right after the timed region (same clock
+    # state): the same K launches captured as one HIP graph and replayed, HIP
+    # events on the launch stream, so only the kernels are timed.
+    ms = time_launches(lambda: ops.gemm(A, B, C), args.steps, args.warmup, torch)
+    tflops = flops / (ms * 1e-3) / 1e12
+    traffic = read_traffic(TRAFFIC_FILE)
+    roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                "kernel": "gemm_mfma_dma_kernel<BF16,BF16,256,256,2,4,NN=true,STAGES=2>",
+                "algorithmic_flops_per_launch": flops, "avg_launch_ms": round(ms, 5)}
 
     cpu = None
     if not args.quick and not args.no_cpu:
@@ -636,7 +649,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (torch.randn, seed 0: A ~ N(0,1), B ~ N(0,0.02), bf16)",
         "config": {"workload": "bf16 GEMM M=N=K=4096, A [M,K] x B [K,N] row-major, fp32 accumulate, bf16 out "
-                               "(configs[1])", "M": M, "N": N, "K": K, "layout": "NN"},
+                               "(configs[1])", "M": M, "N": N, "K": K, "layout": "NN",
+                   "untimed_clock_settle_s": 0.5},
         "roofline": roofline,
         "cpu_baseline": cpu,
         **sections,

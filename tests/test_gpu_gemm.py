@@ -145,17 +145,16 @@ def test_batched_and_alpha_beta(orc, yt, dtype):
         assert rel_err(g[b], r) <= tol
 
 
-# Grids with fewer 64 x 64 tiles than CUs split each tile's k loop over 2 or 4
-# wave groups of one workgroup (bf16/fp16: k/64 steps, fp32: k/32): (130, 200,
-# 512) bf16 -> 2 groups, fp32 -> 4; (96, 192, 1024) -> 4; (64, 100, 256) fp32 -> 2.
-KSPLIT_SHAPES = [(130, 200, 512), (96, 192, 1024), (64, 100, 256), (1000, 1000, 2048)]
+# Grids with fewer 64 x 64 tiles than CUs take 64 x 32 tiles (two waves per
+# workgroup); (1000, 1000, 2048) x 2 batches stays on 64 x 64.
+SHORT_GRID_SHAPES = [(130, 200, 512), (96, 192, 1024), (64, 100, 256), (1000, 1000, 2048)]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("layout", ["NN", "NT"])
-@pytest.mark.parametrize("shape", KSPLIT_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_split_k_groups_alpha_beta(orc, yt, shape, layout, dtype):
-    """Short grids (k split inside the workgroup), batched, alpha/beta into an fp32 C."""
+@pytest.mark.parametrize("shape", SHORT_GRID_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_short_grid_tiles_alpha_beta(orc, yt, shape, layout, dtype):
+    """Short grids (64 x 32 tiles), batched, alpha/beta into an fp32 C, NN and NT."""
     M, N, K = shape
     Bt = 2
     rng = np.random.default_rng(M + 3 * N + 7 * K)

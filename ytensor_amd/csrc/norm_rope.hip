@@ -178,6 +178,39 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void* x, int64_t ld
     for (int i = threadIdx.x; i < n; i += 256) store_from_f32<TO>(yr, i, (load_as_f32<T>(xr, i) / den) * w[i]);
 }
 
+// rms_norm_kernel for n <= 256 * J: the same element-to-thread assignment and
+// operation order (so the same bits), with every load of the row and its
+// weights issued up front and the row kept in registers for the second pass
+// (one memory round trip instead of a dependent load per loop trip, and no
+// re-read). Indices past n re-read the last element, unused.
+template <class T, class TO, int J>
+__global__ __launch_bounds__(256) void rms_norm_reg_kernel(const void* x, int64_t ldx, const float* w, float eps,
+                                                           void* y, int64_t ldy, int n) {
+    const int64_t row = blockIdx.x;
+    const auto* xr = static_cast<const typename T::raw*>(x) + row * ldx;
+    auto* yr = static_cast<typename TO::raw*>(y) + row * ldy;
+    float v[J], wv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) v[j] = load_as_f32<T>(xr, min((int)threadIdx.x + 256 * j, n - 1));
+#pragma unroll
+    for (int j = 0; j < J; ++j) wv[j] = w[min((int)threadIdx.x + 256 * j, n - 1)];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        if ((int)threadIdx.x + 256 * j < n) ss = fmaf(v[j], v[j], ss);
+    __shared__ float part[4];
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float den = sqrtf(tot / (float)n + eps);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < n) store_from_f32<TO>(yr, i, (v[j] / den) * wv[j]);
+    }
+}
+
 namespace {
 
 template <class T>
@@ -194,7 +227,10 @@ hipError_t launch_norm_rope(const NormRopeArgs& a, int d, hipStream_t s) {
 template <class T, class TO>
 hipError_t launch_rms(int rows, int n, const void* x, int64_t ldx, const float* w, float eps, void* y, int64_t ldy,
                       hipStream_t s) {
-    rms_norm_kernel<T, TO><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
+    if (n <= 1024) rms_norm_reg_kernel<T, TO, 4><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
+    else if (n <= 2048) rms_norm_reg_kernel<T, TO, 8><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
+    else if (n <= 4096) rms_norm_reg_kernel<T, TO, 16><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
+    else rms_norm_kernel<T, TO><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
     return hipGetLastError();
 }
 
