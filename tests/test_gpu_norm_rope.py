@@ -66,7 +66,7 @@ def test_norm_rope_into_cache(orc, yt):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("rows,n", [(1, 1024), (37, 1024), (512, 1024), (5, 100)])
+@pytest.mark.parametrize("rows,n", [(1, 1024), (37, 1024), (512, 1024), (5, 100), (3, 2048), (2, 4000), (2, 5000)])
 def test_rms_norm_rows(orc, yt, dtype, rows, n):
     rng = np.random.default_rng(rows + n)
     x = rng.standard_normal((rows, n)).astype(np.float32)
