@@ -404,7 +404,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; --gpus > 1 is not supported (the multi-GPU "
-                                   "sharding is design-only, see DESIGN.md)", "n_gpus": args.gpus}))
+                                   "sharding is a design in this build, not code)", "n_gpus": args.gpus}))
         return 2
     import torch
     import ytensor_amd as yt

@@ -280,7 +280,7 @@ REXPORT int ref_yt_load(const char* path, const char* name, void* out, int64_t c
 }
 
 // ---------------------------------------------------------------------------
-// MATH backend, masked matmul and predicate masks (SURVEY row f3)
+// MATH backend, masked matmul and predicate masks
 // ---------------------------------------------------------------------------
 
 // yt::function::scaledDotProductAttention on fp32 [H, Lq, D] / [H, Lkv, D] /
