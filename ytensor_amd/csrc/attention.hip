@@ -831,12 +831,15 @@ __global__ __launch_bounds__(D) void attn_decode_merge(DecodeArgs a) {
     for (int q = 0; q < MAXS; ++q) M = fmaxf(M, s_m[q]);
     // Empty splits (m = -inf, also the padding) get weight 0: every split
     // writes finite l and o, so their terms add exact zeros and the result
-    // has the bits of skipping them in the sequential combine.
+    // has the bits of skipping them in the sequential combine. Thread q
+    // computes split q's weight once for the workgroup.
+    __shared__ float s_w[MAXS];
+    if (d < MAXS) s_w[d] = s_m[d] != -INFINITY ? exp2f(s_m[d] - M) : 0.f;
+    __syncthreads();
     float L = 0.f, acc = 0.f;
 #pragma unroll
     for (int q = 0; q < MAXS; ++q) {
-        const float ms = s_m[q];
-        const float w = ms != -INFINITY ? exp2f(ms - M) : 0.f;
+        const float w = s_w[q];
         L = fmaf(s_l[q], w, L);
         acc = fmaf(ov[q], w, acc);
     }
