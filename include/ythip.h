@@ -14,7 +14,8 @@
  *     (nothing was launched), or a positive hipError_t from the launch.
  *     ythip_last_error() returns the calling thread's last message.
  *   - No entry point allocates device memory: scratch space is passed in
- *     (the .yt file calls below own pinned HOST staging buffers).
+ *     (the .yt file calls below own pinned HOST staging buffers), except that
+ *     ythip_attn_decode_noalloc uses a fixed array the library holds per GPU.
  *   - No C++ exceptions cross this boundary.
  */
 #ifndef YTHIP_H
@@ -156,6 +157,25 @@ int ythip_attn_decode(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
                       const void* Kc, const void* Vc, const int64_t kv_str[3],
                       const int32_t* kv_len, void* O, const int64_t o_str[2],
                       float scale, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * ythip_attn_decode without a workspace argument. No counterpart in the
+ * reference: this entry point is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, hosts that forbid
+ * hipMalloc). It calls no allocating routine; the split-K partials go to a
+ * fixed array of ythip_attn_decode_noalloc_max_bytes() bytes (4 MiB) that the
+ * library holds once per GPU until the process ends. A call whose
+ * ythip_attn_decode_workspace_size(B, Hq, max_ctx, d) exceeds that returns
+ * YTHIP_EINVAL. All calls on one GPU share the array: calls that overlap on one
+ * GPU (other streams, other threads) race. Same kernels, same bits as
+ * ythip_attn_decode.
+ */
+size_t ythip_attn_decode_noalloc_max_bytes(void);
+int ythip_attn_decode_noalloc(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
+                              const void* Q, const int64_t q_str[2],
+                              const void* Kc, const void* Vc, const int64_t kv_str[3],
+                              const int32_t* kv_len, void* O, const int64_t o_str[2],
+                              float scale, void* stream);
 
 /*
  * One decode step's attention for the Qwen3 layer with the q/k norm and RoPE

@@ -51,6 +51,25 @@ def test_abi_version_and_argument_errors():
     assert st == -2  # head dim 96 unsupported
 
 
+def test_decode_noalloc_rejects_oversize_without_a_launch():
+    """ythip_attn_decode_noalloc refuses a shape whose split-K partials exceed
+    its fixed per-GPU array before touching the GPU (the pointers are never
+    dereferenced). B=128, Hq=64, d=128 needs 128*64*1*(128+2)*4 bytes > 4 MiB."""
+    import ytensor_amd
+    from ytensor_amd import _lib
+    lib = ytensor_amd.load()
+    cap = int(lib.ythip_attn_decode_noalloc_max_bytes())
+    assert cap == 4 << 20
+    need = int(lib.ythip_attn_decode_workspace_size(128, 64, 16, 128))
+    assert need == 128 * 64 * 130 * 4 > cap
+    fake = ctypes.c_void_p(256)
+    st = lib.ythip_attn_decode_noalloc(_lib.BF16, 128, 64, 8, 128, 16, fake, _lib.i64array([64 * 128, 128]),
+                                       fake, fake, _lib.i64array([8 * 16 * 128, 16 * 128, 128]), None,
+                                       fake, _lib.i64array([64 * 128, 128]), 0.0, None)
+    assert st == _lib.YTHIP_EINVAL
+    assert b"fixed array" in lib.ythip_last_error()
+
+
 def test_cpp_mirror_compiles_and_reports_errors(tmp_path):
     """include/ythip.hpp (yt::kernel::hip) builds with the host C++ compiler
     against libythip.so and maps argument errors to exceptions."""

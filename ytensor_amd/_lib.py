@@ -56,6 +56,8 @@ SIGNATURES = {
                                _I, _P, _L, _I, _F, _P, ctypes.c_size_t, _P]),
     "ythip_attn_decode_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I]),
     "ythip_attn_decode_splits": (_I, [_I, _I, _I]),
+    "ythip_attn_decode_noalloc_max_bytes": (ctypes.c_size_t, []),
+    "ythip_attn_decode_noalloc": (_I, [_I, _I, _I, _I, _I, _I, _P, _LP, _P, _P, _LP, _P, _P, _LP, _F, _P]),
     "ythip_attn_decode_rope": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _P, _L, _P, _P, _P, _LP, _P, _LP,
                                     _F, _P, ctypes.c_size_t, _P]),
     "ythip_attn_decode": (_I, [_I, _I, _I, _I, _I, _I, _P, _LP, _P, _P, _LP, _P, _P, _LP, _F, _P,

@@ -28,6 +28,7 @@
 //   merges the splits (log-sum-exp).
 
 #include <algorithm>
+#include <mutex>
 #include <cfloat>
 
 #include "common.hpp"
@@ -1068,6 +1069,77 @@ __attribute__((visibility("default"))) int ythip_attn_decode(int dtype, int B, i
         case YTHIP_F16: return status_of(launch_decode<F16>(a, d, G, s));
         default: return status_of(launch_decode<BF16>(a, d, G, s));
     }
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Decode attention without a caller workspace: the split-K partials live in a
+// fixed device array of this library, so the call allocates nothing. One copy
+// of the array per GPU (held until the process ends); every call on a GPU
+// shares it, so calls that overlap on one GPU (two streams, two threads) race.
+// Every split writes its whole partial before the merge reads it, so the
+// array needs no clearing between calls.
+// ---------------------------------------------------------------------------
+namespace ythip {
+namespace {
+
+constexpr size_t DEC_SCRATCH_BYTES = size_t(4) << 20;
+static __device__ __align__(256) float dec_scratch[DEC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[SCRATCH_MAX_DEVICES];
+
+// Device address of dec_scratch on the current device, looked up once per
+// device (the host-side name dec_scratch is not a device address).
+int scratch_for_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return status_of(e);
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+        return fail(YTHIP_EUNSUPPORTED, "ythip_attn_decode_noalloc: device %d beyond the %d supported", dev,
+                    SCRATCH_MAX_DEVICES);
+    std::lock_guard<std::mutex> lk(scratch_mu);
+    if (scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(dec_scratch));
+        if (e != hipSuccess) return status_of(e);
+        if (p == nullptr) return fail(YTHIP_EINVAL, "ythip_attn_decode_noalloc: no device address for the scratch");
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+}  // namespace ythip
+
+extern "C" {
+
+__attribute__((visibility("default"))) size_t ythip_attn_decode_noalloc_max_bytes(void) { return DEC_SCRATCH_BYTES; }
+
+__attribute__((visibility("default"))) int ythip_attn_decode_noalloc(int dtype, int B, int Hq, int Hkv, int d,
+                                                                     int max_ctx, const void* Q,
+                                                                     const int64_t q_str[2], const void* Kc,
+                                                                     const void* Vc, const int64_t kv_str[3],
+                                                                     const int32_t* kv_len, void* O,
+                                                                     const int64_t o_str[2], float scale,
+                                                                     void* stream) {
+    if (B < 0 || Hq < 0 || Hkv < 0 || max_ctx < 0)
+        return fail(YTHIP_EINVAL, "ythip_attn_decode_noalloc: negative size");
+    if ((int64_t)B * Hq == 0) return 0;
+    const size_t need = ythip_attn_decode_workspace_size(B, Hq, max_ctx > 0 ? max_ctx : 1, d > 0 ? d : 1);
+    if (need > DEC_SCRATCH_BYTES)
+        return fail(YTHIP_EINVAL,
+                    "ythip_attn_decode_noalloc: B=%d Hq=%d max_ctx=%d d=%d needs %zu bytes of split-K scratch, "
+                    "the fixed array holds %zu (use ythip_attn_decode with a workspace)",
+                    B, Hq, max_ctx, d, need, DEC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    const int st = scratch_for_current_device(&ws);
+    if (st != 0) return st;
+    return ythip_attn_decode(dtype, B, Hq, Hkv, d, max_ctx, Q, q_str, Kc, Vc, kv_str, kv_len, O, o_str, scale, ws,
+                             DEC_SCRATCH_BYTES, stream);
 }
 
 __attribute__((visibility("default"))) int ythip_attn_decode_splits(int B, int Hq, int max_ctx) {
