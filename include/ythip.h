@@ -58,6 +58,7 @@ enum ythip_mask_kind {
 };
 
 /* ABI version of this header; bumped on any signature change. */
+#define YTHIP_ABI_VERSION 2
 int ythip_abi_version(void);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
@@ -159,6 +160,41 @@ int ythip_attn_decode(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
                       float scale, void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * Device-resident decode state: int32[YTHIP_ST_WORDS] read by the decode-step
+ * kernels when they run (so one captured HIP graph serves every step) and
+ * advanced by ythip_argmax_step / ythip_argmax_finish. It carries the
+ * bookkeeping of the reference's ring KV cache (KVCache, example/qwen3/src/
+ * qwen3.cpp:57-126) and its RoPE start rule (Qwen3Model::forward, 365-375),
+ * for batch 1:
+ *   TOTAL    tokens written to the cache so far (KVCache::total_written)
+ *   SLOT     cache row of the next token, TOTAL % RING (KVCache::write_pos)
+ *   KV_LEN   keys the next token sees after its append, min(TOTAL + 1, RING)
+ *            (KVCache::cur_len); once the ring is full every row is visible,
+ *            which is what get_mask gives a single query (104-126)
+ *   ROPE_POS RoPE table row of the next token: TOTAL if TOTAL + 1 <= MAX_POS,
+ *            else min(TOTAL, RING) if that + 1 <= MAX_POS, else 0 (365-375)
+ *   RING     cache rows (KVCache::max_len; the reference sizes it MAX_POS)
+ *   MAX_POS  max_position_embeddings (RoPE table rows)
+ *   GENERATED / HISTORY  next history index / history capacity
+ *   ERROR    bits the kernels set instead of touching memory out of range:
+ *            1 = cache row outside the cache, 2 = RoPE row outside the table,
+ *            4 = history full (the token is still returned in *token)
+ */
+enum ythip_decode_state_field {
+    YTHIP_ST_GENERATED = 0,
+    YTHIP_ST_ROPE_POS = 1,
+    YTHIP_ST_KV_LEN = 2,
+    YTHIP_ST_SLOT = 3,
+    YTHIP_ST_TOTAL = 4,
+    YTHIP_ST_RING = 5,
+    YTHIP_ST_MAX_POS = 6,
+    YTHIP_ST_HISTORY = 7,
+    YTHIP_ST_ERROR = 8,
+    YTHIP_ST_WORDS = 16
+};
+enum ythip_decode_error { YTHIP_ST_ERR_CACHE = 1, YTHIP_ST_ERR_ROPE = 2, YTHIP_ST_ERR_HISTORY = 4 };
+
+/*
  * ythip_attn_decode without a workspace argument. No counterpart in the
  * reference: this entry point is for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, hosts that forbid
@@ -179,15 +215,17 @@ int ythip_attn_decode_noalloc(int dtype, int B, int Hq, int Hkv, int d, int max_
 
 /*
  * One decode step's attention for the Qwen3 layer with the q/k norm and RoPE
- * fused in: the equivalent of ythip_rmsnorm_rope (S = 1, dev_pos) followed by
- * ythip_attn_decode (kv_len = *dev_pos + 1), with the same bits:
+ * fused in: the equivalent of ythip_rmsnorm_rope (S = 1, dev_state) followed by
+ * ythip_attn_decode (kv_len = &dev_state[YTHIP_ST_KV_LEN]), with the same bits:
  *   qkv: the new token's projection row per batch entry (row b at qkv + b*ld_qkv),
  *        q heads, then k heads, then v heads (example/qwen3/src/qwen3.cpp:233-248);
- *   q, k <- RMSNorm (wq / wk, may be NULL) + RoPE at position p = *dev_pos (cos/sin
- *        may be NULL); k and v are written to the cache row p (kv_str as for
- *        ythip_attn_decode, K and V share it);
- *   O[b, h] = softmax(scale * q . K[0..p]^T) . V[0..p]  (the q_len == 1 path,
- *        src/kernel/avx2/flash_attention.inl:202-272).
+ *   q, k <- RMSNorm (wq / wk, may be NULL) + RoPE at table row
+ *        dev_state[YTHIP_ST_ROPE_POS] (cos/sin may be NULL; tab_rows rows);
+ *        k and v are written to cache row dev_state[YTHIP_ST_SLOT] (kv_str as
+ *        for ythip_attn_decode, K and V share it; max_ctx rows);
+ *   O[b, h] = softmax(scale * q . K[0..n)^T) . V[0..n), n = dev_state[YTHIP_ST_KV_LEN]
+ *        (the q_len == 1 path, src/kernel/avx2/flash_attention.inl:202-272).
+ * A slot or RoPE row out of range sets the ERROR bits and is not accessed.
  * workspace: ythip_attn_decode_workspace_size(B, Hq, max_ctx, d) bytes. With
  * O == NULL only the split-K partials are produced, in the workspace as
  * fp32 [B][Hq][S][d + 2] = (running max m in log2 units, sum l, o[d]) per
@@ -198,34 +236,38 @@ int ythip_attn_decode_noalloc(int dtype, int B, int Hq, int Hkv, int d, int max_
 int ythip_attn_decode_splits(int B, int Hq, int max_ctx);
 int ythip_attn_decode_rope(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
                            const void* qkv, int64_t ld_qkv, const float* wq, const float* wk, float eps,
-                           const float* cos_tab, const float* sin_tab, int64_t ld_tab, const int32_t* dev_pos,
-                           void* Kc, void* Vc, const int64_t kv_str[3], void* O, const int64_t o_str[2],
-                           float scale, void* workspace, size_t ws_bytes, void* stream);
+                           const float* cos_tab, const float* sin_tab, int64_t ld_tab, int tab_rows,
+                           int32_t* dev_state, void* Kc, void* Vc, const int64_t kv_str[3], void* O,
+                           const int64_t o_str[2], float scale, void* workspace, size_t ws_bytes, void* stream);
 
 /*
  * Fused per-head RMSNorm + rotate-half RoPE on the fused qkv projection output,
- * scattering Q to [B,Hq,S,d] and K/V into cache rows cache_pos + s:
+ * scattering Q to [B,Hq,S,d] and K/V into cache rows (cache_pos + s) % cache_rows
+ * (the ring write of KVCache::append, example/qwen3/src/qwen3.cpp:70-88):
  *   qkv: rows of (Hq + 2*Hkv)*d elements, row (b*S + s) at qkv + (b*S+s)*ld_qkv;
  *        q heads, then k heads, then v heads (example/qwen3/src/qwen3.cpp:233-238)
  *   q, k <- rmsNorm_(x, w, -1, eps) (src/function/normalization.inl:256-267)
  *   q, k <- rope with table row (pos0 + s) (example/qwen3/src/qwen3.cpp:522-559)
  *   v    <- copied unchanged
- * wq / wk (fp32 [d]) may be NULL to skip that norm; cos/sin (fp32 [*, ld_tab],
- * from RoPECache::precompute, qwen3.cpp:161-175) may be NULL to skip RoPE.
- * Output strides are (batch, head, row); d is contiguous. K/V outputs may be NULL.
+ * wq / wk (fp32 [d]) may be NULL to skip that norm; cos/sin (fp32 [tab_rows,
+ * ld_tab], from RoPECache::precompute, qwen3.cpp:161-175) may be NULL to skip RoPE.
+ * Output strides are (batch, head, row); d is contiguous. K/V outputs may be NULL;
+ * when given, 0 <= cache_pos < cache_rows and S <= cache_rows.
  * All tensors, rows, strides and tables must keep 16-byte alignment
  * (YTHIP_EUNSUPPORTED otherwise).
- * dev_pos: optional device int32; when given, pos0 and cache_pos are both read
- * from it when the kernel runs (a decode step captured once in a HIP graph).
+ * dev_state: optional decode-state record (see ythip_decode_state_field); when
+ * given, pos0 = dev_state[YTHIP_ST_ROPE_POS] and cache_pos = dev_state[YTHIP_ST_SLOT]
+ * are read when the kernel runs (a decode step captured once in a HIP graph);
+ * rows out of range then set its ERROR bits and are not accessed.
  */
 int ythip_rmsnorm_rope(int dtype, int B, int S, int Hq, int Hkv, int d,
                        const void* qkv, int64_t ld_qkv,
                        const float* wq, const float* wk, float eps,
-                       const float* cos_tab, const float* sin_tab, int64_t ld_tab, int pos0,
+                       const float* cos_tab, const float* sin_tab, int64_t ld_tab, int tab_rows, int pos0,
                        void* Qout, const int64_t q_str[3],
                        void* Kout, const int64_t k_str[3],
                        void* Vout, const int64_t v_str[3],
-                       int cache_pos, const int32_t* dev_pos, void* stream);
+                       int cache_rows, int cache_pos, int32_t* dev_state, void* stream);
 
 /*
  * RMSNorm over the last axis of [rows, n] (the hidden-state norms of the Qwen3
@@ -247,19 +289,30 @@ int ythip_silu_mul(int dtype_in, int dtype_out, int rows, int n, const void* gat
 
 /*
  * Embedding gather (Qwen3Model::forward, example/qwen3/src/qwen3.cpp:378-385):
- *   out[r][:] = table[ids[r]][:]   (table [V, n], ids device int32[rows])
+ *   out[r][:] = table[ids[r]][:]   (table [vocab, n], ids device int32[rows])
+ * An id outside [0, vocab) is never used as an address: its row is written
+ * as zeros (the reference indexes unchecked; hosts should reject such ids).
  */
-int ythip_embedding(int dtype_table, int dtype_out, int rows, int n, const void* table,
+int ythip_embedding(int dtype_table, int dtype_out, int rows, int n, int vocab, const void* table,
                     const int32_t* ids, void* out, int64_t ld_out, void* stream);
 
 /*
+ * The bias step of yt::function::linear(x, W, b) (src/function/ops.inl:93-104):
+ * the product x . W^T is already in `out` (rows x n, row stride ld_out, stored
+ * in dtype); the bias [n] of the same dtype is then added in that type,
+ *   out[r][j] = T(out[r][j] + bias[j]).
+ */
+int ythip_add_bias(int dtype, int rows, int n, void* out, int64_t ld_out, const void* bias, void* stream);
+
+/*
  * Greedy token selection over fp32 logits [n]: *token = first index of the
- * maximum. If state (device int32[3] = {generated, position, kv_len}) is given:
- * history[state[0]] = token (history may be NULL), then state[0] += 1,
- * state[1] += 1, state[2] = state[1] + 1 -- the counters the next decode step's
- * ythip_rmsnorm_rope (dev_pos = &state[1]) and ythip_attn_decode
- * (kv_len = &state[2]) read. Replaces the example's top-20 sampling
- * (qwen3.cpp:465-486) by argmax, as configs[4] specifies.
+ * maximum. If state (the decode-state record, see ythip_decode_state_field) is
+ * given, the token that was just run is counted as written and the record
+ * advances to the next token: history[GENERATED] = token (history may be NULL;
+ * past HISTORY entries the ERROR bit 4 is set instead), GENERATED += 1,
+ * TOTAL += 1, then SLOT, KV_LEN and ROPE_POS are derived from TOTAL, RING and
+ * MAX_POS. Replaces the example's top-20 sampling (qwen3.cpp:465-486) by
+ * argmax, as configs[4] specifies.
  */
 int ythip_argmax_step(int n, const float* logits, int32_t* token, int32_t* history,
                       int32_t* state, void* stream);

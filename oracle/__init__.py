@@ -54,6 +54,7 @@ def _bind(lib: ctypes.CDLL, prefix: str) -> ctypes.CDLL:
         "rope_precompute": (None, [_I, _I, _F, _P, _P]),
         "rope": (None, [_P, _I, _I, _I, _I, _P, _P]),
         "qwen3_generate": (_I, [_P, _P, _P, _P, _I, _I, _P, _P, _P]),
+        "qwen3_run": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
         "sgemm_masked": (None, [_P, _P, _P, _I, _I, _I, _F, _F, _L, _L, _L, _L, _L, _L, _P]),
         "sdpa_math": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _I]),
         "sdpa_ex": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _I, _I, _I]),
@@ -270,6 +271,29 @@ class CpuPath:
             raise ValueError(f"qwen3_generate failed ({st})")
         return toks, marg, lg0
 
+    def qwen3_run(self, cfg: "Qwen3Config", weights: np.ndarray, turns, logit_steps=()):
+        """Greedy multi-turn generation over one set of KV caches (the caches
+        wrap once more than cfg.max_pos tokens were written). turns: list of
+        (prompt tokens, n_steps). Returns (tokens, margins, logits [len(logit_steps), V])
+        with one token / margin per step of all turns in order."""
+        ci = np.array([cfg.hidden, cfg.layers, cfg.vocab, cfg.inter, cfg.n_heads, cfg.n_kv, cfg.head_dim,
+                       cfg.max_pos], dtype=np.int32)
+        cf = np.array([cfg.eps, cfg.theta], dtype=np.float32)
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        lens = np.array([len(p) for p, _ in turns], np.int32)
+        steps = np.array([n for _, n in turns], np.int32)
+        prompts = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int32) for p, _ in turns]))
+        total = int(steps.sum())
+        toks = np.zeros(total, np.int32)
+        marg = np.zeros(total, np.float32)
+        ls = np.ascontiguousarray(np.asarray(logit_steps, np.int32).reshape(-1))
+        lg = np.zeros((max(len(ls), 1), cfg.vocab), np.float32)
+        st = self._fn("qwen3_run")(_ptr(ci), _ptr(cf), _ptr(w), len(turns), _ptr(lens), _ptr(prompts), _ptr(steps),
+                                   _ptr(toks), _ptr(marg), _ptr(ls) if len(ls) else None, len(ls), _ptr(lg))
+        if st != 0:
+            raise ValueError(f"qwen3_run failed ({st})")
+        return toks, marg, lg[:len(ls)]
+
     # --- .yt files (the compiled reference's yt::io::YTensorIO only) ----------
     def yt_save(self, path: str, tensors, compress: str = "", mode: int = 2) -> None:
         """tensors: [(name, typeName, shape, numpy payload)]; mode 2 = Write, 3 = Append."""
@@ -377,18 +401,27 @@ def qwen3_weight_layout(cfg: Qwen3Config) -> list[tuple[str, tuple[int, ...]]]:
     return out
 
 
-def qwen3_random_weights(path: CpuPath, cfg: Qwen3Config, seed: int = 3, scale: float = 0.02) -> np.ndarray:
+def qwen3_random_weights(path: CpuPath, cfg: Qwen3Config, seed: int = 3, scale: float = 0.02,
+                         norm_spread: float | None = None) -> np.ndarray:
     """configs[4] init: YTensor::seed(seed), then every tensor randn * 0.02 in the
     layout order (norm weights included), rounded to bf16 and up-converted:
-    returns the flat fp32 buffer of the bf16-representable weights."""
+    returns the flat fp32 buffer of the bf16-representable weights.
+
+    norm_spread: the discriminating variant -- the same stream, but every RMSNorm
+    weight (q_norm, k_norm, norm1, norm2, final norm) is 1 + norm_spread * randn
+    instead of randn * scale, so the activations keep their scale through the
+    layers and the greedy stream moves from token to token."""
     path.seed(seed)
     total = sum(int(np.prod(s)) for _, s in qwen3_weight_layout(cfg))
     flat = np.empty(total, np.float32)
     off = 0
-    for _, shp in qwen3_weight_layout(cfg):
+    for name, shp in qwen3_weight_layout(cfg):
         n = int(np.prod(shp))
         x = path.randn(n)
-        x *= np.float32(scale)
+        if norm_spread is not None and "norm" in name:
+            x = (np.float32(1.0) + x * np.float32(norm_spread)).astype(np.float32)
+        else:
+            x *= np.float32(scale)
         flat[off:off + n] = path.bf16_to_f32(path.bf16_round(x))
         off += n
     return flat

@@ -151,10 +151,13 @@ REXPORT void ref_rope(float* x, int B, int H, int L, int D, const float* cosv, c
 
 // The reference's own Qwen3ForCausalLM (example/qwen3/src/qwen3.cpp), weights
 // filled from the same flat fp32 buffer the oracle takes (layout documented in
-// ytoracle.cpp), driven greedily: forward(prompt, chat_only=true), then
-// forward(token, false) per step, argmax on the returned logits.
-REXPORT int ref_qwen3_generate(const int* cfg_i, const float* cfg_f, const float* W, const int* prompt,
-                               int prompt_len, int n_steps, int* out_tokens, float* out_margins, float* logits0) {
+// ytoracle.cpp), driven greedily over n_turns turns with the KV caches kept
+// between turns, as repeated Qwen3ForCausalLM::generate calls keep them: per
+// turn forward(prompt, chat_only=true), then forward(token, false) per step,
+// argmax on the returned logits. Arguments as oracle_qwen3_run.
+REXPORT int ref_qwen3_run(const int* cfg_i, const float* cfg_f, const float* W, int n_turns, const int* prompt_lens,
+                          const int* prompts, const int* steps, int* out_tokens, float* out_margins,
+                          const int* logit_steps, int n_logit_steps, float* out_logits) {
     qwen3::Qwen3Config cfg;
     cfg.hidden_size = cfg_i[0];
     cfg.num_hidden_layers = cfg_i[1];
@@ -196,27 +199,40 @@ REXPORT int ref_qwen3_generate(const int* cfg_i, const float* cfg_f, const float
         L.norm2.weight = take1(H);
     }
     lm->model.norm.weight = take1(H);
-    yt::YTensor<int, 2> ids(1, prompt_len);
-    std::memcpy(ids.data(), prompt, sizeof(int) * prompt_len);
-    auto logits = lm->forward(ids, true);
-    for (int step = 0; step < n_steps; ++step) {
-        auto lc = logits.contiguous();
-        const float* lg = lc.data();
-        if (step == 0 && logits0) std::memcpy(logits0, lg, sizeof(float) * V);
-        int best = 0;
-        for (int j = 1; j < V; ++j) if (lg[j] > lg[best]) best = j;
-        float second = -INFINITY;
-        for (int j = 0; j < V; ++j) if (j != best && lg[j] > second) second = lg[j];
-        out_tokens[step] = best;
-        out_margins[step] = lg[best] - second;
-        if (step + 1 < n_steps) {
-            yt::YTensor<int, 2> nid(1, 1);
-            nid.at(0, 0) = best;
-            logits = lm->forward(nid, false);
+    int g = 0;
+    const int* pr = prompts;
+    for (int t = 0; t < n_turns; ++t) {
+        yt::YTensor<int, 2> ids(1, prompt_lens[t]);
+        std::memcpy(ids.data(), pr, sizeof(int) * prompt_lens[t]);
+        pr += prompt_lens[t];
+        auto logits = lm->forward(ids, true);
+        for (int step = 0; step < steps[t]; ++step, ++g) {
+            auto lc = logits.contiguous();
+            const float* lg = lc.data();
+            for (int q = 0; q < n_logit_steps; ++q)
+                if (out_logits && logit_steps[q] == g) std::memcpy(out_logits + static_cast<size_t>(q) * V, lg, sizeof(float) * V);
+            int best = 0;
+            for (int j = 1; j < V; ++j) if (lg[j] > lg[best]) best = j;
+            float second = -INFINITY;
+            for (int j = 0; j < V; ++j) if (j != best && lg[j] > second) second = lg[j];
+            out_tokens[g] = best;
+            out_margins[g] = lg[best] - second;
+            if (step + 1 < steps[t]) {
+                yt::YTensor<int, 2> nid(1, 1);
+                nid.at(0, 0) = best;
+                logits = lm->forward(nid, false);
+            }
         }
     }
     delete lm;
     return 0;
+}
+
+REXPORT int ref_qwen3_generate(const int* cfg_i, const float* cfg_f, const float* W, const int* prompt,
+                               int prompt_len, int n_steps, int* out_tokens, float* out_margins, float* logits0) {
+    const int zero = 0;
+    return ref_qwen3_run(cfg_i, cfg_f, W, 1, &prompt_len, prompt, &n_steps, out_tokens, out_margins, &zero,
+                         logits0 ? 1 : 0, logits0);
 }
 
 // ---------------------------------------------------------------------------

@@ -25,6 +25,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <immintrin.h>
 #include <limits>
 #include <random>
 #include <vector>
@@ -232,39 +233,90 @@ void gemv_row(const float* A, const float* B, float* C, int n, int k, float alph
 // route (row/row/row, col/col/col, W^T cache, A^T cache) computes each output
 // as one FMA chain over k = 0..K-1 starting from +0: later kc panels reload C
 // and continue the chain (kernel_row_full_accum_fast, 174-202).
-// Implementation: row-major staging of B, then C[i][:] updated rank-1 per p in
-// p order (identical chain per element), OpenMP over rows.
+// Implementation (this oracle's own tiling; only the per-element chain has to
+// match): B is packed into 24-column strips, k runs in blocks of 256, and a
+// 4-row x 24-column register tile (12 AVX2 accumulators) advances every output
+// by one FMA per k in k order; between k blocks the tile is stored and
+// reloaded, which is exact. Edge rows / columns run the same chain in scalar
+// std::fma. OpenMP over the row blocks of a k block.
 // ---------------------------------------------------------------------------
 void gemm_chain(const float* A, int64_t rsa, int64_t csa, const float* B, int64_t rsb, int64_t csb,
                 float* C, int64_t rsc, int64_t csc, int m, int n, int k) {
-    std::vector<float> Bt(static_cast<size_t>(k) * n);
+    constexpr int MR = 4, NR = 24, KB = 256;
+    const int nstrip = (n + NR - 1) / NR;
+    // packed B: strip s, row p -> Bp[(s * k + p) * NR + jj], zero-padded past n
+    std::vector<float> Bp(static_cast<size_t>(nstrip) * k * NR);
 #pragma omp parallel for schedule(static)
-    for (int p = 0; p < k; ++p)
-        for (int j = 0; j < n; ++j) Bt[static_cast<size_t>(p) * n + j] = B[p * rsb + j * csb];
-    // Cache blocking over (8 rows) x (1024 columns); the k loop stays innermost
-    // per block in p order, so each element's chain is unchanged.
-    constexpr int RB = 8, JB = 1024;
-    const int nrb = (m + RB - 1) / RB, njb = (n + JB - 1) / JB;
-#pragma omp parallel
-    {
-        std::vector<float> cblk(static_cast<size_t>(RB) * JB);
-#pragma omp for schedule(dynamic, 1)
-        for (int64_t blk = 0; blk < static_cast<int64_t>(nrb) * njb; ++blk) {
-            const int i0 = static_cast<int>(blk / njb) * RB, j0 = static_cast<int>(blk % njb) * JB;
-            const int ri = std::min(RB, m - i0), jw = std::min(JB, n - j0);
-            std::fill(cblk.begin(), cblk.end(), 0.0f);
-            for (int p = 0; p < k; ++p) {
-                const float* b = &Bt[static_cast<size_t>(p) * n + j0];
-                for (int r = 0; r < ri; ++r) {
-                    const float a = A[(i0 + r) * rsa + p * csa];
-                    float* c = &cblk[static_cast<size_t>(r) * JB];
-                    for (int j = 0; j < jw; ++j) c[j] = std::fma(a, b[j], c[j]);
-                }
+    for (int sidx = 0; sidx < nstrip; ++sidx)
+        for (int p = 0; p < k; ++p)
+            for (int jj = 0; jj < NR; ++jj) {
+                const int j = sidx * NR + jj;
+                Bp[(static_cast<size_t>(sidx) * k + p) * NR + jj] = j < n ? B[p * rsb + j * csb] : 0.0f;
             }
-            for (int r = 0; r < ri; ++r)
-                for (int j = 0; j < jw; ++j) C[(i0 + r) * rsc + (j0 + j) * csc] = cblk[static_cast<size_t>(r) * JB + j];
+    const bool c_row = (csc == 1);
+    std::vector<float> Ctmp;
+    float* Cw = C;
+    int64_t ldc = rsc;
+    if (!c_row) {
+        Ctmp.assign(static_cast<size_t>(m) * n, 0.0f);
+        Cw = Ctmp.data();
+        ldc = n;
+    }
+    // Loop order: k block -> block of MB rows (its A panel, MB x KB, stays in
+    // L2) -> 24-column strip (KB x 24 of packed B, in L1) -> 4-row tiles.
+    constexpr int MB = 128;
+    const int nrb = (m + MB - 1) / MB;
+    for (int p0 = 0; p0 < k; p0 += KB) {
+        const int p1 = std::min(k, p0 + KB);
+        const bool first = (p0 == 0);
+#pragma omp parallel for schedule(dynamic, 1)
+        for (int rb = 0; rb < nrb; ++rb) {
+            const int r0 = rb * MB, r1 = std::min(m, r0 + MB);
+            const int rfull = r0 + (r1 - r0) / MR * MR;
+            for (int sidx = 0; sidx < nstrip; ++sidx) {
+                const int j0 = sidx * NR, nw = std::min(NR, n - j0);
+                const float* bs = &Bp[static_cast<size_t>(sidx) * k * NR];
+                if (nw == NR) {
+                    for (int i0 = r0; i0 < rfull; i0 += MR) {
+                        __m256 acc[MR][3];
+#pragma GCC unroll 4
+                        for (int r = 0; r < MR; ++r)
+#pragma GCC unroll 3
+                            for (int t = 0; t < 3; ++t)
+                                acc[r][t] = first ? _mm256_setzero_ps()
+                                                  : _mm256_loadu_ps(Cw + (i0 + r) * ldc + j0 + 8 * t);
+                        for (int p = p0; p < p1; ++p) {
+                            const __m256 b0 = _mm256_loadu_ps(bs + static_cast<size_t>(p) * NR);
+                            const __m256 b1 = _mm256_loadu_ps(bs + static_cast<size_t>(p) * NR + 8);
+                            const __m256 b2 = _mm256_loadu_ps(bs + static_cast<size_t>(p) * NR + 16);
+#pragma GCC unroll 4
+                            for (int r = 0; r < MR; ++r) {
+                                const __m256 a = _mm256_set1_ps(A[(i0 + r) * rsa + p * csa]);
+                                acc[r][0] = _mm256_fmadd_ps(a, b0, acc[r][0]);
+                                acc[r][1] = _mm256_fmadd_ps(a, b1, acc[r][1]);
+                                acc[r][2] = _mm256_fmadd_ps(a, b2, acc[r][2]);
+                            }
+                        }
+#pragma GCC unroll 4
+                        for (int r = 0; r < MR; ++r)
+#pragma GCC unroll 3
+                            for (int t = 0; t < 3; ++t) _mm256_storeu_ps(Cw + (i0 + r) * ldc + j0 + 8 * t, acc[r][t]);
+                    }
+                }
+                // edge rows (and a partial last strip): the same chain, scalar
+                for (int i = (nw == NR ? rfull : r0); i < r1; ++i)
+                    for (int jj = 0; jj < nw; ++jj) {
+                        float c = first ? 0.0f : Cw[i * ldc + j0 + jj];
+                        for (int p = p0; p < p1; ++p)
+                            c = std::fma(A[i * rsa + p * csa], bs[static_cast<size_t>(p) * NR + jj], c);
+                        Cw[i * ldc + j0 + jj] = c;
+                    }
+            }
         }
     }
+    if (!c_row)
+        for (int i = 0; i < m; ++i)
+            for (int j = 0; j < n; ++j) C[i * rsc + j * csc] = Ctmp[static_cast<size_t>(i) * n + j];
 }
 
 constexpr int KC_DEFAULT = 500;  // include/kernel/avx2/gemm_utils.hpp:55 (g_gemm_kc)
@@ -916,17 +968,22 @@ struct Q3Model {
 }  // namespace
 
 // cfg_i: H, L, V, I, nh, nkv, hd, max_pos ; cfg_f: eps, theta
-// Greedy generation: prompt forward with chat_only = true, then n_steps - 1
-// single-token steps (Qwen3ForCausalLM::generate, 506-516, with argmax in
-// place of the example's top-20 sampling). out_tokens[n_steps]; margins =
-// top1 - top2 logit per step; logits0 (optional [V]) = first step's logits.
-OEXPORT int oracle_qwen3_generate(const int* cfg_i, const float* cfg_f, const float* W, const int* prompt,
-                                  int prompt_len, int n_steps, int* out_tokens, float* out_margins,
-                                  float* logits0) {
+// Greedy multi-turn generation over one set of KV caches, as repeated calls of
+// Qwen3ForCausalLM::generate (506-516) do (the caches persist between calls;
+// argmax replaces the example's top-20 sampling): turn t runs its prompt
+// forward with chat_only = true, then steps[t] - 1 single-token steps; the
+// caches wrap as KVCache::append / get_mask do (57-126) once more than max_pos
+// tokens were written. out_tokens / out_margins (top1 - top2 logit) get one
+// entry per step of all turns in order; logits [n_logit_steps][V] (optional)
+// receives the logits of the global step indices listed in logit_steps.
+OEXPORT int oracle_qwen3_run(const int* cfg_i, const float* cfg_f, const float* W, int n_turns,
+                             const int* prompt_lens, const int* prompts, const int* steps, int* out_tokens,
+                             float* out_margins, const int* logit_steps, int n_logit_steps, float* logits) {
     Q3Model m;
     m.c = {cfg_i[0], cfg_i[1], cfg_i[2], cfg_i[3], cfg_i[4], cfg_i[5], cfg_i[6], cfg_i[7], cfg_f[0], cfg_f[1]};
     const Q3Cfg& c = m.c;
-    if (prompt_len <= 0 || prompt_len + n_steps > c.max_pos) return -1;
+    for (int t = 0; t < n_turns; ++t)
+        if (prompt_lens[t] <= 0 || prompt_lens[t] > c.max_pos || steps[t] <= 0) return -1;
     const float* p = W;
     m.embed = p;
     p += static_cast<size_t>(c.V) * c.H;
@@ -949,17 +1006,32 @@ OEXPORT int oracle_qwen3_generate(const int* cfg_i, const float* cfg_f, const fl
     m.cosv.resize(static_cast<size_t>(c.max_pos) * c.hd);
     m.sinv.resize(m.cosv.size());
     oracle_rope_precompute(c.hd, c.max_pos, c.theta, m.cosv.data(), m.sinv.data());
-    std::vector<int> ids(prompt, prompt + prompt_len);
-    for (int step = 0; step < n_steps; ++step) {
-        std::vector<float> lg = m.forward(ids.data(), static_cast<int>(ids.size()), step == 0);
-        if (step == 0 && logits0) std::memcpy(logits0, lg.data(), sizeof(float) * c.V);
-        int best = 0;
-        for (int j = 1; j < c.V; ++j) if (lg[j] > lg[best]) best = j;
-        float second = -std::numeric_limits<float>::infinity();
-        for (int j = 0; j < c.V; ++j) if (j != best && lg[j] > second) second = lg[j];
-        out_tokens[step] = best;
-        out_margins[step] = lg[best] - second;
-        ids.assign(1, best);
+    int g = 0;  // global step index
+    const int* pr = prompts;
+    for (int t = 0; t < n_turns; ++t) {
+        std::vector<int> ids(pr, pr + prompt_lens[t]);
+        pr += prompt_lens[t];
+        for (int step = 0; step < steps[t]; ++step, ++g) {
+            std::vector<float> lg = m.forward(ids.data(), static_cast<int>(ids.size()), step == 0);
+            for (int q = 0; q < n_logit_steps; ++q)
+                if (logits && logit_steps[q] == g) std::memcpy(logits + static_cast<size_t>(q) * c.V, lg.data(), sizeof(float) * c.V);
+            int best = 0;
+            for (int j = 1; j < c.V; ++j) if (lg[j] > lg[best]) best = j;
+            float second = -std::numeric_limits<float>::infinity();
+            for (int j = 0; j < c.V; ++j) if (j != best && lg[j] > second) second = lg[j];
+            out_tokens[g] = best;
+            out_margins[g] = lg[best] - second;
+            ids.assign(1, best);
+        }
     }
     return 0;
+}
+
+// Single turn of oracle_qwen3_run with the first step's logits (logits0, optional [V]).
+OEXPORT int oracle_qwen3_generate(const int* cfg_i, const float* cfg_f, const float* W, const int* prompt,
+                                  int prompt_len, int n_steps, int* out_tokens, float* out_margins,
+                                  float* logits0) {
+    const int zero = 0;
+    return oracle_qwen3_run(cfg_i, cfg_f, W, 1, &prompt_len, prompt, &n_steps, out_tokens, out_margins, &zero,
+                            logits0 ? 1 : 0, logits0);
 }

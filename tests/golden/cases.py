@@ -9,6 +9,15 @@ import oracle
 RANDN_SEEDS = (0, 1, 2, 3)
 RANDN_N = 1 << 20
 
+# The discriminating configs[4]-shaped model: configs[4]'s seeded stream,
+# layout and prompt, but matrices randn * 0.03 (about 1/sqrt(hidden)) and
+# RMSNorm weights 1 + 0.1 * randn, so the greedy stream moves (26 distinct
+# tokens in 32, top-2 margins >= 0.044; the literal configs[4] recipe, all
+# weights randn * 0.02, repeats one token). Larger matrix scales move the stream
+# too but make the 28-layer stack amplify perturbations: at 0.05 a bf16
+# activation path is 3e-2 off the fp32 logits, at 0.03 about 1.5e-2.
+QWEN3_VAR = {"seed": 3, "scale": 0.03, "norm_spread": 0.1, "prompt_len": 512, "prompt_seed": 4, "steps": 32}
+
 
 def digest(x: np.ndarray) -> str:
     """SHA-256 of the raw bytes (float32 arrays hash their bit patterns)."""

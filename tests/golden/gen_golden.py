@@ -11,6 +11,7 @@ regenerated in the tests from the pinned RNG, so only outputs are stored.
 
     python tests/golden/gen_golden.py            # small fixtures
     python tests/golden/gen_golden.py --qwen3    # + the configs[4] 0.6B run (minutes)
+    python tests/golden/gen_golden.py --qwen3-var  # only the discriminating 0.6B run (minutes)
 """
 from __future__ import annotations
 
@@ -31,10 +32,14 @@ import cases  # noqa: E402
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--qwen3", action="store_true")
+    ap.add_argument("--qwen3-var", action="store_true")
     args = ap.parse_args()
     ref = oracle.reference()
     if ref is None:
         raise SystemExit("oracle/_ref/libytref.so is not built (make -C oracle ref)")
+    if args.qwen3_var:
+        qwen3_var(ref)
+        return
     out = {}
     for s in cases.RANDN_SEEDS:
         ref.seed(s)
@@ -81,6 +86,29 @@ def main() -> None:
                             logits0_head=lg[:4096], logits0_sha256=np.array(cases.digest(lg)),
                             prompt=pr)
         print("wrote reference_qwen3_0p6b.npz", t)
+
+
+def qwen3_var(ref) -> None:
+    """The configs[4] shape with a discriminating random init: the same seeded
+    stream and layout as configs[4], matrices randn * 0.03 and every RMSNorm
+    weight 1 + 0.1 * randn (cases.QWEN3_VAR), the same 512-token prompt, 32
+    greedy steps through the reference's Qwen3ForCausalLM. Stored per step: the
+    token, the top-1 - top-2 margin, the logits' SHA-256, the 16 largest logits
+    (index, value) and the logits at 1024 fixed indices."""
+    cfg = oracle.Qwen3Config()
+    r = cases.QWEN3_VAR
+    W = oracle.qwen3_random_weights(ref, cfg, seed=r["seed"], scale=r["scale"], norm_spread=r["norm_spread"])
+    pr = oracle.qwen3_prompt(cfg, r["prompt_len"], seed=r["prompt_seed"])
+    steps = r["steps"]
+    t, m, lg = ref.qwen3_run(cfg, W, [(pr, steps)], logit_steps=list(range(steps)))
+    idx = cases.sample_index(cfg.vocab, 1024)
+    top = np.argsort(-lg, axis=1, kind="stable")[:, :16]
+    np.savez_compressed(os.path.join(HERE, "reference_qwen3_0p6b_var.npz"), tokens=t, margins=m,
+                        logits_sha256=np.array([cases.digest(x) for x in lg]),
+                        top_idx=top.astype(np.int32), top_val=np.take_along_axis(lg, top, 1),
+                        sample_idx=idx.astype(np.int32), sample_val=lg[:, idx], prompt=pr,
+                        recipe=np.array(repr(sorted(r.items()))))
+    print("wrote reference_qwen3_0p6b_var.npz", t.tolist(), "min margin", float(m.min()))
 
 
 if __name__ == "__main__":

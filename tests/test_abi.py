@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_argument_errors():
     import ytensor_amd
     lib = ytensor_amd.load()
-    assert lib.ythip_abi_version() == 1
+    assert lib.ythip_abi_version() == 2
     # invalid dtype / negative sizes are rejected before any HIP call
     st = lib.ythip_gemm(7, 0, 1, 2, 2, 2, None, 0, 2, 1, None, 0, 2, 1, None, 0, 2, 1, 1.0, 0.0, None)
     assert st == -1 and b"dtype" in lib.ythip_last_error()
@@ -46,8 +46,8 @@ def test_abi_version_and_argument_errors():
     assert st == -1
     # m == 0: a no-op that succeeds (src/kernel/avx2/sgemm.inl:594)
     assert lib.ythip_gemm(0, 0, 1, 0, 2, 2, None, 0, 2, 1, None, 0, 2, 1, None, 0, 2, 1, 1.0, 0.0, None) == 0
-    st = lib.ythip_rmsnorm_rope(2, 1, 1, 1, 1, 96, None, 0, None, None, 1e-6, None, None, 0, 0,
-                                None, None, None, None, None, None, 0, None, None)
+    st = lib.ythip_rmsnorm_rope(2, 1, 1, 1, 1, 96, None, 0, None, None, 1e-6, None, None, 0, 0, 0,
+                                None, None, None, None, None, None, 0, 0, None, None)
     assert st == -2  # head dim 96 unsupported
 
 

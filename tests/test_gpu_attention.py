@@ -188,10 +188,12 @@ def test_single_visible_key_and_zero_query(orc, yt):
 @pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("Hq,Hkv,d", [(16, 8, 128), (8, 8, 64), (16, 4, 128), (32, 4, 64)])
 def test_decode_attention_rope_equals_unfused(orc, yt, dtype, Hq, Hkv, d):
-    """ythip_attn_decode_rope == ythip_rmsnorm_rope (S = 1, dev_pos) followed
-    by ythip_attn_decode (kv_len = pos + 1): the same bits in the output, the
-    cache rows and (O == NULL) the split-K partials, over a run of positions
-    (the owner split moves across chunk boundaries)."""
+    """ythip_attn_decode_rope == ythip_rmsnorm_rope (S = 1, dev_state) followed
+    by ythip_attn_decode (kv_len = the record's KV_LEN): the same bits in the
+    output, the cache rows and (O == NULL) the split-K partials, over a run of
+    positions (the owner split moves across chunk boundaries), including
+    tokens past the ring's end (slot = total % rows, every row visible, RoPE
+    row 0 once max_pos is passed, as the reference's KVCache does)."""
     rng = np.random.default_rng(Hq * 7 + d)
     B, max_ctx = 2, 300
     dt = TORCH_DT[dtype]
@@ -209,15 +211,15 @@ def test_decode_attention_rope_equals_unfused(orc, yt, dtype, Hq, Hkv, d):
     ws = torch.empty(yt.ops.decode_workspace_bytes(B, Hq, max_ctx, d), dtype=torch.uint8, device="cuda")
     ws2 = torch.empty_like(ws)
     ws3 = torch.empty_like(ws)
-    for pos in (100, 101, 149, 150, 151, 299):
+    for pos in (100, 101, 149, 150, 151, 299, 300, 451):
         qkv = torch.from_numpy(rng.standard_normal((B, width)).astype(np.float32)).to("cuda").to(dt)
-        p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        p = yt.ops.decode_state(pos, max_ctx, max_ctx)
         o_f = torch.empty((B, Hq, d), dtype=dt, device="cuda")
         yt.ops.decode_attention_rope(qkv, Hq, Hkv, d, wq, wk, 1e-6, cos_d, sin_d, p, kc, vc, o_f, ws)
         qd = torch.empty((B, Hq, 1, d), dtype=dt, device="cuda")
         yt.rms_norm_rope(qkv.view(B, 1, width), Hq, Hkv, d, wq, wk, 1e-6, cos_d, sin_d, q_out=qd, k_out=kc2,
-                         v_out=vc2, dev_pos=p)
-        kvl = torch.full((B,), pos + 1, dtype=torch.int32, device="cuda")
+                         v_out=vc2, dev_state=p)
+        kvl = torch.full((B,), min(pos + 1, max_ctx), dtype=torch.int32, device="cuda")
         o_u = yt.decode_attention(qd.view(B, Hq, d), kc2, vc2, kv_len=kvl, workspace=ws2)
         torch.cuda.synchronize()
         assert torch.equal(o_f, o_u), (dtype, pos)
@@ -247,7 +249,7 @@ def test_gemv_attn_merge_equals_merge_then_gemv(yt, dtype, out_dtype, B, Hq, Hkv
     splits = yt.ops.decode_splits(B, Hq, max_ctx)
     for pos in sorted({0, 1, max_ctx // 3, max_ctx - 1}):
         qkv = torch.from_numpy(rng.standard_normal((B, width)).astype(np.float32)).to("cuda").to(dt)
-        p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        p = yt.ops.decode_state(pos, max_ctx, max_ctx)
         base = torch.from_numpy(rng.standard_normal((B, N)).astype(np.float32)).to("cuda").to(out_dtype)
         attn = torch.empty((B, Hq, d), dtype=dt, device="cuda")
         k1, v1 = kc.clone(), vc.clone()

@@ -203,3 +203,71 @@ def test_argument_errors(yt):
     with pytest.raises(ValueError):
         yt.matmul(torch.ones((3, 4), device="cuda", dtype=torch.float64),
                   torch.ones((4, 6), device="cuda", dtype=torch.float64))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_matmul_broadcasts_leading_dims(orc, yt, dtype):
+    """YTensor::matmul broadcasts the leading dims of both operands
+    (src/ytensor_math.inl:1021-1050, computeBroadcastShape): 2-D @ 3-D,
+    [1,3,M,K] @ [2,1,K,N] -> [2,3,M,N], a contiguous 4-D @ 2-D (batch-flatten
+    path), and unequal batch sizes raise."""
+    rng = np.random.default_rng(21)
+    M, K, N = 37, 64, 48
+    tol = REL_F32 if dtype == "f32" else REL_16
+    a2 = rng.standard_normal((M, K)).astype(np.float32)
+    b3 = rng.standard_normal((4, K, N)).astype(np.float32)
+    a2d, a2h = make_input(orc, a2, dtype)
+    b3d, b3h = make_input(orc, b3, dtype)
+    g = host_f32(yt.matmul(a2d, b3d, out_dtype=torch.float32))
+    assert g.shape == (4, M, N)
+    for i in range(4):
+        assert rel_err(g[i], orc.sgemm(a2h, b3h[i])) <= tol
+    a4 = rng.standard_normal((1, 3, M, K)).astype(np.float32)
+    b4 = rng.standard_normal((2, 1, K, N)).astype(np.float32)
+    a4d, a4h = make_input(orc, a4, dtype)
+    b4d, b4h = make_input(orc, b4, dtype)
+    g = host_f32(yt.matmul(a4d, b4d, out_dtype=torch.float32))
+    assert g.shape == (2, 3, M, N)
+    for i in range(2):
+        for j in range(3):
+            assert rel_err(g[i, j], orc.sgemm(a4h[0, j], b4h[i, 0])) <= tol
+    # contiguous [2,3,M,K] @ [K,N]: one flattened launch
+    a5 = rng.standard_normal((2, 3, M, K)).astype(np.float32)
+    a5d, a5h = make_input(orc, a5, dtype)
+    b2d, b2h = make_input(orc, b3[0], dtype)
+    g = host_f32(yt.matmul(a5d, b2d, out_dtype=torch.float32))
+    for i in range(2):
+        for j in range(3):
+            assert rel_err(g[i, j], orc.sgemm(a5h[i, j], b2h)) <= tol
+    with pytest.raises(ValueError):
+        yt.matmul(make_input(orc, rng.standard_normal((2, M, K)).astype(np.float32), dtype)[0],
+                  make_input(orc, rng.standard_normal((3, K, N)).astype(np.float32), dtype)[0])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_linear_bias_rounds_product_first(orc, yt, dtype):
+    """linear(x, W, b) (src/function/ops.inl:93-104): x.W^T is rounded to T,
+    then the bias is added in T. Bit-exact against that order applied to the
+    GPU's own unbiased product; the product itself within tolerance of the oracle."""
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((70, 96)).astype(np.float32)
+    W = (rng.standard_normal((130, 96)) * 0.5).astype(np.float32)
+    bvec = rng.standard_normal(130).astype(np.float32)
+    xd, xh = make_input(orc, x, dtype)
+    Wd, Wh = make_input(orc, W, dtype)
+    bd, bh = make_input(orc, bvec, dtype)
+    plain = yt.linear(xd, Wd)
+    biased = yt.linear(xd, Wd, bd)
+    tol = REL_F32 if dtype == "f32" else REL_16
+    r = orc.sgemm(xh, Wh, b_trans=True)
+    assert rel_err(host_f32(plain), r) <= tol
+    p = host_f32(plain).astype(np.float32)
+    s = (p + bh[None, :].astype(np.float32)).astype(np.float32)  # fp32 add of two T values
+    if dtype == "f32":
+        expect = s
+    else:
+        tt = torch.bfloat16 if dtype == "bf16" else torch.float16
+        expect = torch.from_numpy(s).to(tt).float().numpy()  # RNE to T, as the device stores
+    assert np.array_equal(host_f32(biased).view(np.uint32), expect.view(np.uint32))
+    with pytest.raises(ValueError):
+        yt.linear(xd, Wd, bd[:-1])

@@ -112,7 +112,7 @@ def test_lm_head_argmax_parts_match_argmax_step(yt, dev):
     for use_parts in (True, False):
         tok = torch.zeros((1,), dtype=torch.int32, device=dev)
         hist = torch.zeros((8,), dtype=torch.int32, device=dev)
-        state = torch.tensor([2, 40, 41], dtype=torch.int32, device=dev)
+        state = yt.ops.decode_state(40, 64, 64, generated=2, history=8, device=dev)
         lg = torch.empty((1, n), dtype=torch.float32, device=dev)
         if use_parts:
             yt.gemv_fused(x, w, lg, "rmsnorm", nw, 1e-6, argmax_parts=parts)
@@ -123,7 +123,9 @@ def test_lm_head_argmax_parts_match_argmax_step(yt, dev):
         torch.cuda.synchronize()
         assert int(tok.item()) == min(lo, win), (use_parts, int(tok.item()), lo, win)
         assert int(hist[2].item()) == int(tok.item())
-        assert state.tolist() == [3, 41, 42]
+        st = state.tolist()
+        assert (st[yt.ops.ST_GENERATED], st[yt.ops.ST_TOTAL], st[yt.ops.ST_SLOT], st[yt.ops.ST_KV_LEN],
+                st[yt.ops.ST_ROPE_POS], st[yt.ops.ST_ERROR]) == (3, 41, 41, 42, 41, 0)
         if use_parts:
             lg_fused = lg.clone()
         else:

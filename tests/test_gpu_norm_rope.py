@@ -65,6 +65,65 @@ def test_norm_rope_into_cache(orc, yt):
     assert np.all(kh[:, :, :cache_pos] == 7.0) and np.all(kh[:, :, cache_pos + S:] == 7.0)
 
 
+def test_norm_rope_ring_write_wraps(orc, yt):
+    """K/V rows go to (cache_pos + s) % rows, the ring write of KVCache::append
+    (example/qwen3/src/qwen3.cpp:70-88): 9 tokens from row 15 of a 20-row cache
+    land in rows 15..19 and 0..3; rows 4..14 are untouched."""
+    B, S, Hq, Hkv, d, cache_pos, rows = 1, 9, 4, 2, 128, 15, 20
+    rng = np.random.default_rng(44)
+    qkv = rng.standard_normal((B, S, (Hq + 2 * Hkv) * d)).astype(np.float32)
+    w = (rng.standard_normal(d) * 0.1 + 1.0).astype(np.float32)
+    cos, sin = orc.rope_tables(d, 64, 1e6)
+    kc = torch.full((B, Hkv, rows, d), 7.0, device="cuda")
+    vc = torch.full((B, Hkv, rows, d), 7.0, device="cuda")
+    yt.rms_norm_rope(dev_f32(qkv), Hq, Hkv, d, dev_f32(w), dev_f32(w), 1e-6, dev_f32(cos), dev_f32(sin),
+                     pos0=30, k_out=kc, v_out=vc, cache_pos=cache_pos)
+    rq, rk, rv = _oracle_norm_rope(orc, qkv, B, S, Hq, Hkv, d, w, w, 1e-6, cos, sin, 30)
+    kh, vh = host_f32(kc), host_f32(vc)
+    order = [(cache_pos + s) % rows for s in range(S)]
+    assert rel_err(kh[:, :, order], rk) <= 1e-4
+    assert np.array_equal(vh[:, :, order], rv)
+    assert np.all(kh[:, :, 4:15] == 7.0) and np.all(vh[:, :, 4:15] == 7.0)
+    with pytest.raises(ValueError):  # a host cache_pos outside the ring is refused before any launch
+        yt.rms_norm_rope(dev_f32(qkv), Hq, Hkv, d, None, None, 1e-6, None, None, k_out=kc, v_out=vc, cache_pos=rows)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_state_out_of_range_flags_and_skips(orc, yt, fused):
+    """A decode-state record whose cache slot or RoPE row lies outside the cache
+    / table sets the ERROR bits and neither writes the cache row nor reads the
+    table row. The cache and the tables are views into larger buffers with a
+    sentinel slab right behind them, so an access past the end would land in
+    owned memory and show up as a changed sentinel."""
+    ops = yt.ops
+    Hq, Hkv, d, rows, tab = 4, 2, 64, 32, 40
+    rng = np.random.default_rng(45)
+    big_k = torch.full((1, Hkv, rows + 4, d), 3.0, dtype=torch.bfloat16, device="cuda")
+    big_v = torch.full_like(big_k, 3.0)
+    kc, vc = big_k[:, :, :rows], big_v[:, :, :rows]
+    cos, sin = orc.rope_tables(d, tab + 4, 1e6)
+    cos_d, sin_d = dev_f32(cos), dev_f32(sin)
+    qkv = torch.from_numpy(rng.standard_normal((1, (Hq + 2 * Hkv) * d)).astype(np.float32)).cuda().to(torch.bfloat16)
+    ws = torch.empty(ops.decode_workspace_bytes(1, Hq, rows, d), dtype=torch.uint8, device="cuda")
+    for field, bad, bit in ((ops.ST_SLOT, rows, ops.ST_ERR_CACHE), (ops.ST_ROPE_POS, tab, ops.ST_ERR_ROPE)):
+        st = ops.decode_state(5, rows, tab)
+        st[field] = bad
+        before_k, before_v = big_k.clone(), big_v.clone()
+        if fused:
+            o = torch.empty((1, Hq, d), dtype=torch.bfloat16, device="cuda")
+            ops.decode_attention_rope(qkv, Hq, Hkv, d, None, None, 1e-6, cos_d[:tab], sin_d[:tab], st, kc, vc, o, ws)
+        else:
+            qd = torch.empty((1, Hq, 1, d), dtype=torch.bfloat16, device="cuda")
+            yt.rms_norm_rope(qkv.view(1, 1, -1), Hq, Hkv, d, None, None, 1e-6, cos_d[:tab], sin_d[:tab], q_out=qd,
+                             k_out=kc, v_out=vc, dev_state=st)
+        torch.cuda.synchronize()
+        assert int(st[ops.ST_ERROR]) & bit, (field, st.tolist())
+        assert torch.equal(big_k[:, :, rows:], before_k[:, :, rows:]) and torch.equal(big_v[:, :, rows:],
+                                                                                     before_v[:, :, rows:])
+        if field == ops.ST_SLOT:  # no cache row changed at all
+            assert torch.equal(big_k, before_k) and torch.equal(big_v, before_v)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,n", [(1, 1024), (37, 1024), (512, 1024), (5, 100), (3, 2048), (2, 4000), (2, 5000)])
 def test_rms_norm_rows(orc, yt, dtype, rows, n):

@@ -58,15 +58,16 @@ SIGNATURES = {
     "ythip_attn_decode_splits": (_I, [_I, _I, _I]),
     "ythip_attn_decode_noalloc_max_bytes": (ctypes.c_size_t, []),
     "ythip_attn_decode_noalloc": (_I, [_I, _I, _I, _I, _I, _I, _P, _LP, _P, _P, _LP, _P, _P, _LP, _F, _P]),
-    "ythip_attn_decode_rope": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _P, _L, _P, _P, _P, _LP, _P, _LP,
-                                    _F, _P, ctypes.c_size_t, _P]),
+    "ythip_attn_decode_rope": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _P, _L, _I, _P, _P, _P, _LP, _P,
+                                    _LP, _F, _P, ctypes.c_size_t, _P]),
     "ythip_attn_decode": (_I, [_I, _I, _I, _I, _I, _I, _P, _LP, _P, _P, _LP, _P, _P, _LP, _F, _P,
                                ctypes.c_size_t, _P]),
-    "ythip_rmsnorm_rope": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _P, _L, _I,
-                                _P, _LP, _P, _LP, _P, _LP, _I, _P, _P]),
+    "ythip_rmsnorm_rope": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _P, _L, _I, _I,
+                                _P, _LP, _P, _LP, _P, _LP, _I, _I, _P, _P]),
     "ythip_rms_norm": (_I, [_I, _I, _I, _I, _P, _L, _P, _F, _P, _L, _P]),
     "ythip_silu_mul": (_I, [_I, _I, _I, _I, _P, _L, _P, _L, _P]),
-    "ythip_embedding": (_I, [_I, _I, _I, _I, _P, _P, _P, _L, _P]),
+    "ythip_embedding": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _L, _P]),
+    "ythip_add_bias": (_I, [_I, _I, _I, _P, _L, _P, _P]),
     "ythip_argmax_step": (_I, [_I, _P, _P, _P, _P, _P]),
     "ythip_gemv_fused": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _F, _P, _L, _P, _L, _F, _F, _P, _P]),
     "ythip_gemv_swiglu": (_I, [_I, _I, _I, _I, _I, _P, _L, _P, _F, _P, _L, _P, _L, _P]),

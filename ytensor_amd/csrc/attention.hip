@@ -432,7 +432,8 @@ struct DecodeArgs {
     const float* cos_tab;
     const float* sin_tab;
     int64_t ld_tab;
-    const int32_t* dev_pos;
+    int tab_rows;
+    int32_t* dev_state;  // decode-state record: RoPE row, cache slot, visible keys
     int fused;
     int direct;  // splits == 1 and O given: the split kernel writes O itself
 };
@@ -508,12 +509,22 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
             }
         }
     }
-    int len, pos = -1;
-    bool owner = false;  // FUSED: this workgroup's chunk holds the new token's position
+    int len, pos = -1, rpos = 0;
+    bool owner = false;  // FUSED: this workgroup's chunk holds the new token's cache row
+    bool rope_ok = false;
     if constexpr (FUSED) {
-        pos = a.dev_pos[0];
-        len = min(pos + 1, a.max_ctx);
-        owner = pos >= 0 && pos < a.max_ctx && pos >= kbeg && pos < kbeg + a.chunk;
+        // the new token's cache row (ring slot), RoPE row and visible keys; rows
+        // out of range are flagged and never used as addresses
+        pos = a.dev_state[YTHIP_ST_SLOT];
+        rpos = a.dev_state[YTHIP_ST_ROPE_POS];
+        len = max(0, min(a.dev_state[YTHIP_ST_KV_LEN], a.max_ctx));
+        const bool slot_ok = pos >= 0 && pos < a.max_ctx;
+        rope_ok = rpos >= 0 && rpos < a.tab_rows;
+        owner = slot_ok && pos >= kbeg && pos < kbeg + a.chunk;
+        if (tid == 0 && split == 0 && kvh == 0 && b == 0) {
+            if (!slot_ok) atomicOr(&a.dev_state[YTHIP_ST_ERROR], (int)YTHIP_ST_ERR_CACHE);
+            if (a.cos_tab != nullptr && !rope_ok) atomicOr(&a.dev_state[YTHIP_ST_ERROR], (int)YTHIP_ST_ERR_ROPE);
+        }
     } else {
         len = a.kv_len ? min(a.kv_len[b], a.max_ctx) : a.max_ctx;
     }
@@ -579,8 +590,8 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     };
     // Fused: the RoPE rows of the position, then the first K/V batch.
     if constexpr (FUSED) {
-        if (prow && pr <= G && a.cos_tab != nullptr) {
-            const int64_t t = (int64_t)pos * a.ld_tab + 8 * pj;
+        if (prow && pr <= G && a.cos_tab != nullptr && rope_ok) {
+            const int64_t t = (int64_t)rpos * a.ld_tab + 8 * pj;
             cs[0] = *reinterpret_cast<const f32x4*>(a.cos_tab + t);
             cs[1] = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
             cs[2] = *reinterpret_cast<const f32x4*>(a.sin_tab + t);
@@ -636,7 +647,7 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
                     x2[e + 4] = (x2[e + 4] / den) * wd[e];
                 }
             }
-            if (r <= G && a.cos_tab != nullptr) {
+            if (r <= G && a.cos_tab != nullptr && rope_ok) {
                 const f32x4 c0 = cs[0], c1 = cs[1], s0 = cs[2], s1 = cs[3];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -1149,9 +1160,9 @@ __attribute__((visibility("default"))) int ythip_attn_decode_splits(int B, int H
 
 __attribute__((visibility("default"))) int ythip_attn_decode_rope(
     int dtype, int B, int Hq, int Hkv, int d, int max_ctx, const void* qkv, int64_t ld_qkv, const float* wq,
-    const float* wk, float eps, const float* cos_tab, const float* sin_tab, int64_t ld_tab, const int32_t* dev_pos,
-    void* Kc, void* Vc, const int64_t kv_str[3], void* O, const int64_t o_str[2], float scale, void* workspace,
-    size_t ws_bytes, void* stream) {
+    const float* wk, float eps, const float* cos_tab, const float* sin_tab, int64_t ld_tab, int tab_rows,
+    int32_t* dev_state, void* Kc, void* Vc, const int64_t kv_str[3], void* O, const int64_t o_str[2], float scale,
+    void* workspace, size_t ws_bytes, void* stream) {
     const char* who = "ythip_attn_decode_rope";
     if (B < 0 || Hq < 0 || Hkv < 0 || max_ctx <= 0) return fail(YTHIP_EINVAL, "%s: bad size", who);
     if ((int64_t)B * Hq == 0) return 0;
@@ -1160,8 +1171,9 @@ __attribute__((visibility("default"))) int ythip_attn_decode_rope(
     if (d != 64 && d != 128) return fail(YTHIP_EUNSUPPORTED, "%s: head dim %d (supported: 64, 128)", who, d);
     if (G != 1 && G != 2 && G != 4 && G != 8)
         return fail(YTHIP_EUNSUPPORTED, "%s: group size %d (supported: 1, 2, 4, 8)", who, G);
-    if (!qkv || !dev_pos || !Kc || !Vc || !kv_str || (O && !o_str) || (cos_tab == nullptr) != (sin_tab == nullptr))
+    if (!qkv || !dev_state || !Kc || !Vc || !kv_str || (O && !o_str) || (cos_tab == nullptr) != (sin_tab == nullptr))
         return fail(YTHIP_EINVAL, "%s: NULL pointer", who);
+    if (cos_tab != nullptr && (tab_rows <= 0 || ld_tab < d)) return fail(YTHIP_EINVAL, "%s: bad table args", who);
     if (dtype != YTHIP_F32 && dtype != YTHIP_F16 && dtype != YTHIP_BF16)
         return fail(YTHIP_EINVAL, "%s: invalid dtype %d", who, dtype);
     const int es = dtype == YTHIP_F32 ? 4 : 2;
@@ -1188,7 +1200,7 @@ __attribute__((visibility("default"))) int ythip_attn_decode_rope(
     a.scale_log2 = scale * LOG2E;
     a.ws = static_cast<float*>(workspace);
     a.qkv = qkv; a.ld_qkv = ld_qkv; a.wq = wq; a.wk = wk; a.eps = eps;
-    a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.ld_tab = ld_tab; a.dev_pos = dev_pos;
+    a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.ld_tab = ld_tab; a.tab_rows = tab_rows; a.dev_state = dev_state;
     a.fused = 1;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (dtype) {

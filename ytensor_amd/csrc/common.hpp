@@ -214,4 +214,30 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Elements per 16-byte chunk.
 template <class T> struct Vec { static constexpr int n = 16 / sizeof(typename T::raw); };
 
+// Decode-state record (include/ythip.h, ythip_decode_state_field): derive the
+// next token's cache row, visible key count and RoPE row from TOTAL, the ring
+// size and max_position_embeddings, as KVCache::append / get_mask and
+// Qwen3Model::forward's start rule do (example/qwen3/src/qwen3.cpp:70-126,
+// 365-375) for a one-token step.
+__host__ __device__ inline void decode_state_derive(int32_t* st) {
+    const int T = st[YTHIP_ST_TOTAL], L = st[YTHIP_ST_RING], P = st[YTHIP_ST_MAX_POS];
+    const int cur = T < L ? T : L;  // KVCache::cur_len before the append
+    st[YTHIP_ST_SLOT] = L > 0 ? T % L : 0;
+    st[YTHIP_ST_KV_LEN] = T + 1 < L ? T + 1 : L;
+    st[YTHIP_ST_ROPE_POS] = T + 1 <= P ? T : (cur + 1 <= P ? cur : 0);
+}
+
+// The argmax step's update (one thread): the token just run was written to the
+// cache; record the new token and advance to the next one.
+__device__ inline void decode_state_advance(int32_t* st, int32_t* history, int token) {
+    const int g = st[YTHIP_ST_GENERATED];
+    if (history != nullptr) {
+        if (g >= 0 && g < st[YTHIP_ST_HISTORY]) history[g] = token;
+        else st[YTHIP_ST_ERROR] |= YTHIP_ST_ERR_HISTORY;
+    }
+    st[YTHIP_ST_GENERATED] = g + 1;
+    st[YTHIP_ST_TOTAL] += 1;
+    decode_state_derive(st);
+}
+
 }  // namespace ythip

@@ -79,13 +79,27 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const void* gu, int64
     *reinterpret_cast<u32x4*>(static_cast<typename TO::raw*>(out) + (int64_t)r * ld_out + j) = o;
 }
 
+// Rows whose id is outside [0, vocab) get zeros: the id is never used as an
+// address.
 template <class T, class TO>
 __global__ __launch_bounds__(256) void embedding_kernel(const void* table, const int32_t* ids, void* out,
-                                                        int64_t ld_out, int n) {
+                                                        int64_t ld_out, int n, int vocab) {
     const int r = blockIdx.y;
     const int64_t row = ids[r];
+    const bool valid = row >= 0 && row < vocab;
     for (int j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256)
-        store_from_f32<TO>(out, (int64_t)r * ld_out + j, load_as_f32<T>(table, row * n + j));
+        store_from_f32<TO>(out, (int64_t)r * ld_out + j, valid ? load_as_f32<T>(table, row * n + j) : 0.0f);
+}
+
+// linear's bias (src/function/ops.inl:93-104): the product is already stored
+// (rounded to T); the bias is then added in T, out = T(out + bias).
+template <class T>
+__global__ __launch_bounds__(256) void add_bias_kernel(void* out, int64_t ld_out, const void* bias, int n) {
+    const int r = blockIdx.y;
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= n) return;
+    const int64_t i = (int64_t)r * ld_out + j;
+    store_from_f32<T>(out, i, load_as_f32<T>(out, i) + load_as_f32<T>(bias, j));
 }
 
 // One workgroup scans all n logits; ties resolve to the lowest index (the
@@ -116,12 +130,7 @@ __global__ __launch_bounds__(1024) void argmax_step_kernel(const float* x, int n
             if (sb[w] > b || (sb[w] == b && si[w] < id)) { b = sb[w]; id = si[w]; }
         if (id == 0x7fffffff) id = 0;  // all NaN / empty: token 0
         token[0] = id;
-        if (state != nullptr) {
-            if (history != nullptr) history[state[0]] = id;
-            state[0] += 1;            // tokens generated
-            state[1] += 1;            // cache position of the next token
-            state[2] = state[1] + 1;  // keys visible to the next decode step
-        }
+        if (state != nullptr) decode_state_advance(state, history, id);
     }
 }
 
@@ -144,10 +153,10 @@ hipError_t launch_silu(int rows, int n, const void* gu, int64_t ld_gu, void* out
 }
 
 template <class T, class TO>
-hipError_t launch_embed(int rows, int n, const void* table, const int32_t* ids, void* out, int64_t ld_out,
-                        hipStream_t s) {
+hipError_t launch_embed(int rows, int n, int vocab, const void* table, const int32_t* ids, void* out,
+                        int64_t ld_out, hipStream_t s) {
     dim3 grid((unsigned)((n + 255) / 256), rows);
-    embedding_kernel<T, TO><<<grid, 256, 0, s>>>(table, ids, out, ld_out, n);
+    embedding_kernel<T, TO><<<grid, 256, 0, s>>>(table, ids, out, ld_out, n, vocab);
     return hipGetLastError();
 }
 
@@ -183,15 +192,33 @@ __attribute__((visibility("default"))) int ythip_silu_mul(int dtype_in, int dtyp
 }
 
 __attribute__((visibility("default"))) int ythip_embedding(int dtype_table, int dtype_out, int rows, int n,
-                                                           const void* table, const int32_t* ids, void* out,
-                                                           int64_t ld_out, void* stream) {
-    if (rows < 0 || n < 0) return fail(YTHIP_EINVAL, "ythip_embedding: negative size");
+                                                           int vocab, const void* table, const int32_t* ids,
+                                                           void* out, int64_t ld_out, void* stream) {
+    if (rows < 0 || n < 0 || vocab < 0) return fail(YTHIP_EINVAL, "ythip_embedding: negative size");
     if ((int64_t)rows * n == 0) return 0;
+    if (rows > 65535) return fail(YTHIP_EUNSUPPORTED, "ythip_embedding: %d rows (at most 65535 per call)", rows);
     if (!table || !ids || !out || ld_out < n)
         return fail(YTHIP_EINVAL, "ythip_embedding: NULL pointer or leading dimension too small");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    YTHIP_DISPATCH2(dtype_table, dtype_out, launch_embed, rows, n, table, ids, out, ld_out, s);
+    YTHIP_DISPATCH2(dtype_table, dtype_out, launch_embed, rows, n, vocab, table, ids, out, ld_out, s);
     return fail(YTHIP_EUNSUPPORTED, "ythip_embedding: dtype pair %d/%d", dtype_table, dtype_out);
+}
+
+__attribute__((visibility("default"))) int ythip_add_bias(int dtype, int rows, int n, void* out, int64_t ld_out,
+                                                          const void* bias, void* stream) {
+    if (rows < 0 || n < 0) return fail(YTHIP_EINVAL, "ythip_add_bias: negative size");
+    if ((int64_t)rows * n == 0) return 0;
+    if (rows > 65535) return fail(YTHIP_EUNSUPPORTED, "ythip_add_bias: %d rows (at most 65535 per call)", rows);
+    if (!out || !bias || ld_out < n) return fail(YTHIP_EINVAL, "ythip_add_bias: NULL pointer or ld_out < n");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    dim3 grid((unsigned)((n + 255) / 256), rows);
+    switch (dtype) {
+        case YTHIP_F32: add_bias_kernel<F32><<<grid, 256, 0, s>>>(out, ld_out, bias, n); break;
+        case YTHIP_F16: add_bias_kernel<F16><<<grid, 256, 0, s>>>(out, ld_out, bias, n); break;
+        case YTHIP_BF16: add_bias_kernel<BF16><<<grid, 256, 0, s>>>(out, ld_out, bias, n); break;
+        default: return fail(YTHIP_EINVAL, "ythip_add_bias: invalid dtype %d", dtype);
+    }
+    return status_of(hipGetLastError());
 }
 
 __attribute__((visibility("default"))) int ythip_argmax_step(int n, const float* logits, int32_t* token,

@@ -596,12 +596,7 @@ __global__ __launch_bounds__(1024) void argmax_finish_kernel(const float* parts,
             if (sb[w] > b || (sb[w] == b && si[w] < id)) { b = sb[w]; id = si[w]; }
         if (id == 0x7fffffff) id = 0;  // all NaN / empty: token 0
         token[0] = id;
-        if (state != nullptr) {
-            if (history != nullptr) history[state[0]] = id;
-            state[0] += 1;
-            state[1] += 1;
-            state[2] = state[1] + 1;
-        }
+        if (state != nullptr) decode_state_advance(state, history, id);
     }
 }
 

@@ -36,7 +36,9 @@ struct NormRopeArgs {
     int64_t qs0, qs1, qs2, ks0, ks1, ks2, vs0, vs1, vs2;
     int B, S, Hq, Hkv;
     int cache_pos;
-    const int32_t* dev_pos;  // when set: pos0 = cache_pos = *dev_pos (graph-replayable decode)
+    int cache_rows;   // K/V rows are written at (cache_pos + s) % cache_rows (a ring)
+    int tab_rows;     // cos/sin rows
+    int32_t* dev_state;  // when set: pos0 / cache_pos from the decode-state record (graph-replayable decode)
 };
 
 // LPR lanes per (token, head) row of d = 2 * HALF: lane j of a row holds
@@ -57,8 +59,18 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
     const int tok = row / H;
     const int s = tok % a.S;
     const int b = tok / a.S;
-    const int pos0 = a.dev_pos ? a.dev_pos[0] : a.pos0;
-    const int cache_pos = a.dev_pos ? a.dev_pos[0] : a.cache_pos;
+    const int pos0 = a.dev_state ? a.dev_state[YTHIP_ST_ROPE_POS] : a.pos0;
+    const int cache_pos = a.dev_state ? a.dev_state[YTHIP_ST_SLOT] : a.cache_pos;
+    // A device-held position out of range is flagged and never used as an
+    // address (host positions were checked before the launch).
+    const bool rope_ok = pos0 >= 0 && pos0 + s < a.tab_rows;
+    const bool slot_ok = cache_pos >= 0 && cache_pos < a.cache_rows;
+    if (a.dev_state != nullptr && j == 0 && h == 0) {
+        if (a.cos_tab != nullptr && !rope_ok) atomicOr(&a.dev_state[YTHIP_ST_ERROR], (int)YTHIP_ST_ERR_ROPE);
+        if ((a.k != nullptr || a.v != nullptr) && !slot_ok)
+            atomicOr(&a.dev_state[YTHIP_ST_ERROR], (int)YTHIP_ST_ERR_CACHE);
+    }
+    const int64_t crow = slot_ok ? (cache_pos + s) % a.cache_rows : 0;
 
     const raw* src = static_cast<const raw*>(a.qkv) + (int64_t)tok * a.ld_qkv + (int64_t)h * D + 8 * j;
     float x1[8], x2[8];
@@ -107,7 +119,7 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
         wd = w2[1];
     }
     f32x4 c0 = {}, c1 = {}, s0 = {}, s1 = {};
-    if (a.cos_tab != nullptr) {
+    if (a.cos_tab != nullptr && rope_ok) {
         const int64_t t = (int64_t)(pos0 + s) * a.ld_tab + 8 * j;
         c0 = *reinterpret_cast<const f32x4*>(a.cos_tab + t);
         c1 = *reinterpret_cast<const f32x4*>(a.cos_tab + t + 4);
@@ -119,10 +131,11 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NormRopeArgs a) {
     if (is_q) {
         dst = static_cast<raw*>(a.q) + b * a.qs0 + h * a.qs1 + s * a.qs2;
     } else if (is_k) {
-        dst = static_cast<raw*>(a.k) + b * a.ks0 + (h - a.Hq) * a.ks1 + (int64_t)(cache_pos + s) * a.ks2;
+        if (!slot_ok) return;
+        dst = static_cast<raw*>(a.k) + b * a.ks0 + (h - a.Hq) * a.ks1 + crow * a.ks2;
     } else {
-        if (a.v == nullptr) return;
-        dst = static_cast<raw*>(a.v) + b * a.vs0 + (h - a.Hq - a.Hkv) * a.vs1 + (int64_t)(cache_pos + s) * a.vs2;
+        if (a.v == nullptr || !slot_ok) return;
+        dst = static_cast<raw*>(a.v) + b * a.vs0 + (h - a.Hq - a.Hkv) * a.vs1 + crow * a.vs2;
         store8(dst + 8 * j, x1);
         store8(dst + HALF + 8 * j, x2);
         return;
@@ -244,18 +257,25 @@ extern "C" {
 
 __attribute__((visibility("default"))) int ythip_rmsnorm_rope(
     int dtype, int B, int S, int Hq, int Hkv, int d, const void* qkv, int64_t ld_qkv, const float* wq,
-    const float* wk, float eps, const float* cos_tab, const float* sin_tab, int64_t ld_tab, int pos0, void* Qout,
-    const int64_t q_str[3], void* Kout, const int64_t k_str[3], void* Vout, const int64_t v_str[3], int cache_pos,
-    const int32_t* dev_pos, void* stream) {
+    const float* wk, float eps, const float* cos_tab, const float* sin_tab, int64_t ld_tab, int tab_rows, int pos0,
+    void* Qout, const int64_t q_str[3], void* Kout, const int64_t k_str[3], void* Vout, const int64_t v_str[3],
+    int cache_rows, int cache_pos, int32_t* dev_state, void* stream) {
     if (B < 0 || S < 0 || Hq < 0 || Hkv < 0) return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: negative size");
     if (d != 64 && d != 128) return fail(YTHIP_EUNSUPPORTED, "ythip_rmsnorm_rope: head dim %d (supported: 64, 128)", d);
     if ((int64_t)B * S * (Hq + 2 * Hkv) == 0) return 0;
     if (qkv == nullptr || Qout == nullptr || q_str == nullptr) return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: NULL qkv/Q");
     if ((cos_tab == nullptr) != (sin_tab == nullptr))
         return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: cos and sin must both be given or both NULL");
-    if (cos_tab != nullptr && (pos0 < 0 || ld_tab < d)) return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: bad table args");
-    if ((Kout != nullptr && k_str == nullptr) || (Vout != nullptr && v_str == nullptr) || cache_pos < 0)
+    if (cos_tab != nullptr && (ld_tab < d || tab_rows < 0))
+        return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: bad table args");
+    if (cos_tab != nullptr && dev_state == nullptr && (pos0 < 0 || (int64_t)pos0 + S > tab_rows))
+        return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: RoPE rows %d..%d outside the %d-row table", pos0,
+                    pos0 + S - 1, tab_rows);
+    if ((Kout != nullptr && k_str == nullptr) || (Vout != nullptr && v_str == nullptr))
         return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: bad K/V output args");
+    if ((Kout != nullptr || Vout != nullptr) &&
+        (cache_rows <= 0 || S > cache_rows || (dev_state == nullptr && (cache_pos < 0 || cache_pos >= cache_rows))))
+        return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: cache row %d / %d rows for S=%d", cache_pos, cache_rows, S);
     if (ld_qkv < (int64_t)(Hq + 2 * Hkv) * d) return fail(YTHIP_EINVAL, "ythip_rmsnorm_rope: ld_qkv too small");
     if ((int64_t)B * S * (Hq + 2 * Hkv) >= (int64_t)1 << 31)
         return fail(YTHIP_EUNSUPPORTED, "ythip_rmsnorm_rope: more than 2^31 rows");
@@ -282,7 +302,9 @@ __attribute__((visibility("default"))) int ythip_rmsnorm_rope(
     a.qs0 = q_str[0]; a.qs1 = q_str[1]; a.qs2 = q_str[2];
     if (k_str) { a.ks0 = k_str[0]; a.ks1 = k_str[1]; a.ks2 = k_str[2]; }
     if (v_str) { a.vs0 = v_str[0]; a.vs1 = v_str[1]; a.vs2 = v_str[2]; }
-    a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.cache_pos = cache_pos; a.dev_pos = dev_pos;
+    a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.cache_pos = cache_pos; a.dev_state = dev_state;
+    a.cache_rows = cache_rows > 0 ? cache_rows : 1;
+    a.tab_rows = tab_rows;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (dtype) {
         case YTHIP_F32: return status_of(launch_norm_rope<F32>(a, d, s));

@@ -36,7 +36,7 @@ using namespace ythip;
 
 extern "C" {
 
-__attribute__((visibility("default"))) int ythip_abi_version(void) { return 1; }
+__attribute__((visibility("default"))) int ythip_abi_version(void) { return YTHIP_ABI_VERSION; }
 
 __attribute__((visibility("default"))) const char* ythip_last_error(void) { return g_last_error; }
 

@@ -19,6 +19,7 @@ done here, mirroring src/function/ops.inl:123-128, 382-387).
 """
 from __future__ import annotations
 
+import itertools
 import math
 
 import torch
@@ -82,27 +83,44 @@ def gemm(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, alpha: float = 1.0
 
 
 def matmul(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """YTensor::matmul: a [..., M, K] @ b [K, N] (or same-batch [..., K, N])."""
+    """YTensor::matmul (src/ytensor_math.inl:284-316, 954-1051): a [..., M, K] @
+    b [..., K, N] over the last two dims, the leading dims broadcast against each
+    other (a size-1 dim repeats; unequal sizes raise, as computeBroadcastShape
+    does). Output [broadcast lead..., M, N]."""
+    if a.dim() < 2 or b.dim() < 2:
+        raise ValueError("matmul: both operands need at least 2 dimensions")
     out_dtype = out_dtype or a.dtype
-    lead = a.shape[:-2]
     m, k = a.shape[-2], a.shape[-1]
-    n = b.shape[-1]
-    if b.dim() == 2:
-        # Batch-flatten fast path (src/ytensor_math.inl:960-1017) when rows are uniform.
-        if a.dim() > 2 and a.is_contiguous():
+    kb, n = b.shape[-2], b.shape[-1]
+    if kb != k:
+        raise ValueError(f"matmul: inner dimensions differ ({k} vs {kb})")
+    try:
+        lead = tuple(torch.broadcast_shapes(a.shape[:-2], b.shape[:-2]))
+    except RuntimeError:
+        raise ValueError(f"matmul: batch dimensions {tuple(a.shape[:-2])} and {tuple(b.shape[:-2])} "
+                         "do not broadcast") from None
+    b_is_2d = all(s == 1 for s in b.shape[:-2])
+    if b_is_2d:
+        b2 = b.reshape(k, n) if b.dim() > 2 else b
+        # Batch-flatten fast path (src/ytensor_math.inl:960-1017): a's rows are
+        # uniform, so [..., M, K] is one [prod(lead) * M, K] product.
+        if a.dim() > 2 and a.is_contiguous() and tuple(a.shape[:-2]) == lead:
             a2 = a.reshape(-1, k)
             out = torch.empty((a2.shape[0], n), dtype=out_dtype, device=a.device)
-            gemm(a2, b, out)
+            gemm(a2, b2, out)
             return out.reshape(*lead, m, n)
-        a3 = a.reshape(-1, m, k) if a.dim() > 2 else a
-        out = torch.empty((*a3.shape[:-1], n), dtype=out_dtype, device=a.device)
-        gemm(a3, b, out)
-        return out.reshape(*lead, m, n)
-    a3 = a.reshape(-1, m, k)
-    b3 = b.reshape(-1, k, n)
-    out = torch.empty((a3.shape[0], m, n), dtype=out_dtype, device=a.device)
-    gemm(a3, b3, out)
-    return out.reshape(*lead, m, n)
+    out = torch.empty((*lead, m, n), dtype=out_dtype, device=a.device)
+    if not lead:
+        gemm(a, b, out)
+        return out
+    ae = a.expand(*lead, m, k)
+    be = b.expand(*lead, k, n)
+    # One batched launch over the last lead dim per index of the others (an
+    # expanded dim has stride 0, i.e. a shared operand).
+    outer = lead[:-1]
+    for idx in itertools.product(*[range(s) for s in outer]):
+        gemm(ae[idx], be[idx], out[idx])
+    return out
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
@@ -111,13 +129,22 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     k = x.shape[-1]
     if weight.shape[1] != k:
         raise ValueError(f"linear: weight has in_features {weight.shape[1]}, input has {k}")
-    x2 = x.reshape(-1, k)
-    out = torch.empty((x2.shape[0], weight.shape[0]), dtype=out_dtype or x.dtype, device=x.device)
+    out_dtype = out_dtype or x.dtype
     if bias is not None:
-        out.copy_(bias.to(out.dtype).expand_as(out))
-        gemm(x2, weight.t(), out, beta=1.0)
-    else:
-        gemm(x2, weight.t(), out)
+        if bias.dim() != 1 or bias.shape[0] != weight.shape[0]:
+            raise ValueError("linear: bias size must match weight.shape(0)")
+        if bias.dtype != out_dtype:
+            raise ValueError(f"linear: bias has dtype {bias.dtype}, the output {out_dtype}")
+        _dev(bias)
+    x2 = x.reshape(-1, k)
+    out = torch.empty((x2.shape[0], weight.shape[0]), dtype=out_dtype, device=x.device)
+    gemm(x2, weight.t(), out)
+    if bias is not None:
+        # ops.inl:93-104: the product is rounded to the output type first, then
+        # the bias is added in that type
+        b = bias.contiguous()
+        check(_lib.lib().ythip_add_bias(_code(out), out.shape[0], out.shape[1], out.data_ptr(), out.stride(0),
+                                        b.data_ptr(), _stream()), "ythip_add_bias")
     return out.reshape(*x.shape[:-1], weight.shape[0])
 
 
@@ -352,7 +379,9 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     if workspace is None or workspace.numel() * workspace.element_size() < ws_need:
         workspace = torch.empty(max(ws_need, 1), dtype=torch.uint8, device=q.device)
     if kv_len is not None:
-        kv_len = kv_len.to(torch.int32).contiguous()
+        if kv_len.dtype != torch.int32 or kv_len.numel() < B:
+            raise ValueError(f"kv_len must be an int32 device tensor with {B} entries")
+        kv_len = kv_len.contiguous()
     st = _lib.lib().ythip_attn_decode(
         _code(q), B, Hq, Hkv, D, ctx,
         q3.data_ptr(), i64array(q3.stride()[:2]),
@@ -370,15 +399,17 @@ def decode_splits(B: int, Hq: int, max_ctx: int) -> int:
 
 def decode_attention_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torch.Tensor | None,
                           wk: torch.Tensor | None, eps: float, cos: torch.Tensor | None, sin: torch.Tensor | None,
-                          dev_pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                          dev_state: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                           out: torch.Tensor | None, workspace: torch.Tensor, scale: float = 0.0):
     """One decode step of a Qwen3 attention layer: the new token's qkv row
-    [B, (Hq + 2 Hkv) d] gets per-head RMSNorm + RoPE at position *dev_pos, k/v
-    are appended to the caches [B, Hkv, max_ctx, d] there, and out [B, Hq, d] =
-    attention over keys 0..*dev_pos -- the same bits as rms_norm_rope followed
-    by decode_attention. With out=None the result stays as split-K partials in
-    `workspace` (decode_workspace_bytes)."""
-    _dev(qkv, k_cache, v_cache, workspace, dev_pos)
+    [B, (Hq + 2 Hkv) d] gets per-head RMSNorm + RoPE at the record's RoPE row,
+    k/v are written to the ring caches [B, Hkv, max_ctx, d] at its slot, and
+    out [B, Hq, d] = attention over the record's KV_LEN cache rows -- the same
+    bits as rms_norm_rope followed by decode_attention. With out=None the
+    result stays as split-K partials in `workspace` (decode_workspace_bytes)."""
+    _dev(qkv, k_cache, v_cache, workspace, dev_state)
+    if dev_state.dtype != torch.int32 or dev_state.numel() < ST_WORDS:
+        raise ValueError("dev_state must be the int32[16] decode-state record")
     B = qkv.shape[0]
     ctx = k_cache.shape[2]
     if k_cache.stride() != v_cache.stride():
@@ -390,7 +421,7 @@ def decode_attention_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torc
         _code(qkv), B, Hq, Hkv, d, ctx, qkv.data_ptr(), qkv.stride(0),
         None if wq is None else wq.data_ptr(), None if wk is None else wk.data_ptr(), float(eps),
         None if cos is None else cos.data_ptr(), None if sin is None else sin.data_ptr(),
-        0 if cos is None else cos.stride(0), dev_pos.data_ptr(),
+        0 if cos is None else cos.stride(0), 0 if cos is None else cos.shape[0], dev_state.data_ptr(),
         k_cache.data_ptr(), v_cache.data_ptr(), i64array(k_cache.stride()[:3]),
         None if o3 is None else o3.data_ptr(), None if o3 is None else i64array(o3.stride()[:2]), float(scale),
         workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream())
@@ -421,15 +452,48 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
     return out
 
 
+# Decode-state record fields (include/ythip.h, ythip_decode_state_field).
+ST_GENERATED, ST_ROPE_POS, ST_KV_LEN, ST_SLOT, ST_TOTAL, ST_RING, ST_MAX_POS, ST_HISTORY, ST_ERROR = range(9)
+ST_WORDS = 16
+ST_ERR_CACHE, ST_ERR_ROPE, ST_ERR_HISTORY = 1, 2, 4
+
+
+def decode_state_fields(total: int, ring: int, max_pos: int) -> tuple[int, int, int]:
+    """(slot, kv_len, rope_pos) of the next token once `total` tokens were
+    written to a ring KV cache of `ring` rows: KVCache::append / get_mask and
+    Qwen3Model::forward's start rule (example/qwen3/src/qwen3.cpp:70-126,
+    365-375) for a one-token step; the device derives the same values
+    (csrc/common.hpp, decode_state_derive)."""
+    cur = min(total, ring)
+    rope = total if total + 1 <= max_pos else (cur if cur + 1 <= max_pos else 0)
+    return total % ring, min(total + 1, ring), rope
+
+
+def decode_state(total: int, ring: int, max_pos: int, generated: int = 0, history: int = 0,
+                 device="cuda", out: torch.Tensor | None = None) -> torch.Tensor:
+    """The device decode-state record (int32[16]) for a next token after `total`
+    written tokens; written into `out` when given (a captured graph's record)."""
+    slot, kv_len, rope = decode_state_fields(total, ring, max_pos)
+    vals = [0] * ST_WORDS
+    vals[ST_GENERATED], vals[ST_ROPE_POS], vals[ST_KV_LEN], vals[ST_SLOT] = generated, rope, kv_len, slot
+    vals[ST_TOTAL], vals[ST_RING], vals[ST_MAX_POS], vals[ST_HISTORY] = total, ring, max_pos, history
+    t = torch.tensor(vals, dtype=torch.int32)
+    if out is None:
+        return t.to(device)
+    out.copy_(t)
+    return out
+
+
 def rms_norm_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torch.Tensor | None, wk: torch.Tensor | None,
                   eps: float, cos: torch.Tensor | None, sin: torch.Tensor | None, pos0: int = 0,
                   q_out: torch.Tensor | None = None, k_out: torch.Tensor | None = None,
-                  v_out: torch.Tensor | None = None, cache_pos: int = 0, dev_pos: torch.Tensor | None = None):
+                  v_out: torch.Tensor | None = None, cache_pos: int = 0, dev_state: torch.Tensor | None = None):
     """Fused per-head RMSNorm + RoPE on qkv [B, S, (Hq+2*Hkv)*d].
 
     Returns (q [B,Hq,S,d], k, v) where k/v are written to rows
-    cache_pos..cache_pos+S-1 of k_out/v_out [B,Hkv,*,d] when given (KV cache),
-    else to new [B,Hkv,S,d] tensors.
+    (cache_pos + s) % rows of k_out/v_out [B,Hkv,rows,d] when given (a ring KV
+    cache), else to new [B,Hkv,S,d] tensors. dev_state: the decode-state record,
+    whose RoPE row and cache slot replace pos0 / cache_pos when the kernel runs.
     """
     _dev(qkv)
     B, S, W = qkv.shape
@@ -445,12 +509,16 @@ def rms_norm_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torch.Tensor
     if v_out is None:
         v_out = torch.empty((B, Hkv, S, d), dtype=dt, device=dev)
     for name, t, h in (("q_out", q_out, Hq), ("k_out", k_out, Hkv), ("v_out", v_out, Hkv)):
-        rows_needed = S if (name == "q_out" or dev_pos is not None) else cache_pos + S
-        if t.dim() != 4 or t.shape[0] != B or t.shape[1] != h or t.shape[3] != d or t.shape[2] < rows_needed:
-            raise ValueError(f"{name} has shape {tuple(t.shape)}; needs [{B}, {h}, >={rows_needed}, {d}]")
+        if t.dim() != 4 or t.shape[0] != B or t.shape[1] != h or t.shape[3] != d or t.shape[2] < S:
+            raise ValueError(f"{name} has shape {tuple(t.shape)}; needs [{B}, {h}, >={S}, {d}]")
         if t.stride(3) != 1 or t.dtype != dt:
             raise ValueError(f"{name} must have a contiguous last dim and dtype {dt}")
-    if cos is not None and dev_pos is None and (cos.shape[0] < pos0 + S or cos.shape[1] < d):
+    cache_rows = k_out.shape[2]
+    if v_out.shape[2] != cache_rows:
+        raise ValueError("k_out and v_out must have the same number of rows")
+    if dev_state is None and not 0 <= cache_pos < cache_rows:
+        raise ValueError(f"cache_pos {cache_pos} outside the {cache_rows} cache rows")
+    if cos is not None and dev_state is None and (cos.shape[0] < pos0 + S or cos.shape[1] < d):
         raise ValueError(f"RoPE tables {tuple(cos.shape)} too small for positions {pos0}..{pos0 + S - 1}")
     keep = []
 
@@ -466,11 +534,12 @@ def rms_norm_rope(qkv: torch.Tensor, Hq: int, Hkv: int, d: int, wq: torch.Tensor
     st = _lib.lib().ythip_rmsnorm_rope(
         _code(qkv), B, S, Hq, Hkv, d, qkv.data_ptr(), qkv.stride(1),
         None if wq is None else wq.data_ptr(), None if wk is None else wk.data_ptr(), float(eps),
-        None if cos is None else cos.data_ptr(), None if sin is None else sin.data_ptr(), ld_tab, int(pos0),
+        None if cos is None else cos.data_ptr(), None if sin is None else sin.data_ptr(), ld_tab,
+        0 if cos is None else cos.shape[0], int(pos0),
         q_out.data_ptr(), i64array(q_out.stride()[:3]),
         k_out.data_ptr(), i64array(k_out.stride()[:3]),
         v_out.data_ptr(), i64array(v_out.stride()[:3]),
-        int(cache_pos), None if dev_pos is None else dev_pos.data_ptr(), _stream())
+        cache_rows, int(cache_pos), None if dev_state is None else dev_state.data_ptr(), _stream())
     check(st, "ythip_rmsnorm_rope")
     return q_out, k_out, v_out
 
@@ -493,15 +562,25 @@ def embedding(table: torch.Tensor, ids: torch.Tensor, out: torch.Tensor) -> torc
     _dev(table, ids, out)
     if ids.dtype != torch.int32:
         raise ValueError("ids must be int32")
-    check(_lib.lib().ythip_embedding(_code(table), _code(out), ids.numel(), table.shape[1], table.data_ptr(),
-                                     ids.data_ptr(), out.data_ptr(), out.stride(0), _stream()), "ythip_embedding")
+    check(_lib.lib().ythip_embedding(_code(table), _code(out), ids.numel(), table.shape[1], table.shape[0],
+                                     table.data_ptr(), ids.data_ptr(), out.data_ptr(), out.stride(0), _stream()),
+          "ythip_embedding")
     return out
+
+
+def _check_state(state: torch.Tensor | None) -> None:
+    """The argmax kernels advance a whole decode-state record (int32[16]);
+    its HISTORY field must not exceed the history buffer handed with it."""
+    if state is not None and (state.dtype != torch.int32 or state.numel() < ST_WORDS or not state.is_contiguous()):
+        raise ValueError("state must be the contiguous int32[16] decode-state record (ops.decode_state)")
 
 
 def argmax_step(logits: torch.Tensor, token: torch.Tensor, history: torch.Tensor | None = None,
                 state: torch.Tensor | None = None) -> torch.Tensor:
-    """Greedy token (first max index) into token[0]; optionally history/state updates."""
+    """Greedy token (first max index) into token[0]; optionally the history
+    entry and the decode-state record's advance (ythip_argmax_step)."""
     _dev(logits, token)
+    _check_state(state)
     if logits.dtype != torch.float32:
         raise ValueError("logits must be float32")
     check(_lib.lib().ythip_argmax_step(logits.numel(), logits.data_ptr(), token.data_ptr(),
@@ -613,6 +692,7 @@ def argmax_finish(parts: torch.Tensor, n_parts: int, token: torch.Tensor, histor
                   state: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy token from gemv_fused's per-tile (max, index) pairs; as argmax_step."""
     _dev(parts, token)
+    _check_state(state)
     check(_lib.lib().ythip_argmax_finish(parts.data_ptr(), int(n_parts), token.data_ptr(),
                                          None if history is None else history.data_ptr(),
                                          None if state is None else state.data_ptr(), _stream()), "ythip_argmax_finish")

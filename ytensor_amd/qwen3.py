@@ -103,7 +103,12 @@ class Qwen3:
     """Greedy batch-1 generation on one GPU."""
 
     def __init__(self, cfg: Qwen3Config, weights, device="cuda", max_ctx: int | None = None,
-                 max_prompt: int = 512, fused: bool = True, dtype: torch.dtype = torch.bfloat16):
+                 max_prompt: int = 512, fused: bool = True, dtype: torch.dtype = torch.bfloat16,
+                 max_tokens: int = 4096):
+        """max_ctx: rows of the ring KV cache (default max_position_embeddings, the
+        size the reference's KVCache::init gives it, qwen3.cpp:415-421; a smaller
+        ring saves memory and wraps earlier by the same rules). max_tokens:
+        history capacity, the most tokens one generate() call returns."""
         if dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("the decoder runs its matrices, activations and KV cache in bfloat16 or float16")
         self.cfg = cfg
@@ -112,6 +117,7 @@ class Qwen3:
         self.dev = torch.device(device)
         self.max_ctx = min(cfg.max_pos, max_ctx or cfg.max_pos)
         self.max_prompt = max_prompt
+        self.max_tokens = max_tokens
         self._upload(weights)
         self._alloc()
         self.graph = None
@@ -257,8 +263,12 @@ class Qwen3:
         self.logits = torch.empty((1, cfg.vocab), dtype=f32, device=dev)
         self.ids = torch.zeros((P,), dtype=torch.int32, device=dev)
         self.token = torch.zeros((1,), dtype=torch.int32, device=dev)
-        self.history = torch.zeros((self.max_ctx,), dtype=torch.int32, device=dev)
-        self.state = torch.zeros((3,), dtype=torch.int32, device=dev)  # generated, position, kv_len
+        self.history = torch.zeros((self.max_tokens,), dtype=torch.int32, device=dev)
+        # decode-state record (ring cache bookkeeping, include/ythip.h); `total`
+        # mirrors its TOTAL on the host between calls
+        self.state = ops.decode_state(0, self.max_ctx, cfg.max_pos, history=self.max_tokens, device=dev)
+        self.total = 0
+        self.mask = None  # bool mask of a prefill into a full ring (get_mask, qwen3.cpp:104-126)
         self.ws = torch.empty((ops.decode_workspace_bytes(1, nh, self.max_ctx, hd),), dtype=torch.uint8, device=dev)
         self.qd = torch.empty((1, nh, 1, hd), dtype=bf, device=dev)  # decode query
         self.amax = torch.empty((2 * ((cfg.vocab + 15) // 16),), dtype=f32, device=dev)  # LM-head tile maxima
@@ -269,7 +279,12 @@ class Qwen3:
         nh, hd = self.cfg.n_heads, self.cfg.head_dim
         return self.attn[:S].view(S, nh, hd).permute(1, 0, 2).unsqueeze(0)
 
-    def _layer(self, i: int, S: int, pos0: int, decode: bool) -> None:
+    def _layer(self, i: int, S: int, decode: bool, pre: dict | None = None) -> None:
+        """Layer i on S rows. Decode: one token at the decode-state record's
+        RoPE row / cache slot. Prefill: `pre` gives the RoPE start, the first
+        cache row of the ring write, the keys visible after the append and the
+        mask (None = causal over physical rows; a bool mask once the ring is
+        full, as get_mask builds it)."""
         cfg, L = self.cfg, self.layers[i]
         nh, nkv, hd = cfg.n_heads, cfg.n_kv, cfg.head_dim
         x, h = self.x[:S], self.h[:S]
@@ -282,14 +297,17 @@ class Qwen3:
         if decode:
             qv = self.qd
             ops.rms_norm_rope(self.qkv[:S].view(1, S, -1), nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
-                              q_out=qv, k_out=kc, v_out=vc, dev_pos=self.state[1:2])
-            ops.decode_attention(qv.view(1, nh, hd), kc, vc, kv_len=self.state[2:3],
+                              q_out=qv, k_out=kc, v_out=vc, dev_state=self.state)
+            kv_len = self.state[ops.ST_KV_LEN:ops.ST_KV_LEN + 1]
+            ops.decode_attention(qv.view(1, nh, hd), kc, vc, kv_len=kv_len,
                                  out=self.attn[:1].view(1, nh, hd), workspace=self.ws)
         else:
             qv = self.q[:, :, :S, :]
             ops.rms_norm_rope(self.qkv[:S].view(1, S, -1), nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
-                              pos0=pos0, q_out=qv, k_out=kc, v_out=vc, cache_pos=pos0)
-            ops.scaled_dot_product_attention(qv, kc[:, :, :pos0 + S], vc[:, :, :pos0 + S], 0.0, mask="causal",
+                              pos0=pre["start"], q_out=qv, k_out=kc, v_out=vc, cache_pos=pre["row"])
+            n = pre["kv_len"]
+            ops.scaled_dot_product_attention(qv, kc[:, :, :n], vc[:, :, :n], 0.0,
+                                             mask="causal" if pre["mask"] is None else pre["mask"],
                                              out=self._attn_view(S))
         ops.gemm(self.attn[:S], L["o"].t(), x, beta=1.0)          # x += attn . Wo^T
         ops.rms_norm(x, L["n2"], cfg.eps, out=h)
@@ -312,7 +330,7 @@ class Qwen3:
         # (partials in the workspace), then the merge of the splits as the o
         # projection's prologue
         ops.decode_attention_rope(self.qkv[:1], nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
-                                  self.state[1:2], kc, vc, None, self.ws)
+                                  self.state, kc, vc, None, self.ws)
         ops.gemv_attn_merge(self.ws, 1, nh, hd, self.max_ctx, L["o"], x, beta=1.0)  # x += attn . Wo^T
         ops.gemv_swiglu(x, L["gu"], self.act[:1], "rmsnorm", L["n2"], cfg.eps)    # act = swiglu(norm(x) . Wgu^T)
         ops.gemv_fused(self.act[:1], L["down"], x, beta=1.0)                      # x += act . Wdown^T
@@ -328,39 +346,72 @@ class Qwen3:
         ops.gemm(self.hf, self.lm_head.t(), self.logits)           # LM head (tied by default), fp32 logits
         ops.argmax_step(self.logits, self.token, self.history, self.state)
 
-    def _prefill_body(self, P: int) -> None:
+    def _prefill_body(self, P: int, pre: dict) -> None:
         ops.embedding(self.embed, self.ids[:P], self.x[:P])
         for i in range(self.cfg.layers):
-            self._layer(i, P, 0, decode=False)
+            self._layer(i, P, decode=False, pre=pre)
         self._head(P)
 
-    def prefill(self, prompt, use_graph: bool = False) -> None:
+    def _prefill_plan(self, P: int, t0: int) -> dict:
+        """Where a P-token prompt goes when t0 tokens are already in the ring:
+        the RoPE start (Qwen3Model::forward, qwen3.cpp:365-375), the first cache
+        row (KVCache::append, 70-88), the keys visible after the append and the
+        mask -- causal over physical rows while the ring has not wrapped, else
+        get_mask's logical-order mask (104-126)."""
+        ring, max_pos = self.max_ctx, self.cfg.max_pos
+        cur = min(t0, ring)
+        start = t0 if t0 > 0 else 0
+        if start + P > max_pos:
+            start = cur
+            if start + P > max_pos:
+                start = 0
+        kv_len = min(cur + P, ring)
+        mask = None
+        if t0 + P > ring:  # full after the append: keys in logical order (ki - write_pos) mod ring
+            wp = (t0 + P) % ring
+            ki = np.arange(kv_len)[None, :]
+            qi = np.arange(P)[:, None]
+            vis = ((ki - wp + ring) % ring) <= (kv_len - P) + qi
+            mask = torch.from_numpy(np.ascontiguousarray(vis, dtype=np.uint8)).to(self.dev)
+        return {"start": start, "row": t0 % ring, "kv_len": kv_len, "mask": mask}
+
+    def prefill(self, prompt, use_graph: bool = False, reset: bool = True) -> None:
         """Run the prompt; the first generated token lands in history[0].
 
-        With use_graph the prompt's launches (embedding, every layer, head) are
+        reset=False continues over the tokens already in the KV cache (a new
+        turn, as a second Qwen3ForCausalLM::generate call does): RoPE rows,
+        cache rows and the mask follow the reference's ring rules. With
+        use_graph a fresh prompt's launches (embedding, every layer, head) are
         captured once per prompt length as a HIP graph and replayed: the token
         ids and the decode state are device buffers written before the replay,
         so one capture serves every prompt of that length with the eager
-        path's bits."""
+        path's bits (a continued prompt runs eagerly)."""
         P = len(prompt)
-        if P > self.max_prompt or P >= self.max_ctx:
-            raise ValueError(f"prompt of {P} tokens exceeds max_prompt={self.max_prompt} / max_ctx={self.max_ctx}")
-        self.ids[:P].copy_(torch.as_tensor(np.asarray(prompt, dtype=np.int32)))
-        # state after the head's argmax: generated = 1, position = P, kv_len = P + 1
-        self.state.copy_(torch.tensor([0, P - 1, P], dtype=torch.int32))
-        if use_graph:
+        ids = np.asarray(prompt, dtype=np.int64)
+        if P == 0 or P > self.max_prompt or P > self.max_ctx or P > self.cfg.max_pos:
+            raise ValueError(f"prompt of {P} tokens: need 1 <= P <= max_prompt={self.max_prompt}, "
+                             f"max_ctx={self.max_ctx}, max_pos={self.cfg.max_pos}")
+        if ids.min() < 0 or ids.max() >= self.cfg.vocab:
+            raise ValueError(f"token ids must lie in [0, {self.cfg.vocab})")
+        t0 = 0 if reset else self.total
+        pre = self._prefill_plan(P, t0)
+        self.ids[:P].copy_(torch.from_numpy(ids.astype(np.int32)))
+        # the head's argmax counts the last prompt token as written: TOTAL = t0 + P after it
+        ops.decode_state(t0 + P - 1, self.max_ctx, self.cfg.max_pos, history=self.max_tokens, out=self.state)
+        if use_graph and t0 == 0:
             g = self.prefill_graphs.get(P)
             if g is None:
-                g = self.prefill_graphs[P] = self._capture(lambda: self._prefill_body(P))
+                g = self.prefill_graphs[P] = self._capture(lambda: self._prefill_body(P, pre))
             g.replay()
         else:
-            self._prefill_body(P)
+            self._prefill_body(P, pre)
         self.prompt_len = P
+        self.total = t0 + P
 
     def _decode_step(self) -> None:
         ops.embedding(self.embed, self.token, self.x[:1])
         for i in range(self.cfg.layers):
-            self._layer(i, 1, 0, decode=True)
+            self._layer(i, 1, decode=True)
         self._head(1)
 
     @staticmethod
@@ -379,12 +430,15 @@ class Qwen3:
         """Capture one decode step as a HIP graph (replayed per token)."""
         self.graph = self._capture(self._decode_step)
 
-    def generate(self, prompt, n_tokens: int, use_graph: bool = True) -> np.ndarray:
+    def generate(self, prompt, n_tokens: int, use_graph: bool = True, reset: bool = True) -> np.ndarray:
         """Greedy: prompt forward, then n_tokens - 1 decode steps. Returns the tokens.
-        use_graph replays captured graphs for both (one prefill graph per prompt length)."""
-        self.prefill(prompt, use_graph=use_graph)
-        if len(prompt) + n_tokens > self.max_ctx:
-            raise ValueError("max_ctx too small for prompt + generated tokens")
+        use_graph replays captured graphs for both (one prefill graph per prompt length).
+        reset=False keeps the KV cache of the previous calls (multi-turn, as the
+        reference's generate does); the ring wraps once more than max_ctx
+        tokens were written."""
+        if not 1 <= n_tokens <= self.max_tokens:
+            raise ValueError(f"n_tokens={n_tokens}: this model's history holds 1..{self.max_tokens} tokens")
+        self.prefill(prompt, use_graph=use_graph, reset=reset)
         if use_graph and self.graph is None:
             # capturing does not execute the step; state is untouched
             self.capture()
@@ -394,4 +448,16 @@ class Qwen3:
             else:
                 self._decode_step()
         torch.cuda.synchronize()
+        self.total += n_tokens - 1
+        self.check_state()
         return self.history[:n_tokens].cpu().numpy()
+
+    def check_state(self) -> None:
+        """Raise if a kernel flagged an out-of-range cache row, RoPE row or
+        history entry in the decode-state record (it never accesses them)."""
+        st = self.state.cpu().tolist()
+        if st[ops.ST_ERROR]:
+            raise RuntimeError(f"decode state error bits {st[ops.ST_ERROR]:#x} (1 cache row, 2 RoPE row, "
+                               f"4 history full): {st}")
+        if st[ops.ST_TOTAL] != self.total:
+            raise RuntimeError(f"decode state TOTAL {st[ops.ST_TOTAL]} != {self.total} expected")
