@@ -43,6 +43,29 @@ def _compile(src: str, resource: bool) -> tuple[str, str]:
     return obj, err
 
 
+ROOT = os.path.dirname(HERE)
+BIN = os.path.join(HERE, "bin")
+HOST_PROGRAMS = {"yt_host_parity": os.path.join(ROOT, "tests", "cpp", "host_parity.cpp")}
+
+
+def build_host_programs() -> list[str]:
+    """C++ programs over the host API (include/yt/ytensor.hpp) linked against
+    libythip.so, built with the host compiler into ytensor_amd/bin/."""
+    os.makedirs(BIN, exist_ok=True)
+    out = []
+    for name, src in HOST_PROGRAMS.items():
+        exe = os.path.join(BIN, name)
+        cmd = ["g++", "-std=c++20", "-O2", "-Wall", f"-I{os.path.join(ROOT, 'include')}", "-I/opt/rocm/include",
+               "-D__HIP_PLATFORM_AMD__", src, "-o", exe + ".tmp", f"-L{HERE}", "-lythip", "-L/opt/rocm/lib",
+               "-lamdhip64", "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,/opt/rocm/lib"]
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        if p.returncode != 0:
+            raise RuntimeError(f"g++ failed for {src}:\n{p.stderr}")
+        os.replace(exe + ".tmp", exe)
+        out.append(exe)
+    return out
+
+
 def build(resource: bool = False, verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -56,6 +79,7 @@ def build(resource: bool = False, verbose: bool = False) -> str:
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lz"]
     subprocess.check_call(cmd)
     os.replace(tmp, LIB)
+    build_host_programs()
     return LIB
 
 
