@@ -527,6 +527,23 @@ def main() -> int:
             pre.append({"S": S, "ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
                         "frac_bf16_peak": round(fl / t / 1e9 / PEAK_BF16_TFLOPS, 4)})
         sections["attn_prefill_causal_bf16"] = pre
+        # the reference Qwen3's call form: the causal mask as a bool tensor
+        # (KVCache::get_mask, example/qwen3/src/qwen3.cpp:104-126), staged per
+        # key block; flops count the visible half, as for the causal rows
+        pre_b = []
+        for S in (2048, 8192):
+            q = torch.randn(1, 16, S, 128, device=dev).to(torch.bfloat16)
+            k = torch.randn(1, 8, S, 128, device=dev).to(torch.bfloat16)
+            v = torch.randn(1, 8, S, 128, device=dev).to(torch.bfloat16)
+            o = torch.empty_like(q)
+            mk = torch.ones(S, S, device=dev, dtype=torch.bool).tril()
+            fl = 4.0 * 1 * 16 * 128 * S * (S + 1) / 2
+            t = time_launches(lambda: ops.scaled_dot_product_attention(q, k, v, 1 / math.sqrt(128), mk, out=o),
+                              max(args.steps // 2, 10), args.warmup, torch)
+            pre_b.append({"S": S, "ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                          "frac_bf16_peak": round(fl / t / 1e9 / PEAK_BF16_TFLOPS, 4)})
+            del q, k, v, o, mk
+        sections["attn_prefill_bool_mask_bf16"] = pre_b
 
     if want("decode") and not args.quick:
         dec = []

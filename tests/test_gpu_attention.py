@@ -94,6 +94,63 @@ def test_prefill_cases(orc, yt, case, dtype):
     _check(orc, g, r, dtype, f"{case} {dtype}")
 
 
+def _staged_mask(kind, Sq, Skv, rng):
+    if kind == "random":
+        m = rng.random((Sq, Skv)) > 0.4
+    elif kind == "blocks":
+        # 64-key blocks wholly hidden from some row groups, whole for others, and an empty row
+        m = np.zeros((Sq, Skv), bool)
+        for qb in range(0, Sq, 16):
+            for kb in range(0, Skv, 64):
+                sel = (qb // 16 + kb // 64) % 3
+                if sel == 1:
+                    m[qb:qb + 16, kb:kb + 64] = True
+                elif sel == 2:
+                    m[qb:qb + 16, kb:kb + 64] = rng.random((min(16, Sq - qb), min(64, Skv - kb))) > 0.5
+        m[5] = False
+    elif kind == "ring":
+        # KVCache::get_mask once the ring is full (example/qwen3/src/qwen3.cpp:115-123):
+        # physical key ki has logical position (ki - write_pos) mod max_len
+        wp = 77
+        ki = np.arange(Skv)[None, :]
+        qi = np.arange(Sq)[:, None]
+        m = ((ki - wp + Skv) % Skv) <= (Skv - Sq) + qi
+    else:
+        m = np.tril(np.ones((Sq, Skv), bool), Skv - Sq)
+    return m
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("kind,Sq,Skv,Hq,Hkv", [("random", 200, 336, 2, 1), ("blocks", 300, 512, 4, 2),
+                                                 ("ring", 96, 256, 4, 2), ("causal", 513, 1024, 2, 2),
+                                                 ("blocks", 1100, 1040, 2, 1)])
+def test_prefill_bool_mask_staged(orc, yt, dtype, kind, Sq, Skv, Hq, Hkv):
+    """Bool masks with 16-byte aligned rows take the staged MFMA path (mask tile
+    per key block in LDS, all-false blocks skipped, all-true blocks unmasked; a
+    partial last key block reads its bytes directly): against the oracle's
+    flash_attention with the same mask (src/kernel/avx2/flash_attention.inl:
+    335-379), fully masked rows zero."""
+    D = 128
+    rng = np.random.default_rng(Sq + Skv)
+    Q = rng.standard_normal((1, Hq, Sq, D)).astype(np.float32)
+    K = rng.standard_normal((1, Hkv, Skv, D)).astype(np.float32)
+    V = rng.standard_normal((1, Hkv, Skv, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, dtype)
+    Kd, Kh = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    m = _staged_mask(kind, Sq, Skv, rng)
+    assert Skv % 16 == 0  # 16-byte aligned mask rows
+    scale = 1.0 / math.sqrt(D)
+    r = np.zeros((1, Hq, Sq, D), np.float32)
+    for h in range(Hq):
+        kh = h // (Hq // Hkv)
+        r[0, h] = orc.flash_attention(Qh[0, h], Kh[0, kh], Vh[0, kh], scale, m, None)
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask=torch.from_numpy(m).cuda()))
+    empty = ~m.any(axis=1)
+    assert np.all(g[:, :, empty] == 0.0)
+    check16(orc, g, r, dtype, True, f"staged mask {kind} {Sq}x{Skv} {dtype}")
+
+
 def test_prefill_strided_views(orc, yt):
     """q/k/v as [B,S,H,D] memory viewed as [B,H,S,D] (the qwen3 permute views)."""
     rng = np.random.default_rng(4)

@@ -56,7 +56,14 @@ struct AttnArgs {
     int nqb;
 };
 
-// MODE 0: no mask; 1: causal; 2: byte mask and/or bias read per element.
+// MODE 0: no mask; 1: causal; 2: byte mask and/or bias read per element;
+// 3: byte mask staged per key block: the block's [BQ x BKV] mask tile is DMA'd
+// into LDS with K and V (16-byte aligned rows, full key blocks; the last,
+// partial block reads its bytes directly), each wave skips a block none of
+// whose keys its rows see, drops the per-score masking in a block its rows
+// see whole, and otherwise takes visibility from the LDS tile (the bool-mask
+// call of src/kernel/avx2/flash_attention.inl:335-379 with the tile tests of
+// 14-49).
 // GH query heads of one GQA group share a workgroup (4 waves per head, 32
 // queries per wave), so each K/V tile is staged once for GH*128 queries.
 // K and V tiles reach LDS by DMA (global_load_lds, 16 bytes per lane), both
@@ -90,6 +97,11 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     constexpr int KMASK = KCH - 1 < 15 ? KCH - 1 : 15;
     __shared__ u32x4 sK[2 * STG];
     __shared__ u32x4 sV[2 * STG];
+    constexpr int MCH = BKV / 16;                 // MODE 3: 16-byte mask chunks per row of a block
+    constexpr int MSTG = BQ * MCH;                // mask chunks per stage
+    constexpr int MPT = MSTG / THREADS;
+    static_assert(MODE != 3 || MPT * THREADS == MSTG, "mask tile / thread mismatch");
+    __shared__ u32x4 sM[MODE == 3 ? 2 * MSTG : 1];
 
     // (batch, kv head or head pair, query block) from the XCD-remapped id.
     const int G = a.Hq / a.Hkv;
@@ -179,6 +191,19 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         const int k0 = kb * BKV;
         u32x4* dK = sK + (kb & 1) * STG;
         u32x4* dV = sV + (kb & 1) * STG;
+        if constexpr (MODE == 3) {
+            if (k0 + BKV <= a.Skv) {
+                // mask rows of the query block (clamped to the last query row)
+#pragma unroll
+                for (int i = 0; i < MPT; ++i) {
+                    const int slot = i * THREADS + wave * 64 + lane;
+                    const int r = slot / MCH, c = slot % MCH;
+                    const int row = min(qb * BQ + r, a.Sq - 1);
+                    dma16_async(a.mask + (int64_t)row * a.mask_ld + k0 + c * 16,
+                                &sM[(kb & 1) * MSTG + i * THREADS + wave * 64]);
+                }
+            }
+        }
         const raw* kbase = Kp + (int64_t)k0 * a.ks2;
         const raw* vbase = Vp + (int64_t)k0 * a.vs2;
         if (k0 + BKV <= a.Skv) {
@@ -217,10 +242,42 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
             }
         }
     };
+    // MODE 3: this wave's view of the staged mask tile of block kb -- does any
+    // key of the block reach its rows, do all of them?
+    bool tile_any = true, tile_all = false;
+    auto mask_tile = [&](int kb) {
+        if constexpr (MODE == 3) {
+            if (kb * BKV + BKV > a.Skv) {  // partial last block: not staged
+                tile_any = true;
+                tile_all = false;
+                return;
+            }
+            constexpr int WCH = WQ * MCH;  // 16-byte chunks of this wave's rows
+            const u32x4* t = sM + (kb & 1) * MSTG + ((wave & 3) * WQ) * MCH;
+            bool any = false, all = true;
+#pragma unroll
+            for (int i = 0; i < (WCH + 63) / 64; ++i) {
+                const int c = i * 64 + lane;
+                if (c < WCH) {
+                    const u32x4 v = t[c];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t w = v[e];
+                        any = any || w != 0u;
+                        all = all && ((w - 0x01010101u) & ~w & 0x80808080u) == 0u;  // no zero byte
+                    }
+                }
+            }
+            tile_any = __ballot(any) != 0;
+            tile_all = __ballot(!all) == 0;
+        }
+    };
     // Online softmax of block kb and O += V^T P^T (V stage kb & 1).
     auto softmax_pv = [&](int kb) {
         const int k0 = kb * BKV;
-        const bool need_mask = (MODE == 2) || (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off);
+        const bool staged = MODE == 3 && k0 + BKV <= a.Skv;
+        const bool need_mask = (MODE == 2) || (MODE == 3 && !tile_all) || (k0 + BKV > a.Skv) ||
+                               (MODE == 1 && k0 + BKV - 1 > q0 + off);
         u32x4 pk[QT][NKT / 2];
         bool rescale = false;
         float alpha[QT];
@@ -237,6 +294,15 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
                         const int key = k0 + kt * 16 + g * 4 + r;
                         bool vis = key < a.Skv;
                         if (MODE == 1) vis = vis && (key <= qa + off);
+                        if (MODE == 3) {
+                            if (staged) {
+                                const uint32_t w = reinterpret_cast<const uint32_t*>(sM + (kb & 1) * MSTG)
+                                    [((qa - qb * BQ) * BKV + kt * 16 + g * 4) >> 2];
+                                vis = ((w >> (8 * r)) & 0xffu) != 0u;
+                            } else if (vis && qa < a.Sq) {
+                                vis = a.mask[(int64_t)qa * a.mask_ld + key] != 0;
+                            }
+                        }
                         if (MODE == 2 && vis && qa < a.Sq) {
                             if (a.mask != nullptr) vis = a.mask[(int64_t)qa * a.mask_ld + key] != 0;
                             // bias is added after scaling: log2 units, like the scores
@@ -327,8 +393,11 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     for (int kb = 0; kb < nkb; ++kb) {
         if (kb + 1 < nkb) issue(kb + 1);
         if (active(kb)) {
-            qk(kb);
-            softmax_pv(kb);
+            mask_tile(kb);
+            if (tile_any) {
+                qk(kb);
+                softmax_pv(kb);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -873,7 +942,11 @@ hipError_t launch_prefill_gh(AttnArgs a, int mode, hipStream_t s) {
     dim3 grid(a.nqb * a.B * a.Hq / GH);
     if (mode == 0) attn_fwd_mfma<T, D, 0, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
     else if (mode == 1) attn_fwd_mfma<T, D, 1, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
-    else attn_fwd_mfma<T, D, 2, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
+    else if (mode == 2) attn_fwd_mfma<T, D, 2, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
+    else {
+        if constexpr (GH == 1) attn_fwd_mfma<T, D, 3, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
+        else return hipErrorInvalidValue;  // the staged mask runs one head per workgroup
+    }
     return hipGetLastError();
 }
 
@@ -882,7 +955,7 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     // Two query heads per workgroup (K/V staged once for both) when the GQA
     // group size is even and the paired grid still covers the 256 CUs twice.
     const int64_t paired = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq / 2;
-    if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) return launch_prefill_gh<T, D, 2, 2, 8>(a, mode, s);
+    if (mode != 3 && (a.Hq / a.Hkv) % 2 == 0 && paired >= 512) return launch_prefill_gh<T, D, 2, 2, 8>(a, mode, s);
     // Short sequences: 16 queries per wave doubles the workgroups (two per CU)
     // and halves the per-block work on the longest causal row's serial chain.
     const int64_t wgs = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq;
@@ -901,7 +974,10 @@ template <class T>
 int prefill_typed(AttnArgs a, hipStream_t s) {
     constexpr int es = sizeof(typename T::raw);
     const bool simple_mask = a.mask == nullptr && a.bias == nullptr;
-    const int mode = a.causal ? 1 : (simple_mask ? 0 : 2);
+    // a byte mask whose rows are 16-byte aligned is staged per key block (MODE 3)
+    const bool stage_mask = a.mask != nullptr && a.bias == nullptr && !a.causal && al(a.mask, 16) &&
+                            a.mask_ld % 16 == 0;
+    const int mode = a.causal ? 1 : (simple_mask ? 0 : (stage_mask ? 3 : 2));
     const bool unit_d = a.qs3 == 1 && a.ks3 == 1 && a.vs3 == 1 && a.os3 == 1;
     const bool mfma_ok = es == 2 && unit_d && (a.D == 64 || a.D == 128) && a.Dv == a.D &&
                          !(a.causal && !simple_mask) &&
