@@ -94,8 +94,15 @@ def time_launches(fn, steps: int, warmup: int, torch, graph: bool = True) -> flo
                 for _ in range(steps):
                     fn()
         torch.cuda.current_stream().wait_stream(side)
-        g.replay()  # warm replay
-        torch.cuda.synchronize()
+        # Capturing keeps the GPU idle for tens of milliseconds; the clocks then
+        # boost, overshoot the power limit and settle over ~50 ms of load (a
+        # kernel trace shows the same GEMM at 118 -> 142 -> 105 us per launch in
+        # that window). Replay until 0.2 s of load have passed, as the headline
+        # region's 0.5 s settle does, so every section is timed at steady clocks.
+        t_end = time.perf_counter() + 0.2
+        while time.perf_counter() < t_end:
+            g.replay()
+            torch.cuda.synchronize()
         s.record()
         g.replay()
         e.record()

@@ -56,8 +56,9 @@ def check16(orc, g: np.ndarray, r: np.ndarray, dtype: str, out16: bool, label: s
     den = np.abs(r64).max()
     re = float(np.abs(g64 - r64).max() / (den if den > 0 else 1.0))
     me = float(np.abs(g64 - r64).mean())
-    bar = max(MAE_16, 1.1 * floor16(orc, r, dtype)) if out16 else MAE_16
-    print(f"{label}: rel={re:.3e} mae={me:.3e} bar={bar:.3e}", flush=True)
+    fl = floor16(orc, r, dtype) if out16 else 0.0
+    bar = max(MAE_16, 1.1 * fl) if out16 else MAE_16
+    print(f"{label}: rel={re:.3e} mae={me:.3e} floor={fl:.3e} bar={bar:.3e}", flush=True)
     assert re <= REL_16, f"{label}: rel err {re}"
     assert me <= bar, f"{label}: MAE {me} > {bar}"
     return re, me

@@ -29,6 +29,32 @@ def _small_weights(orc, cfg, seed=5):
     return np.concatenate(parts)
 
 
+def test_qwen3_rejects_bad_requests_before_device_work():
+    """Prompt ids outside [0, vocab), empty or oversize prompts and oversize
+    generate() requests raise ValueError before anything is uploaded or run:
+    the model's buffers live on the CPU here, so any launch would fail
+    differently, and the decode-state record and TOTAL stay untouched."""
+    torch = pytest.importorskip("torch")
+    from ytensor_amd.qwen3 import Qwen3, Qwen3Config, weight_layout
+    cfg = Qwen3Config(hidden=64, layers=1, vocab=100, inter=128, n_heads=2, n_kv=1, head_dim=32, max_pos=64)
+    total = sum(int(np.prod(s)) for _, s in weight_layout(cfg))
+    m = Qwen3(cfg, np.zeros(total, np.float32), device="cpu", max_prompt=16, max_tokens=8)
+    state0 = m.state.clone()
+    for prompt in ([5, 100], [-1, 3], [7, 2**31 - 1]):
+        with pytest.raises(ValueError, match="token ids must lie in"):
+            m.prefill(prompt)
+    with pytest.raises(ValueError, match="prompt of 0 tokens"):
+        m.prefill([])
+    with pytest.raises(ValueError, match="prompt of 17 tokens"):
+        m.prefill(list(range(17)))
+    with pytest.raises(ValueError, match="n_tokens=9"):
+        m.generate([1, 2], 9)
+    with pytest.raises(ValueError, match="token ids must lie in"):
+        m.generate([1, 200], 2)
+    assert m.total == 0 and torch.equal(m.state, state0)
+    assert int(m.ids.abs().sum()) == 0
+
+
 def test_oracle_qwen3_matches_reference(orc, ref):
     """CPU: the restatement equals the compiled reference's Qwen3ForCausalLM
     bit for bit (first-step logits) and in its greedy tokens."""
