@@ -34,9 +34,9 @@
 //
 // This build has no CPU kernels: every MatmulBackend / sdpaBackend value that
 // names a CPU implementation (Naive, Eigen, AVX2, FLASH_AVX2) runs the HIP
-// kernels too -- the reference's Qwen3 example, which asks for FLASH_AVX2
-// (example/qwen3/src/qwen3.cpp:256-264), works unchanged. MATH runs the
-// materialised-score path (ythip_attn_math).
+// kernels too -- a call site such as the Qwen3 example's attention, which asks
+// for FLASH_AVX2 (example/qwen3/src/qwen3.cpp:256-264), needs no edit. MATH
+// runs the materialised-score path (ythip_attn_math).
 //
 // Compile with a C++20 host compiler, -I<repo>/include -I/opt/rocm/include
 // -D__HIP_PLATFORM_AMD__, and link libythip.so and libamdhip64.so.
