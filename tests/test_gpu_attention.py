@@ -108,6 +108,18 @@ def _staged_mask(kind, Sq, Skv, rng):
                 elif sel == 2:
                     m[qb:qb + 16, kb:kb + 64] = rng.random((min(16, Sq - qb), min(64, Skv - kb))) > 0.5
         m[5] = False
+    elif kind == "wgblocks":
+        # whole 128-row x 64-key regions hidden, whole or mixed in turn: a workgroup's
+        # next key block alternates between skipped (no K/V staged) and loaded
+        m = np.zeros((Sq, Skv), bool)
+        for qb in range(0, Sq, 128):
+            for kb in range(0, Skv, 64):
+                sel = (qb // 128 + kb // 64) % 3
+                if sel == 1:
+                    m[qb:qb + 128, kb:kb + 64] = True
+                elif sel == 2:
+                    m[qb:qb + 128, kb:kb + 64] = rng.random((min(128, Sq - qb), min(64, Skv - kb))) > 0.5
+        m[200] = False
     elif kind == "ring":
         # KVCache::get_mask once the ring is full (example/qwen3/src/qwen3.cpp:115-123):
         # physical key ki has logical position (ki - write_pos) mod max_len
@@ -120,11 +132,17 @@ def _staged_mask(kind, Sq, Skv, rng):
     return m
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("kind,Sq,Skv,Hq,Hkv", [("random", 200, 336, 2, 1), ("blocks", 300, 512, 4, 2),
-                                                 ("ring", 96, 256, 4, 2), ("causal", 513, 1024, 2, 2),
-                                                 ("blocks", 1100, 1040, 2, 1)])
-def test_prefill_bool_mask_staged(orc, yt, dtype, kind, Sq, Skv, Hq, Hkv):
+STAGED_CASES = [(d, k, sq, skv, hq, hkv, 1) for d in ("bf16", "f16")
+                for (k, sq, skv, hq, hkv) in [("random", 200, 336, 2, 1), ("blocks", 300, 512, 4, 2),
+                                              ("ring", 96, 256, 4, 2), ("causal", 513, 1024, 2, 2),
+                                              ("blocks", 1100, 1040, 2, 1)]]
+# GQA pairs with >= 512 paired workgroups: two heads per workgroup, the mask staged
+# one key block ahead of K/V, key blocks no row of a workgroup sees skipped whole
+STAGED_CASES += [("bf16", k, 2048, 2048, 16, 8, 4) for k in ("causal", "ring", "wgblocks")]
+
+
+@pytest.mark.parametrize("dtype,kind,Sq,Skv,Hq,Hkv,B", STAGED_CASES)
+def test_prefill_bool_mask_staged(orc, yt, dtype, kind, Sq, Skv, Hq, Hkv, B):
     """Bool masks with 16-byte aligned rows take the staged MFMA path (mask tile
     per key block in LDS, all-false blocks skipped, all-true blocks unmasked; a
     partial last key block reads its bytes directly): against the oracle's
@@ -132,23 +150,24 @@ def test_prefill_bool_mask_staged(orc, yt, dtype, kind, Sq, Skv, Hq, Hkv):
     335-379), fully masked rows zero."""
     D = 128
     rng = np.random.default_rng(Sq + Skv)
-    Q = rng.standard_normal((1, Hq, Sq, D)).astype(np.float32)
-    K = rng.standard_normal((1, Hkv, Skv, D)).astype(np.float32)
-    V = rng.standard_normal((1, Hkv, Skv, D)).astype(np.float32)
+    Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
     Qd, Qh = make_input(orc, Q, dtype)
     Kd, Kh = make_input(orc, K, dtype)
     Vd, Vh = make_input(orc, V, dtype)
     m = _staged_mask(kind, Sq, Skv, rng)
     assert Skv % 16 == 0  # 16-byte aligned mask rows
     scale = 1.0 / math.sqrt(D)
-    r = np.zeros((1, Hq, Sq, D), np.float32)
-    for h in range(Hq):
-        kh = h // (Hq // Hkv)
-        r[0, h] = orc.flash_attention(Qh[0, h], Kh[0, kh], Vh[0, kh], scale, m, None)
+    r = np.zeros((B, Hq, Sq, D), np.float32)
+    for b in range(B):
+        for h in range(Hq):
+            kh = h // (Hq // Hkv)
+            r[b, h] = orc.flash_attention(Qh[b, h], Kh[b, kh], Vh[b, kh], scale, m, None)
     g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask=torch.from_numpy(m).cuda()))
     empty = ~m.any(axis=1)
     assert np.all(g[:, :, empty] == 0.0)
-    check16(orc, g, r, dtype, True, f"staged mask {kind} {Sq}x{Skv} {dtype}")
+    check16(orc, g, r, dtype, True, f"staged mask {kind} B={B} {Hq}/{Hkv} heads {Sq}x{Skv} {dtype}")
 
 
 def test_prefill_strided_views(orc, yt):

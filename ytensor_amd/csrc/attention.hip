@@ -65,7 +65,8 @@ struct AttnArgs {
 // call of src/kernel/avx2/flash_attention.inl:335-379 with the tile tests of
 // 14-49).
 // GH query heads of one GQA group share a workgroup (4 waves per head, 32
-// queries per wave), so each K/V tile is staged once for GH*128 queries.
+// queries per wave), so each K/V tile is staged once for GH*128 queries; the
+// mask (one per query/key pair, the same for every head) then serves both.
 // K and V tiles reach LDS by DMA (global_load_lds, 16 bytes per lane), both
 // kept in their natural [key][d] layout:
 //   K rows: 16-byte chunk c stored at c ^ (key & KMASK) -> the S^T operand is
@@ -940,12 +941,17 @@ hipError_t launch_prefill_gh(AttnArgs a, int mode, hipStream_t s) {
     constexpr int BQ = 64 * QT;
     a.nqb = (a.Sq + BQ - 1) / BQ;
     dim3 grid(a.nqb * a.B * a.Hq / GH);
-    if (mode == 0) attn_fwd_mfma<T, D, 0, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
-    else if (mode == 1) attn_fwd_mfma<T, D, 1, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
-    else if (mode == 2) attn_fwd_mfma<T, D, 2, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
-    else {
-        if constexpr (GH == 1) attn_fwd_mfma<T, D, 3, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
-        else return hipErrorInvalidValue;  // the staged mask runs one head per workgroup
+    // paired heads take 128-key blocks, except the staged mask (64-key blocks)
+    constexpr bool paired_mask = GH == 2 && NKT == 4;
+    if (mode == 3) {
+        if constexpr (GH == 1 || paired_mask) attn_fwd_mfma<T, D, 3, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
+        else return hipErrorInvalidValue;
+    } else if constexpr (paired_mask) {
+        return hipErrorInvalidValue;
+    } else {
+        if (mode == 0) attn_fwd_mfma<T, D, 0, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
+        else if (mode == 1) attn_fwd_mfma<T, D, 1, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
+        else attn_fwd_mfma<T, D, 2, GH, QT, NKT><<<grid, 256 * GH, 0, s>>>(a);
     }
     return hipGetLastError();
 }
@@ -955,7 +961,13 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     // Two query heads per workgroup (K/V staged once for both) when the GQA
     // group size is even and the paired grid still covers the 256 CUs twice.
     const int64_t paired = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq / 2;
-    if (mode != 3 && (a.Hq / a.Hkv) % 2 == 0 && paired >= 512) return launch_prefill_gh<T, D, 2, 2, 8>(a, mode, s);
+    // The staged bool mask pairs heads with 64-key blocks (80 KB of LDS): with
+    // 128-key blocks K, V and the two mask tiles fill all 160 KB and the kernel
+    // spills registers (measured slower).
+    if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) {
+        if (mode == 3) return launch_prefill_gh<T, D, 2, 2, 4>(a, mode, s);
+        return launch_prefill_gh<T, D, 2, 2, 8>(a, mode, s);
+    }
     // Short sequences: 16 queries per wave doubles the workgroups (two per CU)
     // and halves the per-block work on the longest causal row's serial chain.
     const int64_t wgs = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq;
