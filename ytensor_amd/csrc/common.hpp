@@ -132,6 +132,22 @@ __device__ __forceinline__ void dma16_async(const void* gsrc, void* lds_wave_bas
 #endif
 }
 
+// The same DMA from a wave-uniform base (scalar registers) plus this lane's
+// 32-bit byte offset, i.e. global_load_lds's scalar-base form: a caller that
+// keeps the offsets fixed across a loop and moves only the base (and the LDS
+// destination, both scalar) issues its DMA with no per-load VALU address
+// arithmetic. lds_wave_base is the LDS byte address of lane 0's 16 bytes.
+__device__ __forceinline__ void dma16_soff(const void* sbase, uint32_t voff, uint32_t lds_wave_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_wave_base)
+                 : "memory", "m0");
+#else
+    (void)sbase; (void)voff; (void)lds_wave_base;
+#endif
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane j supplies the LDS byte
 // address of 4 consecutive 16-bit values R[j][0..3]; lane i receives
 // { R[4t + i/4][i%4] : t = 0..3 }.

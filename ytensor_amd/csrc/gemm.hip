@@ -303,7 +303,12 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <class T, class TO, int BM, int BN, int WM, int WN, bool NN, int STAGES>
+// SOFF: every operand spans less than 2^31 bytes (checked on the host): the DMA
+// then goes from a wave-uniform base, moved by scalar adds per k step, plus a
+// per-lane 32-bit byte offset fixed for the whole k loop (dma16_soff), and the
+// LDS destination is the wave's base plus constants -- no VALU address work
+// between the MFMAs of consecutive k steps.
+template <class T, class TO, int BM, int BN, int WM, int WN, bool NN, int STAGES, bool SOFF>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a) {
     using raw = typename T::raw;
     constexpr int THREADS = 64 * WM * WN;
@@ -368,9 +373,50 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
             dma16_async(g, &sB[i * THREADS + wave * 64]);
         }
     };
-    auto issue = [&](int kt, u32x4* sA, u32x4* sB) {
-        issue_a(kt, sA);
-        issue_b(kt, sB);
+    // SOFF: per-lane byte offsets of the stage-0 loads (the k loop moves the base)
+    uint32_t offA[SOFF ? A_PT : 1], offB[SOFF ? B_PT : 1];
+    uint32_t ldsA0 = 0, ldsB0 = 0;
+    if constexpr (SOFF) {
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i) {
+            const int slot = i * THREADS + wave * 64 + lane;
+            const int r = slot >> 3;
+            const int c = swz_dma(r, slot & 7);
+            const int row = min(m0 + r, a.m - 1);
+            offA[i] = (uint32_t)(((int64_t)row * a.rsa + c * VEC) * (int64_t)sizeof(raw));
+        }
+#pragma unroll
+        for (int i = 0; i < B_PT; ++i) {
+            const int slot = i * THREADS + wave * 64 + lane;
+            int64_t e;
+            if constexpr (!NN) {
+                const int r = slot >> 3;
+                const int c = swz_dma(r, slot & 7);
+                e = (int64_t)min(n0 + r, a.n - 1) * a.csb + c * VEC;
+            } else {
+                const int r = slot / (2 * NBLK), ps = slot % (2 * NBLK);
+                const int lb = nn_blk(r, ps >> 1, BLK_MASK);
+                e = (int64_t)r * a.rsb + min(n0 + lb * 16, a.n - 16) + (ps & 1) * 8;
+            }
+            offB[i] = (uint32_t)(e * (int64_t)sizeof(raw));
+        }
+        ldsA0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sbuf[wave * 64]);
+        ldsB0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sbuf[STAGES * STA + wave * 64]);
+    }
+    // DMA of k step kt into stage st
+    auto issue_st = [&](int kt, int st) {
+        if constexpr (SOFF) {
+            const char* bA = reinterpret_cast<const char*>(Ap) + (int64_t)kt * BK * (int64_t)sizeof(raw);
+            const char* bB = reinterpret_cast<const char*>(Bp) +
+                             (int64_t)kt * BK * (NN ? a.rsb : (int64_t)1) * (int64_t)sizeof(raw);
+#pragma unroll
+            for (int i = 0; i < A_PT; ++i) dma16_soff(bA, offA[i], ldsA0 + (uint32_t)(st * STA + i * THREADS) * 16u);
+#pragma unroll
+            for (int i = 0; i < B_PT; ++i) dma16_soff(bB, offB[i], ldsB0 + (uint32_t)(st * STB + i * THREADS) * 16u);
+        } else {
+            issue_a(kt, sbuf + st * STA);
+            issue_b(kt, sbuf + STAGES * STA + st * STB);
+        }
     };
 
     f32x4 acc[FM][FN];
@@ -438,12 +484,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
     u32x4* sB = sbuf + STAGES * STA;
     if constexpr (STAGES == 2) {
         // Double buffer: DMA of step kt+1 overlaps the MFMAs of step kt.
-        issue(0, sA, sB);
+        issue_st(0, 0);
         wait_vmcnt<0>();
         __syncthreads();
         for (int kt = 0; kt < KT; ++kt) {
             const int cur = kt & 1;
-            if (kt + 1 < KT) issue(kt + 1, sA + (cur ^ 1) * STA, sB + (cur ^ 1) * STB);
+            if (kt + 1 < KT) issue_st(kt + 1, cur ^ 1);
             compute(sA + cur * STA, sB + cur * STB);
             wait_vmcnt<0>();  // this wave's DMA for the next step has landed
             __syncthreads();
@@ -452,7 +498,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
     // STAGES-deep ring: STAGES-1 k steps are in flight while one is computed.
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
-        if (st < KT) issue(st, sA + st * STA, sB + st * STB);
+        if (st < KT) issue_st(st, st);
     for (int kt = 0; kt < KT; ++kt) {
         // Stage kt has landed for this wave once at most `ahead` later stages are outstanding.
         const int ahead = min(STAGES - 2, KT - 1 - kt);
@@ -461,7 +507,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
         else wait_vmcnt<0>();
         __syncthreads();  // every wave's share of stage kt is in LDS; stage kt-1 is consumed
         const int nxt = kt + STAGES - 1;
-        if (nxt < KT) issue(nxt, sA + (nxt % STAGES) * STA, sB + (nxt % STAGES) * STB);
+        if (nxt < KT) issue_st(nxt, nxt % STAGES);
         compute(sA + (kt % STAGES) * STA, sB + (kt % STAGES) * STB);
     }
     }
@@ -700,13 +746,20 @@ hipError_t launch_dma_tile(const GemmArgs& a0, bool nn, int batch, hipStream_t s
     a.tiles_n = (a.n + BN - 1) / BN;
     dim3 grid(a.tiles_m * a.tiles_n, batch);
     dim3 block(64 * WM * WN);
+    // bytes spanned by one batch entry's A and B (the DMA addresses stay inside)
+    constexpr int64_t es = sizeof(typename T::raw);
+    const int64_t span_a = ((int64_t)(a.m - 1) * a.rsa + a.k) * es;
+    const int64_t span_b = (nn ? (int64_t)(a.k - 1) * a.rsb + a.n : (int64_t)(a.n - 1) * a.csb + a.k) * es;
+    const bool soff = span_a < (int64_t(1) << 31) && span_b < (int64_t(1) << 31);
     if constexpr (sizeof(typename T::raw) == 2) {
         if (nn) {
-            gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, true, STAGES><<<grid, block, 0, s>>>(a);
+            if (soff) gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, true, STAGES, true><<<grid, block, 0, s>>>(a);
+            else gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, true, STAGES, false><<<grid, block, 0, s>>>(a);
             return hipGetLastError();
         }
     }
-    gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, false, STAGES><<<grid, block, 0, s>>>(a);
+    if (soff) gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, false, STAGES, true><<<grid, block, 0, s>>>(a);
+    else gemm_mfma_dma_kernel<T, TO, BM, BN, WM, WN, false, STAGES, false><<<grid, block, 0, s>>>(a);
     return hipGetLastError();
 }
 
