@@ -170,6 +170,32 @@ def test_prefill_bool_mask_staged(orc, yt, dtype, kind, Sq, Skv, Hq, Hkv, B):
     check16(orc, g, r, dtype, True, f"staged mask {kind} B={B} {Hq}/{Hkv} heads {Sq}x{Skv} {dtype}")
 
 
+# Two query heads per workgroup without a byte mask (>= 512 paired workgroups):
+# the ping-pong kernel, on ragged lengths, a causal offset, d = 64 and fp16.
+PINGPONG_CASES = [
+    ("bf16", 4, 16, 8, 2048, 2048, 128, "causal"),
+    ("bf16", 4, 16, 8, 2000, 2100, 128, "causal"),   # kv longer than q, partial last blocks
+    ("bf16", 4, 16, 8, 2048, 1500, 128, "none"),
+    ("f16", 4, 16, 8, 2047, 2047, 128, "causal"),
+    ("bf16", 4, 16, 4, 2048, 2048, 64, "causal"),    # d = 64, GQA 4:1 (two head pairs per kv head)
+]
+
+
+@pytest.mark.parametrize("dtype,B,Hq,Hkv,Sq,Skv,D,mk", PINGPONG_CASES)
+def test_prefill_paired_heads(orc, yt, dtype, B, Hq, Hkv, Sq, Skv, D, mk):
+    rng = np.random.default_rng(Sq * 3 + Skv + D)
+    Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, dtype)
+    Kd, Kh = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    scale = 1.0 / math.sqrt(D)
+    r = orc.sdpa_gqa(Qh, Kh, Vh, scale, mk == "causal")
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask="causal" if mk == "causal" else None))
+    check16(orc, g, r, dtype, True, f"paired heads B={B} {Hq}/{Hkv} {Sq}x{Skv} d={D} {mk} {dtype}")
+
+
 def test_prefill_strided_views(orc, yt):
     """q/k/v as [B,S,H,D] memory viewed as [B,H,S,D] (the qwen3 permute views)."""
     rng = np.random.default_rng(4)

@@ -422,6 +422,318 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     }
 }
 
+// Paired-head ping-pong prefill (no mask or causal, 16-bit, d in {64, 128}).
+// A workgroup of 8 waves serves two query heads of one GQA group over the same
+// 128 queries: waves 0-3 (group A) head h0, waves 4-7 (group B) head h1, each
+// wave 32 queries, the 64-key K/V tiles staged once for both. The hardware
+// places waves w and w+4 on the same SIMD. Each wave alternates
+//   M(j): PV(j-1) and QK(j) on the matrix cores (operand fragments read three
+//         fragments ahead of their MFMAs, raised issue priority), and
+//   S(j): mask, row max, reference-point update, exp2 and packing of block j,
+// with group B one phase behind group A and a workgroup barrier per phase, so
+// on every SIMD one wave's MFMA phase runs beside the other wave's softmax.
+// Group B stages K(j+1) and V(j) during its S(j-1) and waits for them at the
+// end of its M(j); A reads them from phase 2j+2 on. The arithmetic per score
+// and its order (accumulator started at -m, lazy reference point, packed p,
+// ones-MFMA row sums, O accumulated block by block) are those of
+// attn_fwd_mfma with 64-key blocks.
+template <class T, int D, int MODE>
+__global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
+    using raw = typename T::raw;
+    constexpr int QT = 2, NKT = 4;
+    constexpr int WQ = 16 * QT, BQ = 4 * WQ, BKV = 16 * NKT;
+    constexpr int KCH = D / 8;
+    constexpr int DT = D / 16;
+    constexpr int KS = D / 32;
+    constexpr int GT = 256;  // threads of one wave group (the issuers of a tile's DMA)
+    constexpr int PT = BKV * KCH / GT;
+    static_assert(PT * GT == BKV * KCH, "tile / thread mismatch");
+    constexpr int NB = D / 16;
+    constexpr int BMASK = (NB < 8 ? NB : 8) - 1;
+    constexpr int STG = BKV * KCH;
+    constexpr int KMASK = KCH - 1 < 15 ? KCH - 1 : 15;
+    __shared__ u32x4 sK[2 * STG];
+    __shared__ u32x4 sV[2 * STG];
+
+    const int G = a.Hq / a.Hkv;
+    const int hgroups = G / 2;
+    const int units = a.B * a.Hkv * hgroups;
+    const int total = units * a.nqb;
+    int w = blockIdx.x;
+    if ((total & 7) == 0) w = (w & 7) * (total >> 3) + (w >> 3);
+    const int unit = w / a.nqb;
+    const int qi = w % a.nqb;
+    const int qb = (MODE == 1) ? (a.nqb - 1 - qi) : qi;
+    const int b = unit / (a.Hkv * hgroups);
+    const int rem = unit % (a.Hkv * hgroups);
+    const int kvh = rem / hgroups;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool grpB = wave >= 4;
+    const int h = kvh * G + (rem % hgroups) * 2 + (wave >> 2);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int q0 = qb * BQ + (wave & 3) * WQ;
+
+    const raw* Qp = static_cast<const raw*>(a.Q) + b * a.qs0 + h * a.qs1;
+    const raw* Kp = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1;
+    const raw* Vp = static_cast<const raw*>(a.V) + b * a.vs0 + kvh * a.vs1;
+
+    // Q pre-scaled by scale*log2(e) and rounded back to T, as in attn_fwd_mfma
+    const float c = a.scale_log2;
+    u32x4 qf[QT][KS];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int q = q0 + qt * 16 + l16;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (q < a.Sq) v = *reinterpret_cast<const u32x4*>(Qp + (int64_t)q * a.qs2 + ks * 32 + g * 8);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t w2 = v[e];
+                v[e] = pack2<T>(lo_as_f32(T{}, w2) * c, hi_as_f32(T{}, w2) * c);
+            }
+            qf[qt][ks] = v;
+        }
+    }
+
+    const int off = a.diag_off;  // causal: key j visible to query i iff j <= i + off
+    int kv_end = a.Skv;
+    if (MODE == 1) kv_end = min(a.Skv, qb * BQ + BQ + off);
+    const int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;  // blocks the workgroup stages
+    int kv_end_w = a.Skv;
+    if (MODE == 1) kv_end_w = min(a.Skv, q0 + WQ + off);
+    const int nkw = kv_end_w > 0 ? (kv_end_w + BKV - 1) / BKV : 0;  // blocks this wave's rows see
+
+    constexpr float LAZY = 8.0f;
+    constexpr uint32_t ONE2 = std::is_same_v<T, BF16> ? 0x3F803F80u : 0x3C003C00u;
+    const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
+    float m[QT];
+    bool mset[QT];
+    f32x4 lsum[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        m[qt] = 0.f;
+        mset[qt] = false;
+        lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    f32x4 o[QT][DT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // DMA slots of this thread within its wave group
+    const int gw = (tid & (GT - 1)) >> 6;
+    int koff[PT], voff[PT], krow[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        const int slot = i * GT + gw * 64 + lane;
+        const int row = slot / KCH, ps = slot % KCH;
+        krow[i] = row;
+        koff[i] = row * (int)a.ks2 + (ps ^ (row & KMASK)) * 8;
+        voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
+    }
+    // rows past the end re-read the last key (their scores are masked)
+    auto issue_k = [&](int kb) {
+        const int k0 = kb * BKV;
+        u32x4* dK = sK + (kb & 1) * STG;
+        const raw* kbase = Kp + (int64_t)k0 * a.ks2;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int sh = (k0 + BKV <= a.Skv) ? 0 : min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
+            dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * GT + gw * 64]);
+        }
+    };
+    auto issue_v = [&](int kb) {
+        const int k0 = kb * BKV;
+        u32x4* dV = sV + (kb & 1) * STG;
+        const raw* vbase = Vp + (int64_t)k0 * a.vs2;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int sh = (k0 + BKV <= a.Skv) ? 0 : min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
+            dma16_async(vbase + voff[i] + sh * (int)a.vs2, &dV[i * GT + gw * 64]);
+        }
+    };
+
+    f32x4 s[QT][NKT];
+    u32x4 pk[QT][NKT / 2];
+
+    // M phase: O += V^T P^T for block jp (and the row sums), then S^T - m = K Q^T
+    // for block jq. A unit is one K or V fragment feeding QT MFMAs; fragments are
+    // read PF units ahead, the scheduling barriers keep that order.
+    constexpr int PF = 3;
+    auto mphase = [&](int jp, bool do_pv, int jq, bool do_qk) {
+        __builtin_amdgcn_s_setprio(1);
+        const u32x4* cV = sV + (jp & 1) * STG;
+        const u32x4* cK = sK + (jq & 1) * STG;
+        auto ldv = [&](int kk, int dt) -> u32x4 {
+            u32x4 vf;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int key = (2 * kk + hh) * 16 + g * 4 + (l16 >> 2);
+                const int byte = key * (D * 2) + ((dt ^ (key & BMASK)) << 5) + 8 * (l16 & 3);
+                const u32x2 w2 = lds_read_tr16(cV, byte);
+                vf[2 * hh] = w2[0];
+                vf[2 * hh + 1] = w2[1];
+            }
+            return vf;
+        };
+        auto ldk = [&](int ks, int kt) -> u32x4 {
+            const int key = kt * 16 + l16;
+            return cK[key * KCH + ((ks * 4 + g) ^ (key & KMASK))];
+        };
+        if (do_pv) {
+            constexpr int NU = (NKT / 2) * DT;
+            u32x4 fr[PF + 1];
+            static_for<0, PF>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                fr[u] = ldv(u / DT, u % DT);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<0, NU>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                constexpr int kk = u / DT, dt = u % DT;
+                if constexpr (u + PF < NU) fr[(u + PF) % (PF + 1)] = ldv((u + PF) / DT, (u + PF) % DT);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_chunk(T{}, fr[u % (PF + 1)], pk[qt][kk], o[qt][dt]);
+                if constexpr (dt == DT - 1) {
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) lsum[qt] = mfma_chunk(T{}, ones, pk[qt][kk], lsum[qt]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+        if (do_qk) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) s[qt][kt] = f32x4{-m[qt], -m[qt], -m[qt], -m[qt]};
+            constexpr int NU = KS * NKT;
+            u32x4 fr[PF + 1];
+            static_for<0, PF>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                fr[u] = ldk(u / NKT, u % NKT);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<0, NU>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                constexpr int ks = u / NKT, kt = u % NKT;
+                if constexpr (u + PF < NU) fr[(u + PF) % (PF + 1)] = ldk((u + PF) / NKT, (u + PF) % NKT);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma_chunk(T{}, fr[u % (PF + 1)], qf[qt][ks], s[qt][kt]);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+        __builtin_amdgcn_s_setprio(0);
+    };
+    // S phase of block kb: masked scores -> -inf, row max (relative to m), the
+    // lazy reference point (set by the first visible block, moved only when a
+    // block max exceeds it by more than LAZY in log2 units, O and l rescaled
+    // then), p = exp2(s - m) packed to T.
+    auto sphase = [&](int kb) {
+        const int k0 = kb * BKV;
+        const bool msk = (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off);
+        float alpha[QT];
+        bool rescale = false;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const int qa = q0 + qt * 16 + l16;
+            if (msk) {
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int key = k0 + kt * 16 + g * 4 + r;
+                        bool vis = key < a.Skv;
+                        if (MODE == 1) vis = vis && (key <= qa + off);
+                        s[qt][kt][r] = vis ? s[qt][kt][r] : -INFINITY;
+                    }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, s[qt][kt][r]);
+            mx = max_across_rows(mx);
+            const bool move = mset[qt] ? (mx > LAZY) : (mx != -INFINITY);
+            const float delta = move ? mx : 0.f;
+            const bool moved = move && mset[qt];
+            alpha[qt] = moved ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
+            rescale |= moved;
+            m[qt] += delta;
+            mset[qt] = mset[qt] || move;
+            if (__ballot(move) != 0) {
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[qt][kt][r] -= delta;
+            }
+#pragma unroll
+            for (int kk = 0; kk < NKT / 2; ++kk) {
+                float e[8];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    e[r] = __builtin_amdgcn_exp2f(s[qt][2 * kk][r]);
+                    e[4 + r] = __builtin_amdgcn_exp2f(s[qt][2 * kk + 1][r]);
+                }
+                pk[qt][kk] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
+                                   pack2<T>(e[6], e[7])};
+            }
+        }
+        if (__ballot(rescale) != 0) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha[qt];
+                lsum[qt] *= alpha[qt];
+            }
+        }
+    };
+
+    // Phase 2j: A runs M(j), B runs S(j-1) and stages K(j+1), V(j).
+    // Phase 2j+1: A runs S(j), B runs M(j). Every wave passes 2 (nkb + 1) + 1
+    // barriers; K(0) is staged by group A before the first one.
+    if (nkb > 0 && !grpB) issue_k(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    if (!grpB) {
+        for (int j = 0; j <= nkb; ++j) {
+            mphase(j - 1, j >= 1 && j - 1 < nkw, j, j < nkw);
+            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_s_barrier();
+            if (j < nkw) sphase(j);
+            __builtin_amdgcn_s_barrier();
+        }
+    } else {
+        for (int j = 0; j <= nkb; ++j) {
+            if (j + 1 < nkb) issue_k(j + 1);
+            if (j < nkb) issue_v(j);
+            if (j >= 1 && j - 1 < nkw) sphase(j - 1);
+            __builtin_amdgcn_s_barrier();
+            mphase(j - 1, j >= 1 && j - 1 < nkw, j, j < nkw);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's K(j+1) / V(j) DMA has landed
+            __builtin_amdgcn_s_barrier();
+        }
+    }
+
+    raw* Op = static_cast<raw*>(a.O) + b * a.os0 + h * a.os1;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const float L = lsum[qt][0];
+        const float inv = L > 0.f ? 1.0f / L : 0.f;
+        const int q = q0 + qt * 16 + l16;
+        if (q >= a.Sq) continue;
+        raw* orow = Op + (int64_t)q * a.os2;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int d = dt * 16 + g * 4;
+            const f32x4 v = o[qt][dt] * inv;
+            u32x2 p = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+            *reinterpret_cast<u32x2*>(orow + d) = p;
+        }
+    }
+}
+
 // Any layout / any dtype / d, dv <= 256: one wave per (batch, head, query row).
 // Scores for the whole row are kept in LDS (kv_len <= ROW_MAX), then max,
 // exp, sum and P.V in key order (the decode formulation of the reference).
@@ -959,13 +1271,22 @@ hipError_t launch_prefill_gh(AttnArgs a, int mode, hipStream_t s) {
 template <class T, int D>
 hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     // Two query heads per workgroup (K/V staged once for both) when the GQA
-    // group size is even and the paired grid still covers the 256 CUs twice.
+    // group size is even and the paired grid still covers the 256 CUs twice;
+    // without a byte mask those run the ping-pong kernel (S=8192 causal:
+    // 248 us against 265 us for attn_fwd_mfma with 128-key blocks).
     const int64_t paired = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq / 2;
     // The staged bool mask pairs heads with 64-key blocks (80 KB of LDS): with
     // 128-key blocks K, V and the two mask tiles fill all 160 KB and the kernel
     // spills registers (measured slower).
     if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) {
         if (mode == 3) return launch_prefill_gh<T, D, 2, 2, 4>(a, mode, s);
+        if (mode == 0 || mode == 1) {
+            a.nqb = (a.Sq + 127) / 128;
+            dim3 grid(a.nqb * a.B * a.Hq / 2);
+            if (mode == 1) attn_fwd_pingpong<T, D, 1><<<grid, 512, 0, s>>>(a);
+            else attn_fwd_pingpong<T, D, 0><<<grid, 512, 0, s>>>(a);
+            return hipGetLastError();
+        }
         return launch_prefill_gh<T, D, 2, 2, 8>(a, mode, s);
     }
     // Short sequences: 16 queries per wave doubles the workgroups (two per CU)

@@ -199,6 +199,19 @@ __device__ __forceinline__ float dpp_max_to_lane63(float v) {
     v = dpp_max<0x143, 0xc>(v);
     return v;
 }
+// Maximum over lanes l, l^16, l^32, l^48 (the four 16-lane rows of a wave),
+// every lane getting the result: gfx950's v_permlane16_swap / v_permlane32_swap
+// exchange rows inside the VALU (no LDS round trip). IEEE maximum: a NaN
+// propagates, -inf is the identity.
+__device__ __forceinline__ float max_across_rows(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = __builtin_elementwise_maximum(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return __builtin_elementwise_maximum(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+}
+
 // Sum over aligned groups of N = 8 or 16 lanes, every lane of a group getting
 // its group's total (DPP: quad swaps, half-row mirror, then a rotate by 8 within
 // the 16-lane row).
