@@ -54,6 +54,7 @@ struct AttnArgs {
     const float* bias;
     int64_t brs, bcs;
     int nqb;
+    int balance;  // causal: the grid is resident at once, two workgroups per CU (see attn_fwd_mfma)
 };
 
 // MODE 0: no mask; 1: causal; 2: byte mask and/or bias read per element;
@@ -113,7 +114,15 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     if ((total & 7) == 0) w = (w & 7) * (total >> 3) + (w >> 3);
     const int unit = w / a.nqb;
     const int qi = w % a.nqb;
-    const int qb = (MODE == 1) ? (a.nqb - 1 - qi) : qi;
+    // Causal work grows with the query block; heaviest blocks launch first. When
+    // the whole grid is resident at once with two workgroups per CU (balance),
+    // CU k holds workgroups k and k + total/2, which the remap above gives the
+    // same query block of units u and u + 1 (u even) whenever total / 8 is a
+    // multiple of nqb: odd units then take their blocks lightest first, so such
+    // a CU pairs a heavy block with a light one. Per unit the order stays a
+    // permutation of its query blocks.
+    const bool light_first = a.balance && (unit & 1);
+    const int qb = (MODE == 1 && !light_first) ? (a.nqb - 1 - qi) : qi;
     const int b = unit / (a.Hkv * hgroups);
     const int rem = unit % (a.Hkv * hgroups);
     const int kvh = rem / hgroups;
@@ -1248,11 +1257,26 @@ namespace {
 
 bool al(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
+// Compute units of the current device (queried once per device).
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 template <class T, int D, int GH, int QT, int NKT = 4>
 hipError_t launch_prefill_gh(AttnArgs a, int mode, hipStream_t s) {
     constexpr int BQ = 64 * QT;
     a.nqb = (a.Sq + BQ - 1) / BQ;
     dim3 grid(a.nqb * a.B * a.Hq / GH);
+    // 4-wave workgroups run two per CU: a grid of at most two per CU is resident at once
+    a.balance = (GH == 1 && (int64_t)grid.x <= 2 * (int64_t)device_cus()) ? 1 : 0;
     // paired heads take 128-key blocks, except the staged mask (64-key blocks)
     constexpr bool paired_mask = GH == 2 && NKT == 4;
     if (mode == 3) {
