@@ -642,8 +642,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     auto sphase = [&](int kb) {
         const int k0 = kb * BKV;
         const bool msk = (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off);
-        float alpha[QT];
-        bool rescale = false;
+        float delta[QT];
+        bool moved[QT];
+        bool any = false;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             const int qa = q0 + qt * 16 + l16;
@@ -665,18 +666,28 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                 for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, s[qt][kt][r]);
             mx = max_across_rows(mx);
             const bool move = mset[qt] ? (mx > LAZY) : (mx != -INFINITY);
-            const float delta = move ? mx : 0.f;
-            const bool moved = move && mset[qt];
-            alpha[qt] = moved ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
-            rescale |= moved;
-            m[qt] += delta;
+            delta[qt] = move ? mx : 0.f;
+            moved[qt] = move && mset[qt];
+            m[qt] += delta[qt];
             mset[qt] = mset[qt] || move;
-            if (__ballot(move) != 0) {
+            any = any || delta[qt] != 0.f;
+        }
+        // one wave-uniform branch for both query tiles: rare after the first block
+        if (__ballot(any) != 0) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) s[qt][kt][r] -= delta;
+                    for (int r = 0; r < 4; ++r) s[qt][kt][r] -= delta[qt];
+                const float alpha = moved[qt] ? __builtin_amdgcn_exp2f(-delta[qt]) : 1.0f;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha;
+                lsum[qt] *= alpha;
             }
+        }
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
             for (int kk = 0; kk < NKT / 2; ++kk) {
                 float e[8];
@@ -688,15 +699,6 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                 pk[qt][kk] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
                                    pack2<T>(e[6], e[7])};
             }
-        }
-        if (__ballot(rescale) != 0) {
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha[qt];
-                lsum[qt] *= alpha[qt];
-            }
-        }
     };
 
     // Phase 2j: A runs M(j), B runs S(j-1) and stages K(j+1), V(j).
