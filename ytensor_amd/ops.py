@@ -183,7 +183,10 @@ def _mask_args(mask, m: int, n: int, device):
         mask = _predicate_mask(mask, m, n, device)
     if tuple(mask.shape) != (m, n):
         raise ValueError(f"mask shape {tuple(mask.shape)} != {(m, n)}")  # ops.inl:390-393
-    keep = mask.to(device=device, dtype=torch.uint8)
+    if mask.dtype == torch.bool and mask.device == torch.device(device):
+        keep = mask.view(torch.uint8)  # one 0/1 byte per element already: read in place, no copy
+    else:
+        keep = mask.to(device=device, dtype=torch.uint8)
     if keep.stride(1) != 1:
         keep = keep.contiguous()
     return _lib.MASK_BOOL, keep.data_ptr(), keep.stride(0), keep
