@@ -47,6 +47,29 @@ def test_norm_rope(orc, yt, dtype, B, S, pos0):
             check16(orc, g, r, dtype, True, f"{name} B={B} S={S}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_norm_rope_long_prompt(orc, yt, dtype, d):
+    """65568 (token, head) rows at d = 64 and 128; 2049 tokens leave a partly
+    filled last workgroup."""
+    B, S, pos0, Hq, Hkv = 1, 2049, 3, 16, 8
+    rng = np.random.default_rng(d + 7)
+    qkv = rng.standard_normal((B, S, (Hq + 2 * Hkv) * d)).astype(np.float32)
+    wq = (rng.standard_normal(d) * 0.02 + 1.0).astype(np.float32)
+    wk = (rng.standard_normal(d) * 0.02 + 1.0).astype(np.float32)
+    cos, sin = orc.rope_tables(d, 4096, 1e6)
+    qd, qh = make_input(orc, qkv, dtype)
+    rq, rk, rv = _oracle_norm_rope(orc, qh, B, S, Hq, Hkv, d, wq, wk, 1e-6, cos, sin, pos0)
+    gq, gk, gv = yt.rms_norm_rope(qd, Hq, Hkv, d, dev_f32(wq), dev_f32(wk), 1e-6, dev_f32(cos), dev_f32(sin),
+                                  pos0=pos0)
+    for name, g, r in (("q", gq, rq), ("k", gk, rk), ("v", gv, rv)):
+        g = host_f32(g)
+        if dtype == "f32":
+            assert rel_err(g, r) <= 1e-4, name
+        else:
+            check16(orc, g, r, dtype, True, f"{name} d={d} S={S}")
+
+
 def test_norm_rope_into_cache(orc, yt):
     """K/V land in cache rows cache_pos.. of a [B,Hkv,max,d] buffer; other rows untouched."""
     B, S, Hq, Hkv, d, cache_pos, maxlen = 2, 9, 4, 2, 128, 17, 64
