@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from conftest import rel_err
-from helpers import check16, host_f32, make_input
+from helpers import TORCH_DT, check16, host_f32, make_input
 
 pytestmark = pytest.mark.gpu
 
@@ -274,3 +274,25 @@ def test_linear_bias_rounds_product_first(orc, yt, dtype):
     assert np.array_equal(host_f32(biased).view(np.uint32), expect.view(np.uint32))
     with pytest.raises(ValueError):
         yt.linear(xd, Wd, bd[:-1])
+
+
+@pytest.mark.parametrize("dtype,out_dtype,beta,batch", [("bf16", torch.bfloat16, 0.0, 1), ("f16", torch.float16, 0.0, 1),
+                                                        ("bf16", torch.float32, 1.0, 1), ("bf16", torch.bfloat16, 0.0, 2)])
+def test_whole_tile_nn_schedule_bit_identical(yt, dtype, out_dtype, beta, batch):
+    """Whole 256x256 tiles of a row-major B run the ping-pong schedule; the same
+    product with N padded by 16 columns runs the one-phase DMA kernel. Both read
+    the same fragments and issue the same MFMAs in the same order, so the shared
+    columns must agree bit for bit (alpha, beta, fp32 output and a batch too)."""
+    m, n, k = 1024, 12288, 512          # 4 x 48 = 192 tiles of 256 x 256
+    dt = TORCH_DT[dtype]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    a = torch.randn(batch, m, k, device="cuda", generator=g).to(dt)
+    bp = (torch.randn(batch, k, n + 16, device="cuda", generator=g) * 0.05).to(dt)
+    c0 = torch.randn(batch, m, n + 16, device="cuda", generator=g).to(out_dtype)
+    ref = c0.clone()
+    yt.gemm(a, bp, ref, alpha=0.75, beta=beta)                       # N = 12304: not whole tiles
+    out = c0[:, :, :n].contiguous()
+    yt.gemm(a, bp[:, :, :n].contiguous(), out, alpha=0.75, beta=beta)  # N = 12288: whole tiles
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16 if out.element_size() == 2 else torch.int32),
+                       ref[:, :, :n].contiguous().view(torch.int16 if out.element_size() == 2 else torch.int32))

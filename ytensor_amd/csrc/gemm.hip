@@ -547,6 +547,176 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Ping-pong variant of the 256 x 256 DMA kernel for whole tiles with a
+// row-major B (NN, 16-bit). Waves 0-3 (group A) own tile rows 0-127, waves 4-7
+// (group B) rows 128-255; the hardware places waves w and w+4 on one SIMD.
+// Each wave alternates a memory phase X(kt) -- every A and B fragment of k step
+// kt read from LDS into registers (group A also issues the DMA of step kt+1) --
+// and a matrix phase Y(kt) -- the step's 64 MFMAs from registers at raised
+// issue priority -- with group B one phase behind group A and a workgroup
+// barrier per phase, so every SIMD runs one wave's MFMA cluster while the other
+// wave loads. Same LDS layouts, swizzles, fragments and MFMA order as
+// gemm_mfma_dma_kernel (bit-identical C). Group A's DMA of a stage lands
+// before the barrier that ends its Y phase, two phases before it is read.
+// Requirements (host): m % 256 == 0, n % 256 == 0, k % 64 == 0, and every
+// operand spans < 2^31 bytes; each DMA is a scalar base plus a 32-bit lane
+// offset fixed for the kernel (A and the k-rows of B repeat their swizzle
+// every 32 rows / every 16 k-rows of a stage).
+template <class T, class TO>
+__global__ __launch_bounds__(512, 1) void gemm_pingpong_nn_kernel(GemmArgs a) {
+    using raw = typename T::raw;
+    static_assert(sizeof(raw) == 2, "the transposing LDS read is 16-bit");
+    constexpr int BM = 256, BN = 256, BK = 64, GT = 256;
+    constexpr int WTM = 128, WTN = 64, FM = 8, FN = 4;
+    constexpr int STA = BM * 8, STB = BN * 8;        // 16-byte slots per stage
+    constexpr int A_PT = STA / GT, B_PT = STB / GT;  // DMA per group-A thread per step
+    constexpr int NBLK = BN / 16, BLK_MASK = 7;
+    __shared__ u32x4 sbuf[2 * (STA + STB)];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool grpB = wave >= 4;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    int tm, tn;
+    tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int bz = blockIdx.y;
+    const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
+    const raw* __restrict__ Bp = static_cast<const raw*>(a.B) + bz * a.sb_b;
+    const int KT = a.k / BK;
+    u32x4* sA = sbuf;
+    u32x4* sB = sbuf + 2 * STA;
+
+    // DMA slot i*256 + t of a stage (t < 256: group A): A row i*32 + t/8 with a
+    // chunk swizzle that does not depend on i; B k-row i*8 + t/32, whose block
+    // swizzle depends on i only through i & 1.
+    const int t = tid & (GT - 1);
+    uint32_t offA, offB0, offB1;
+    {
+        const int r0 = t >> 3;
+        const int c = swz_dma(r0, t & 7);
+        offA = (uint32_t)(((int64_t)(m0 + r0) * a.rsa + c * 8) * 2);
+        const int kr = t / (2 * NBLK), ps = t % (2 * NBLK);
+        const int lb0 = nn_blk(kr, ps >> 1, BLK_MASK), lb1 = nn_blk(kr + 8, ps >> 1, BLK_MASK);
+        offB0 = (uint32_t)(((int64_t)kr * a.rsb + n0 + lb0 * 16 + (ps & 1) * 8) * 2);
+        offB1 = (uint32_t)(((int64_t)kr * a.rsb + n0 + lb1 * 16 + (ps & 1) * 8) * 2);
+    }
+    const uint32_t ldsA = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sA[(wave & 3) * 64]);
+    const uint32_t ldsB = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sB[(wave & 3) * 64]);
+    auto issue = [&](int kt) {
+        const int st = kt & 1;
+        const char* bA = reinterpret_cast<const char*>(Ap) + (int64_t)kt * BK * 2;
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i)
+            dma16_soff(bA + (int64_t)i * 32 * a.rsa * 2, offA, ldsA + (uint32_t)(st * STA + i * GT) * 16u);
+        const char* bB = reinterpret_cast<const char*>(Bp) + (int64_t)kt * BK * a.rsb * 2;
+#pragma unroll
+        for (int i = 0; i < B_PT; ++i)
+            dma16_soff(bB + (int64_t)i * 8 * a.rsb * 2, (i & 1) ? offB1 : offB0,
+                       ldsB + (uint32_t)(st * STB + i * GT) * 16u);
+    };
+    auto ldA = [&](const u32x4* s, int ks, int i) -> u32x4 {
+        const int r = wm * WTM + i * 16 + lrow;
+        return s[r * 8 + swz_dma(r, ks * 4 + lgrp)];
+    };
+    auto ldB = [&](const u32x4* s, int ks, int j) -> u32x4 {
+        const int nb = (wn * WTN + j * 16) >> 4;
+        u32x4 v;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = ks * 32 + 8 * lgrp + 4 * h + (lrow >> 2);
+            const int byte = r * (BN * 2) + (nn_blk(r, nb, BLK_MASK) << 5) + 8 * (lrow & 3);
+            const u32x2 w = lds_read_tr16(s, byte);
+            v[2 * h] = w[0];
+            v[2 * h + 1] = w[1];
+        }
+        return v;
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 fa[2][FM], fb[2][FN];
+    auto X = [&](int kt) {
+        const u32x4* cA = sA + (kt & 1) * STA;
+        const u32x4* cB = sB + (kt & 1) * STB;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) fb[ks][j] = ldB(cB, ks, j);
+#pragma unroll
+            for (int i = 0; i < FM; ++i) fa[ks][i] = ldA(cA, ks, i);
+        }
+    };
+    // the MFMA order of gemm_mfma_dma_kernel: per output fragment, k chunk 0 then 1
+    auto Y = [&]() {
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma_chunk(T{}, fb[ks][j], fa[ks][i], acc[i][j]);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    constexpr int LGKM0 = 0xc07f;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt not waited
+    if (!grpB) issue(0);
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (!grpB) {
+        for (int kt = 0; kt < KT; ++kt) {
+            if (kt + 1 < KT) issue(kt + 1);  // stage (kt+1)&1: step kt-1, read by B in phase 2kt-1
+            X(kt);
+            __builtin_amdgcn_s_waitcnt(LGKM0);
+            __builtin_amdgcn_s_barrier();
+            Y();
+            wait_vmcnt<0>();  // step kt+1 is in LDS before the next barrier
+            __builtin_amdgcn_s_barrier();
+        }
+        __builtin_amdgcn_s_barrier();  // group B's last matrix phase
+    } else {
+        __builtin_amdgcn_s_barrier();  // group A's first memory phase
+        for (int kt = 0; kt < KT; ++kt) {
+            X(kt);
+            __builtin_amdgcn_s_waitcnt(LGKM0);
+            __builtin_amdgcn_s_barrier();
+            Y();
+            __builtin_amdgcn_s_barrier();
+        }
+    }
+
+    using oraw = typename TO::raw;
+    oraw* Cp = static_cast<oraw*>(a.C) + bz * a.sc_b;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * WTM + i * 16 + lrow;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = n0 + wn * WTN + j * 16 + lgrp * 4;
+            oraw* crow = Cp + (int64_t)m * a.rsc;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = a.alpha * acc[i][j][r];
+            if (a.beta != 0.0f) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] += a.beta * load_as_f32<TO>(crow, n + r);
+            }
+            if (a.c_vec_ok) {
+                if constexpr (sizeof(oraw) == 2) {
+                    *reinterpret_cast<u32x2*>(crow + n) = u32x2{pack2<TO>(v[0], v[1]), pack2<TO>(v[2], v[3])};
+                } else {
+                    *reinterpret_cast<f32x4*>(crow + n) = f32x4{v[0], v[1], v[2], v[3]};
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) store_from_f32<TO>(crow, n + r, v[r]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny GEMM, M <= 16 (the decode GEMVs: x [1..16, K] . W^T). HBM-bound on
 // the weight stream, so the design goal is bytes in flight, not MFMA reuse.
 //   NT (W^T, the `linear` layout): gemv_kernel in gemv.hip.
@@ -772,7 +942,23 @@ hipError_t launch_dma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
     // once it has most of the 256 CUs busy, 128 x 128 (two workgroups per CU) for
     // mid sizes, 64 x 64 below that; the 64 x 64 ring pays off only while its
     // grid is short of several workgroups per CU.
-    if (tiles(256, 256) >= 192) return launch_dma_tile<T, TO, 256, 256, 2, 4, 2>(a, nn, batch, s);
+    if (tiles(256, 256) >= 192) {
+        if constexpr (sizeof(typename T::raw) == 2) {
+            // whole 256 x 256 tiles of a row-major B: the ping-pong schedule (same bits)
+            constexpr int64_t es = 2;
+            const int64_t span_a = ((int64_t)(a.m - 1) * a.rsa + a.k) * es;
+            const int64_t span_b = ((int64_t)(a.k - 1) * a.rsb + a.n) * es;
+            if (nn && a.m % 256 == 0 && a.n % 256 == 0 && span_a < (int64_t(1) << 31) &&
+                span_b < (int64_t(1) << 31)) {
+                GemmArgs g = a;
+                g.tiles_m = a.m / 256;
+                g.tiles_n = a.n / 256;
+                gemm_pingpong_nn_kernel<T, TO><<<dim3(g.tiles_m * g.tiles_n, batch), 512, 0, s>>>(g);
+                return hipGetLastError();
+            }
+        }
+        return launch_dma_tile<T, TO, 256, 256, 2, 4, 2>(a, nn, batch, s);
+    }
     if (tiles(128, 128) >= 384) return launch_dma_tile<T, TO, 128, 128, 2, 2, 2>(a, nn, batch, s);
     if (tiles(64, 64) >= 768) return launch_dma_tile<T, TO, 64, 64, 2, 2, 2>(a, nn, batch, s);
     // Fewer 64 x 64 tiles than CUs: 64 x 32 tiles (two waves) put twice as many
