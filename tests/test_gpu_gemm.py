@@ -276,23 +276,27 @@ def test_linear_bias_rounds_product_first(orc, yt, dtype):
         yt.linear(xd, Wd, bd[:-1])
 
 
-@pytest.mark.parametrize("dtype,out_dtype,beta,batch", [("bf16", torch.bfloat16, 0.0, 1), ("f16", torch.float16, 0.0, 1),
-                                                        ("bf16", torch.float32, 1.0, 1), ("bf16", torch.bfloat16, 0.0, 2)])
-def test_whole_tile_nn_schedule_bit_identical(yt, dtype, out_dtype, beta, batch):
-    """Whole 256x256 tiles of a row-major B run the ping-pong schedule; the same
-    product with N padded by 16 columns runs the one-phase DMA kernel. Both read
-    the same fragments and issue the same MFMAs in the same order, so the shared
-    columns must agree bit for bit (alpha, beta, fp32 output and a batch too)."""
-    m, n, k = 1024, 12288, 512          # 4 x 48 = 192 tiles of 256 x 256
+@pytest.mark.parametrize("dtype,out_dtype,beta,batch,n", [("bf16", torch.bfloat16, 0.0, 1, 12288),
+                                                          ("f16", torch.float16, 0.0, 1, 12288),
+                                                          ("bf16", torch.float32, 1.0, 1, 12288),
+                                                          ("bf16", torch.bfloat16, 0.0, 2, 12288),
+                                                          ("bf16", torch.bfloat16, 1.0, 1, 12176)])
+def test_whole_tile_nn_schedule_bit_identical(yt, dtype, out_dtype, beta, batch, n):
+    """256-row tiles of a row-major B run the ping-pong schedule (N = 12176 leaves
+    a partial last column of tiles); the same product with M padded by 16 rows
+    runs the one-phase DMA kernel. Both read the same fragments and issue the
+    same MFMAs in the same order, so the shared rows must agree bit for bit
+    (alpha, beta, fp32 output and a batch too)."""
+    m, k = 1024, 512                     # 4 x 48 = 192 tiles of 256 x 256
     dt = TORCH_DT[dtype]
     g = torch.Generator(device="cuda").manual_seed(11)
-    a = torch.randn(batch, m, k, device="cuda", generator=g).to(dt)
-    bp = (torch.randn(batch, k, n + 16, device="cuda", generator=g) * 0.05).to(dt)
-    c0 = torch.randn(batch, m, n + 16, device="cuda", generator=g).to(out_dtype)
+    ap = torch.randn(batch, m + 16, k, device="cuda", generator=g).to(dt)
+    b = (torch.randn(batch, k, n, device="cuda", generator=g) * 0.05).to(dt)
+    c0 = torch.randn(batch, m + 16, n, device="cuda", generator=g).to(out_dtype)
     ref = c0.clone()
-    yt.gemm(a, bp, ref, alpha=0.75, beta=beta)                       # N = 12304: not whole tiles
-    out = c0[:, :, :n].contiguous()
-    yt.gemm(a, bp[:, :, :n].contiguous(), out, alpha=0.75, beta=beta)  # N = 12288: whole tiles
+    yt.gemm(ap, b, ref, alpha=0.75, beta=beta)                        # M = 1040: not whole 256-row tiles
+    out = c0[:, :m].contiguous()
+    yt.gemm(ap[:, :m].contiguous(), b, out, alpha=0.75, beta=beta)    # M = 1024: the ping-pong schedule
     torch.cuda.synchronize()
-    assert torch.equal(out.view(torch.int16 if out.element_size() == 2 else torch.int32),
-                       ref[:, :, :n].contiguous().view(torch.int16 if out.element_size() == 2 else torch.int32))
+    iview = torch.int16 if out.element_size() == 2 else torch.int32
+    assert torch.equal(out.view(iview), ref[:, :m].contiguous().view(iview))

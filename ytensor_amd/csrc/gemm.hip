@@ -558,10 +558,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 // wave loads. Same LDS layouts, swizzles, fragments and MFMA order as
 // gemm_mfma_dma_kernel (bit-identical C). Group A's DMA of a stage lands
 // before the barrier that ends its Y phase, two phases before it is read.
-// Requirements (host): m % 256 == 0, n % 256 == 0, k % 64 == 0, and every
+// Requirements (host): m % 256 == 0, n % 16 == 0, k % 64 == 0, and every
 // operand spans < 2^31 bytes; each DMA is a scalar base plus a 32-bit lane
 // offset fixed for the kernel (A and the k-rows of B repeat their swizzle
-// every 32 rows / every 16 k-rows of a stage).
+// every 32 rows / every 16 k-rows of a stage). A partial last column of tiles
+// re-reads B's last 16 columns and stores only columns below N.
 template <class T, class TO>
 __global__ __launch_bounds__(512, 1) void gemm_pingpong_nn_kernel(GemmArgs a) {
     using raw = typename T::raw;
@@ -597,8 +598,9 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_nn_kernel(GemmArgs a) {
         offA = (uint32_t)(((int64_t)(m0 + r0) * a.rsa + c * 8) * 2);
         const int kr = t / (2 * NBLK), ps = t % (2 * NBLK);
         const int lb0 = nn_blk(kr, ps >> 1, BLK_MASK), lb1 = nn_blk(kr + 8, ps >> 1, BLK_MASK);
-        offB0 = (uint32_t)(((int64_t)kr * a.rsb + n0 + lb0 * 16 + (ps & 1) * 8) * 2);
-        offB1 = (uint32_t)(((int64_t)kr * a.rsb + n0 + lb1 * 16 + (ps & 1) * 8) * 2);
+        // columns past N (a partial last tile column) re-read the last 16 (never stored)
+        offB0 = (uint32_t)(((int64_t)kr * a.rsb + min(n0 + lb0 * 16, a.n - 16) + (ps & 1) * 8) * 2);
+        offB1 = (uint32_t)(((int64_t)kr * a.rsb + min(n0 + lb1 * 16, a.n - 16) + (ps & 1) * 8) * 2);
     }
     const uint32_t ldsA = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sA[(wave & 3) * 64]);
     const uint32_t ldsB = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sB[(wave & 3) * 64]);
@@ -694,6 +696,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_nn_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int n = n0 + wn * WTN + j * 16 + lgrp * 4;
+            if (n >= a.n) continue;  // n % 16 == 0: the lane's 4 columns are all in or all out
             oraw* crow = Cp + (int64_t)m * a.rsc;
             float v[4];
 #pragma unroll
@@ -944,15 +947,15 @@ hipError_t launch_dma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
     // grid is short of several workgroups per CU.
     if (tiles(256, 256) >= 192) {
         if constexpr (sizeof(typename T::raw) == 2) {
-            // whole 256 x 256 tiles of a row-major B: the ping-pong schedule (same bits)
+            // whole 256-row tiles of a row-major B: the ping-pong schedule (same bits)
             constexpr int64_t es = 2;
             const int64_t span_a = ((int64_t)(a.m - 1) * a.rsa + a.k) * es;
             const int64_t span_b = ((int64_t)(a.k - 1) * a.rsb + a.n) * es;
-            if (nn && a.m % 256 == 0 && a.n % 256 == 0 && span_a < (int64_t(1) << 31) &&
+            if (nn && a.m % 256 == 0 && a.n % 16 == 0 && span_a < (int64_t(1) << 31) &&
                 span_b < (int64_t(1) << 31)) {
                 GemmArgs g = a;
                 g.tiles_m = a.m / 256;
-                g.tiles_n = a.n / 256;
+                g.tiles_n = (a.n + 255) / 256;
                 gemm_pingpong_nn_kernel<T, TO><<<dim3(g.tiles_m * g.tiles_n, batch), 512, 0, s>>>(g);
                 return hipGetLastError();
             }
