@@ -667,7 +667,7 @@ def main() -> int:
     traffic = read_traffic(TRAFFIC_FILE)
     roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                "kernel": "gemm_pingpong_nn_kernel<BF16,BF16> (256x256 tile, 8 waves, ping-pong)",
+                "kernel": "gemm_pingpong_kernel<BF16,BF16,NN=true> (256x256 tile, 8 waves, ping-pong)",
                 "algorithmic_flops_per_launch": flops, "avg_launch_ms": round(ms, 5)}
 
     cpu = None

@@ -276,22 +276,28 @@ def test_linear_bias_rounds_product_first(orc, yt, dtype):
         yt.linear(xd, Wd, bd[:-1])
 
 
-@pytest.mark.parametrize("dtype,out_dtype,beta,batch,n", [("bf16", torch.bfloat16, 0.0, 1, 12288),
-                                                          ("f16", torch.float16, 0.0, 1, 12288),
-                                                          ("bf16", torch.float32, 1.0, 1, 12288),
-                                                          ("bf16", torch.bfloat16, 0.0, 2, 12288),
-                                                          ("bf16", torch.bfloat16, 1.0, 1, 12176)])
-def test_whole_tile_nn_schedule_bit_identical(yt, dtype, out_dtype, beta, batch, n):
-    """256-row tiles of a row-major B run the ping-pong schedule (N = 12176 leaves
-    a partial last column of tiles); the same product with M padded by 16 rows
-    runs the one-phase DMA kernel. Both read the same fragments and issue the
-    same MFMAs in the same order, so the shared rows must agree bit for bit
-    (alpha, beta, fp32 output and a batch too)."""
+@pytest.mark.parametrize("dtype,out_dtype,beta,batch,n,layout", [("bf16", torch.bfloat16, 0.0, 1, 12288, "NN"),
+                                                                 ("f16", torch.float16, 0.0, 1, 12288, "NN"),
+                                                                 ("bf16", torch.float32, 1.0, 1, 12288, "NN"),
+                                                                 ("bf16", torch.bfloat16, 0.0, 2, 12288, "NN"),
+                                                                 ("bf16", torch.bfloat16, 1.0, 1, 12176, "NN"),
+                                                                 ("bf16", torch.bfloat16, 0.0, 1, 12288, "NT"),
+                                                                 ("f16", torch.float32, 1.0, 2, 12288, "NT")])
+def test_whole_tile_schedule_bit_identical(yt, dtype, out_dtype, beta, batch, n, layout):
+    """256-row tiles run the ping-pong schedule (NN with N = 12176 leaves a
+    partial last column of tiles; NT reads B as a transposed weight [N, K]);
+    the same product with M padded by 16 rows runs the one-phase DMA kernel.
+    Both read the same fragments and issue the same MFMAs in the same order, so
+    the shared rows must agree bit for bit (alpha, beta, fp32 output and a
+    batch too)."""
     m, k = 1024, 512                     # 4 x 48 = 192 tiles of 256 x 256
     dt = TORCH_DT[dtype]
     g = torch.Generator(device="cuda").manual_seed(11)
     ap = torch.randn(batch, m + 16, k, device="cuda", generator=g).to(dt)
-    b = (torch.randn(batch, k, n, device="cuda", generator=g) * 0.05).to(dt)
+    if layout == "NN":
+        b = (torch.randn(batch, k, n, device="cuda", generator=g) * 0.05).to(dt)
+    else:
+        b = (torch.randn(batch, n, k, device="cuda", generator=g) * 0.05).to(dt).transpose(1, 2)
     c0 = torch.randn(batch, m + 16, n, device="cuda", generator=g).to(out_dtype)
     ref = c0.clone()
     yt.gemm(ap, b, ref, alpha=0.75, beta=beta)                        # M = 1040: not whole 256-row tiles

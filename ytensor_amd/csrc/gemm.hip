@@ -547,26 +547,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// Ping-pong variant of the 256 x 256 DMA kernel for whole tiles with a
-// row-major B (NN, 16-bit). Waves 0-3 (group A) own tile rows 0-127, waves 4-7
-// (group B) rows 128-255; the hardware places waves w and w+4 on one SIMD.
-// Each wave alternates a memory phase X(kt) -- every A and B fragment of k step
-// kt read from LDS into registers (group A also issues the DMA of step kt+1) --
-// and a matrix phase Y(kt) -- the step's 64 MFMAs from registers at raised
-// issue priority -- with group B one phase behind group A and a workgroup
-// barrier per phase, so every SIMD runs one wave's MFMA cluster while the other
-// wave loads. Same LDS layouts, swizzles, fragments and MFMA order as
-// gemm_mfma_dma_kernel (bit-identical C). Group A's DMA of a stage lands
-// before the barrier that ends its Y phase, two phases before it is read.
-// Requirements (host): m % 256 == 0, n % 16 == 0, k % 64 == 0, and every
-// operand spans < 2^31 bytes; each DMA is a scalar base plus a 32-bit lane
-// offset fixed for the kernel (A and the k-rows of B repeat their swizzle
-// every 32 rows / every 16 k-rows of a stage). A partial last column of tiles
-// re-reads B's last 16 columns and stores only columns below N.
-template <class T, class TO>
-__global__ __launch_bounds__(512, 1) void gemm_pingpong_nn_kernel(GemmArgs a) {
+// Ping-pong variant of the 256 x 256 DMA kernel for whole 256-row tiles.
+// Waves 0-3 (group A) own tile rows 0-127, waves 4-7 (group B) rows 128-255;
+// the hardware places waves w and w+4 on one SIMD. Per 64-wide k step kt, after
+// one workgroup barrier,
+//   group A: stages step kt+1 (DMA), reads every fragment of step kt from LDS
+//            into registers (X), then runs the step's 64 MFMAs from registers at
+//            raised issue priority (Y);
+//   group B: runs Y(kt-1) on the fragments it read before the barrier, then
+//            X(kt), and drains its LDS reads;
+// so on each SIMD one wave's MFMA cluster runs while the other wave loads.
+// Group A waits for its DMA of step kt+1 before the next barrier; group B's
+// reads of a stage end before the barrier after which group A refills it.
+// Same LDS layouts, swizzles, fragments and MFMA order as
+// gemm_mfma_dma_kernel (bit-identical C).
+// Requirements (host): m % 256 == 0, k % 64 == 0, every operand spans < 2^31
+// bytes, and NN: n % 16 == 0 / NT: n % 256 == 0. Each DMA is a scalar base
+// plus a 32-bit lane offset fixed for the kernel: A's (and NT B's) chunk
+// swizzle repeats every 32 rows of a stage and NN B's block swizzle depends on
+// the 8-k-row group only through its parity. A partial last column of NN
+// tiles re-reads B's last 16 columns and stores only columns below N.
+template <class T, class TO, bool NN>
+__global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
     using raw = typename T::raw;
-    static_assert(sizeof(raw) == 2, "the transposing LDS read is 16-bit");
+    static_assert(sizeof(raw) == 2, "16-bit operands");
     constexpr int BM = 256, BN = 256, BK = 64, GT = 256;
     constexpr int WTM = 128, WTN = 64, FM = 8, FN = 4;
     constexpr int STA = BM * 8, STB = BN * 8;        // 16-byte slots per stage
@@ -587,20 +591,22 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_nn_kernel(GemmArgs a) {
     u32x4* sA = sbuf;
     u32x4* sB = sbuf + 2 * STA;
 
-    // DMA slot i*256 + t of a stage (t < 256: group A): A row i*32 + t/8 with a
-    // chunk swizzle that does not depend on i; B k-row i*8 + t/32, whose block
-    // swizzle depends on i only through i & 1.
+    // DMA slot i*256 + t of a stage (t < 256: group A)
     const int t = tid & (GT - 1);
     uint32_t offA, offB0, offB1;
     {
         const int r0 = t >> 3;
         const int c = swz_dma(r0, t & 7);
         offA = (uint32_t)(((int64_t)(m0 + r0) * a.rsa + c * 8) * 2);
-        const int kr = t / (2 * NBLK), ps = t % (2 * NBLK);
-        const int lb0 = nn_blk(kr, ps >> 1, BLK_MASK), lb1 = nn_blk(kr + 8, ps >> 1, BLK_MASK);
-        // columns past N (a partial last tile column) re-read the last 16 (never stored)
-        offB0 = (uint32_t)(((int64_t)kr * a.rsb + min(n0 + lb0 * 16, a.n - 16) + (ps & 1) * 8) * 2);
-        offB1 = (uint32_t)(((int64_t)kr * a.rsb + min(n0 + lb1 * 16, a.n - 16) + (ps & 1) * 8) * 2);
+        if constexpr (NN) {
+            // columns past N (a partial last tile column) re-read the last 16 (never stored)
+            const int kr = t / (2 * NBLK), ps = t % (2 * NBLK);
+            const int lb0 = nn_blk(kr, ps >> 1, BLK_MASK), lb1 = nn_blk(kr + 8, ps >> 1, BLK_MASK);
+            offB0 = (uint32_t)(((int64_t)kr * a.rsb + min(n0 + lb0 * 16, a.n - 16) + (ps & 1) * 8) * 2);
+            offB1 = (uint32_t)(((int64_t)kr * a.rsb + min(n0 + lb1 * 16, a.n - 16) + (ps & 1) * 8) * 2);
+        } else {
+            offB0 = offB1 = (uint32_t)(((int64_t)(n0 + r0) * a.csb + c * 8) * 2);
+        }
     }
     const uint32_t ldsA = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sA[(wave & 3) * 64]);
     const uint32_t ldsB = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sB[(wave & 3) * 64]);
@@ -610,28 +616,34 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_nn_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < A_PT; ++i)
             dma16_soff(bA + (int64_t)i * 32 * a.rsa * 2, offA, ldsA + (uint32_t)(st * STA + i * GT) * 16u);
-        const char* bB = reinterpret_cast<const char*>(Bp) + (int64_t)kt * BK * a.rsb * 2;
+        const char* bB = reinterpret_cast<const char*>(Bp) + (int64_t)kt * BK * (NN ? a.rsb : (int64_t)1) * 2;
 #pragma unroll
-        for (int i = 0; i < B_PT; ++i)
-            dma16_soff(bB + (int64_t)i * 8 * a.rsb * 2, (i & 1) ? offB1 : offB0,
-                       ldsB + (uint32_t)(st * STB + i * GT) * 16u);
+        for (int i = 0; i < B_PT; ++i) {
+            const int64_t step = NN ? (int64_t)i * 8 * a.rsb * 2 : (int64_t)i * 32 * a.csb * 2;
+            dma16_soff(bB + step, (i & 1) ? offB1 : offB0, ldsB + (uint32_t)(st * STB + i * GT) * 16u);
+        }
     };
     auto ldA = [&](const u32x4* s, int ks, int i) -> u32x4 {
         const int r = wm * WTM + i * 16 + lrow;
         return s[r * 8 + swz_dma(r, ks * 4 + lgrp)];
     };
     auto ldB = [&](const u32x4* s, int ks, int j) -> u32x4 {
-        const int nb = (wn * WTN + j * 16) >> 4;
-        u32x4 v;
+        if constexpr (!NN) {
+            const int r = wn * WTN + j * 16 + lrow;
+            return s[r * 8 + swz_dma(r, ks * 4 + lgrp)];
+        } else {
+            const int nb = (wn * WTN + j * 16) >> 4;
+            u32x4 v;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int r = ks * 32 + 8 * lgrp + 4 * h + (lrow >> 2);
-            const int byte = r * (BN * 2) + (nn_blk(r, nb, BLK_MASK) << 5) + 8 * (lrow & 3);
-            const u32x2 w = lds_read_tr16(s, byte);
-            v[2 * h] = w[0];
-            v[2 * h + 1] = w[1];
+            for (int h = 0; h < 2; ++h) {
+                const int r = ks * 32 + 8 * lgrp + 4 * h + (lrow >> 2);
+                const int byte = r * (BN * 2) + (nn_blk(r, nb, BLK_MASK) << 5) + 8 * (lrow & 3);
+                const u32x2 w = lds_read_tr16(s, byte);
+                v[2 * h] = w[0];
+                v[2 * h + 1] = w[1];
+            }
+            return v;
         }
-        return v;
     };
 
     f32x4 acc[FM][FN];
@@ -663,29 +675,23 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_nn_kernel(GemmArgs a) {
         __builtin_amdgcn_s_setprio(0);
     };
     constexpr int LGKM0 = 0xc07f;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt not waited
-    if (!grpB) issue(0);
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
     if (!grpB) {
+        issue(0);
         for (int kt = 0; kt < KT; ++kt) {
-            if (kt + 1 < KT) issue(kt + 1);  // stage (kt+1)&1: step kt-1, read by B in phase 2kt-1
+            wait_vmcnt<0>();               // this wave's share of step kt has landed
+            __builtin_amdgcn_s_barrier();  // step kt in LDS; group B done with stage (kt+1)&1
+            if (kt + 1 < KT) issue(kt + 1);
             X(kt);
-            __builtin_amdgcn_s_waitcnt(LGKM0);
-            __builtin_amdgcn_s_barrier();
             Y();
-            wait_vmcnt<0>();  // step kt+1 is in LDS before the next barrier
-            __builtin_amdgcn_s_barrier();
         }
-        __builtin_amdgcn_s_barrier();  // group B's last matrix phase
     } else {
-        __builtin_amdgcn_s_barrier();  // group A's first memory phase
         for (int kt = 0; kt < KT; ++kt) {
+            __builtin_amdgcn_s_barrier();
+            if (kt > 0) Y();  // step kt-1, read before the barrier
             X(kt);
-            __builtin_amdgcn_s_waitcnt(LGKM0);
-            __builtin_amdgcn_s_barrier();
-            Y();
-            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_s_waitcnt(LGKM0);  // the stage's reads end before group A refills it
         }
+        Y();
     }
 
     using oraw = typename TO::raw;
@@ -947,16 +953,18 @@ hipError_t launch_dma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
     // grid is short of several workgroups per CU.
     if (tiles(256, 256) >= 192) {
         if constexpr (sizeof(typename T::raw) == 2) {
-            // whole 256-row tiles of a row-major B: the ping-pong schedule (same bits)
+            // whole 256-row tiles: the ping-pong schedule (same bits)
             constexpr int64_t es = 2;
             const int64_t span_a = ((int64_t)(a.m - 1) * a.rsa + a.k) * es;
-            const int64_t span_b = ((int64_t)(a.k - 1) * a.rsb + a.n) * es;
-            if (nn && a.m % 256 == 0 && a.n % 16 == 0 && span_a < (int64_t(1) << 31) &&
+            const int64_t span_b = (nn ? (int64_t)(a.k - 1) * a.rsb + a.n : (int64_t)(a.n - 1) * a.csb + a.k) * es;
+            if (a.m % 256 == 0 && (nn ? a.n % 16 == 0 : a.n % 256 == 0) && span_a < (int64_t(1) << 31) &&
                 span_b < (int64_t(1) << 31)) {
                 GemmArgs g = a;
                 g.tiles_m = a.m / 256;
                 g.tiles_n = (a.n + 255) / 256;
-                gemm_pingpong_nn_kernel<T, TO><<<dim3(g.tiles_m * g.tiles_n, batch), 512, 0, s>>>(g);
+                const dim3 grid(g.tiles_m * g.tiles_n, batch);
+                if (nn) gemm_pingpong_kernel<T, TO, true><<<grid, 512, 0, s>>>(g);
+                else gemm_pingpong_kernel<T, TO, false><<<grid, 512, 0, s>>>(g);
                 return hipGetLastError();
             }
         }
