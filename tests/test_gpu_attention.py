@@ -196,6 +196,60 @@ def test_prefill_paired_heads(orc, yt, dtype, B, Hq, Hkv, Sq, Skv, D, mk):
     check16(orc, g, r, dtype, True, f"paired heads B={B} {Hq}/{Hkv} {Sq}x{Skv} d={D} {mk} {dtype}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_prefill_key_halves(orc, yt, dtype):
+    """Short prompts split each 128-key stage between two wave groups (keys 0-63
+    and 64-127 of the stage) and merge their O, l, m at the end. Closed forms,
+    exact: a row whose only visible key is k gives V[k], for k in either half and
+    in a later stage (one group saw nothing); a row whose two visible keys a, b
+    (one per half) have the same K row gives (V[a] + V[b]) / 2 (both groups set,
+    equal reference points). Then a causal and a random byte mask over 300 keys
+    (three stages, a partial one) against the oracle."""
+    rng = np.random.default_rng(21)
+    D, Sq, Skv = 128, 40, 200  # a 200-byte mask row is not 16-byte aligned: read per element
+    Q = rng.standard_normal((1, 1, Sq, D)).astype(np.float32)
+    K = rng.standard_normal((1, 1, Skv, D)).astype(np.float32)
+    V = rng.standard_normal((1, 1, Skv, D)).astype(np.float32)
+    K[0, 0, 64:128] = K[0, 0, 0:64]  # key 64 + j has the K row of key j
+    Qd, _ = make_input(orc, Q, dtype)
+    Kd, _ = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    tdt = TORCH_DT[dtype]
+    scale = 1.0 / math.sqrt(D)
+
+    keys = np.array([30, 100, 150, 199])[np.arange(Sq) % 4]
+    m = np.zeros((Sq, Skv), bool)
+    m[np.arange(Sq), keys] = True
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask=torch.from_numpy(m).cuda()))
+    assert np.array_equal(g[0, 0], Vh[0, 0][keys]), "single visible key"
+
+    ka = (np.arange(Sq) * 7) % 64
+    m = np.zeros((Sq, Skv), bool)
+    m[np.arange(Sq), ka] = True
+    m[np.arange(Sq), ka + 64] = True
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask=torch.from_numpy(m).cuda()))
+    expect = torch.from_numpy((Vh[0, 0][ka] + Vh[0, 0][ka + 64]) * np.float32(0.5)).to(tdt).float().numpy()
+    assert np.array_equal(g[0, 0], expect), "two keys with equal scores, one per half"
+
+    B, Hq, Hkv, S = 1, 4, 2, 300
+    Q = rng.standard_normal((B, Hq, S, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, dtype)
+    Kd, Kh = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    r = orc.sdpa_gqa(Qh, Kh, Vh, scale, True)
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask="causal"))
+    check16(orc, g, r, dtype, True, f"key halves causal {dtype}")
+    mk = rng.random((S, S)) > 0.7
+    mk[7] = False
+    r = np.stack([np.stack([orc.flash_attention(Qh[0, h], Kh[0, h // 2], Vh[0, h // 2], scale, mk, None)
+                            for h in range(Hq)])])
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask=torch.from_numpy(mk).cuda()))
+    assert np.all(g[:, :, 7] == 0.0)
+    check16(orc, g, r, dtype, True, f"key halves byte mask {dtype}")
+
+
 def test_prefill_strided_views(orc, yt):
     """q/k/v as [B,S,H,D] memory viewed as [B,H,S,D] (the qwen3 permute views)."""
     rng = np.random.default_rng(4)

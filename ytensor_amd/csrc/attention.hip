@@ -10,7 +10,10 @@
 //
 // Prefill kernel (16-bit inputs, d in {64, 128}):
 //   * Workgroup = 4 waves x 32 queries = 128 queries of one (batch, head);
-//     key/value blocks of 64 keys double-buffered in LDS.
+//     key/value blocks of 64 keys double-buffered in LDS. Short prompts take
+//     16 queries per wave, and without a staged mask 8 waves splitting each
+//     128-key stage in two halves merged at the end; long ones with an even
+//     GQA group the paired-head ping-pong kernel.
 //   * S^T = K . Q^T on v_mfma_f32_16x16x32: src0 = K rows, src1 = Q rows, so
 //     lane l holds 16 scores of ONE query (l % 16) -> the online softmax is
 //     lane-local plus two cross-group shuffles (xor 16, 32) for the max.
@@ -80,19 +83,27 @@ struct AttnArgs {
 // the linear id is remapped so each XCD walks a contiguous range of
 // (kv head, query block) pairs -- one KV head's K/V stays in one XCD's L2 --
 // and, for causal masks, the longest query blocks start first.
-template <class T, int D, int MODE, int GH, int QT, int NKT = 4>
-__global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
+// KSPLIT = 2 (one head per workgroup, no staged mask): 8 waves serve the same
+// query block, each stage holds 2 * BKV keys, waves 0-3 take its first BKV
+// keys and waves 4-7 the second, each with its own online softmax; at the end
+// waves 4-7 hand O, l and m to waves 0-3 through LDS, which merge them
+// (O = a0 O0 + a1 O1, l likewise, a = 2^(m - max m)). Short prompts use it:
+// the longest query block's serial chain of key blocks is halved.
+template <class T, int D, int MODE, int GH, int QT, int NKT = 4, int KSPLIT = 1>
+__global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd_mfma(AttnArgs a) {
     using raw = typename T::raw;
-    constexpr int THREADS = 256 * GH;
+    static_assert(KSPLIT == 1 || (KSPLIT == 2 && GH == 1 && MODE != 3), "key split: one head, no staged mask");
+    constexpr int THREADS = 256 * GH * KSPLIT;
     constexpr int WQ = 16 * QT, BQ = 4 * WQ, BKV = 16 * NKT;  // QT 16-query tiles per wave, NKT 16-key tiles per block
+    constexpr int SBKV = BKV * KSPLIT;  // keys per stage
     constexpr int KCH = D / 8;    // 16-byte chunks per K/V row
     constexpr int DT = D / 16;    // output d tiles
     constexpr int KS = D / 32;    // d steps of the score MFMA
-    constexpr int PT = BKV * KCH / THREADS;
-    static_assert(PT * THREADS == BKV * KCH, "tile / thread mismatch");
+    constexpr int PT = SBKV * KCH / THREADS;
+    static_assert(PT * THREADS == SBKV * KCH, "tile / thread mismatch");
     constexpr int NB = D / 16;    // 32-byte blocks per V row
     constexpr int BMASK = (NB < 8 ? NB : 8) - 1;
-    constexpr int STG = BKV * KCH;  // u32x4 slots per tile
+    constexpr int STG = SBKV * KCH;  // u32x4 slots per stage
     // K chunk swizzle: with D = 128 a K row is one full 256-byte bank window, so
     // 16 consecutive keys XOR their chunk index with key & 15 and a fragment read
     // (16 keys, one logical chunk) touches all 64 banks once.
@@ -127,7 +138,8 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     const int rem = unit % (a.Hkv * hgroups);
     const int kvh = rem / hgroups;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = kvh * G + (rem % hgroups) * GH + (wave >> 2);
+    const int grp = KSPLIT == 2 ? (wave >> 2) : 0;  // key half of each stage
+    const int h = kvh * G + (rem % hgroups) * GH + (KSPLIT == 1 ? (wave >> 2) : 0);
     const int l16 = lane & 15, g = lane >> 4;
     const int q0 = qb * BQ + (wave & 3) * WQ;
 
@@ -160,7 +172,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     const int off = a.diag_off;  // causal: key j visible to query i iff j <= i + off
     int kv_end = a.Skv;
     if (MODE == 1) kv_end = min(a.Skv, qb * BQ + BQ + off);
-    const int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;
+    const int nkb = kv_end > 0 ? (kv_end + SBKV - 1) / SBKV : 0;  // stages
 
     // m is the reference point of the exponentials (log2 units), set by the
     // first block with a visible key and moved only when a block's max exceeds
@@ -198,7 +210,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
     }
     auto issue = [&](int kb) {
-        const int k0 = kb * BKV;
+        const int k0 = kb * SBKV;
         u32x4* dK = sK + (kb & 1) * STG;
         u32x4* dV = sV + (kb & 1) * STG;
         if constexpr (MODE == 3) {
@@ -216,7 +228,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         }
         const raw* kbase = Kp + (int64_t)k0 * a.ks2;
         const raw* vbase = Vp + (int64_t)k0 * a.vs2;
-        if (k0 + BKV <= a.Skv) {
+        if (k0 + SBKV <= a.Skv) {
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 dma16_async(kbase + koff[i], &dK[i * THREADS + wave * 64]);
@@ -236,7 +248,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     f32x4 s[QT][NKT];
     // S^T - m = K . Q^T - m for block kb (K stage kb & 1).
     auto qk = [&](int kb) {
-        const u32x4* cK = sK + (kb & 1) * STG;
+        const u32x4* cK = sK + (kb & 1) * STG + grp * BKV * KCH;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
@@ -284,7 +296,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
     };
     // Online softmax of block kb and O += V^T P^T (V stage kb & 1).
     auto softmax_pv = [&](int kb) {
-        const int k0 = kb * BKV;
+        const int k0 = kb * SBKV + grp * BKV;
         const bool staged = MODE == 3 && k0 + BKV <= a.Skv;
         const bool need_mask = (MODE == 2) || (MODE == 3 && !tile_all) || (k0 + BKV > a.Skv) ||
                                (MODE == 1 && k0 + BKV - 1 > q0 + off);
@@ -372,7 +384,7 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
                 lsum[qt] *= alpha[qt];
             }
         }
-        const u32x4* cV = sV + (kb & 1) * STG;
+        const u32x4* cV = sV + (kb & 1) * STG + grp * BKV * KCH;
 #pragma unroll
         for (int kk = 0; kk < NKT / 2; ++kk) {
 #pragma unroll
@@ -394,7 +406,10 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         }
     };
     // Wave-uniform: does block kb hold any key visible to this wave's queries?
-    auto active = [&](int kb) { return (MODE != 1) || (kb * BKV <= q0 + WQ - 1 + off); };
+    auto active = [&](int kb) {
+        const int k0 = kb * SBKV + grp * BKV;
+        return (KSPLIT == 1 || k0 < a.Skv) && ((MODE != 1) || (k0 <= q0 + WQ - 1 + off));
+    };
 
     if (nkb > 0) issue(0);
     __builtin_amdgcn_s_waitcnt(0);
@@ -411,6 +426,44 @@ __global__ __launch_bounds__(256 * GH, 2 / GH) void attn_fwd_mfma(AttnArgs a) {
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+    }
+
+    if constexpr (KSPLIT == 2) {
+        // Every wave is past the last barrier, so the stages are free: waves 4-7
+        // leave O and l (one u32x4 slot per lane) and m (-inf where none of its
+        // keys was visible) for the wave with the same query rows.
+        const int wl = wave & 3;
+        u32x4* xo = sK;
+        float* xm = reinterpret_cast<float*>(sV);
+        if (grp == 1) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                u32x4* dst = xo + ((wl * QT + qt) * (DT + 1)) * 64 + lane;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) dst[dt * 64] = __builtin_bit_cast(u32x4, o[qt][dt]);
+                dst[DT * 64] = __builtin_bit_cast(u32x4, lsum[qt]);
+                xm[(wl * QT + qt) * 64 + lane] = mset[qt] ? m[qt] : -INFINITY;
+            }
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const u32x4* src = xo + ((wl * QT + qt) * (DT + 1)) * 64 + lane;
+            const float m1 = xm[(wl * QT + qt) * 64 + lane];
+            float a0 = 1.f, a1 = 0.f;
+            if (!mset[qt]) {
+                a0 = 0.f;
+                a1 = 1.f;
+            } else if (m1 != -INFINITY) {
+                const float mt = fmaxf(m[qt], m1);
+                a0 = __builtin_amdgcn_exp2f(m[qt] - mt);
+                a1 = __builtin_amdgcn_exp2f(m1 - mt);
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[qt][dt] = o[qt][dt] * a0 + __builtin_bit_cast(f32x4, src[dt * 64]) * a1;
+            lsum[qt] = lsum[qt] * a0 + __builtin_bit_cast(f32x4, src[DT * 64]) * a1;
+        }
     }
 
     raw* Op = static_cast<raw*>(a.O) + b * a.os0 + h * a.os1;
@@ -1294,6 +1347,20 @@ hipError_t launch_prefill_gh(AttnArgs a, int mode, hipStream_t s) {
     return hipGetLastError();
 }
 
+// One head per 8-wave workgroup, 64 queries, 128-key stages split between the
+// two wave groups (128 KB of LDS: one workgroup per CU, heaviest blocks first,
+// each CU's next workgroup taken as the previous one ends).
+template <class T, int D>
+hipError_t launch_prefill_split(AttnArgs a, int mode, hipStream_t s) {
+    a.nqb = (a.Sq + 63) / 64;
+    a.balance = 0;
+    dim3 grid(a.nqb * a.B * a.Hq);
+    if (mode == 0) attn_fwd_mfma<T, D, 0, 1, 1, 4, 2><<<grid, 512, 0, s>>>(a);
+    else if (mode == 1) attn_fwd_mfma<T, D, 1, 1, 1, 4, 2><<<grid, 512, 0, s>>>(a);
+    else attn_fwd_mfma<T, D, 2, 1, 1, 4, 2><<<grid, 512, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 template <class T, int D>
 hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     // Two query heads per workgroup (K/V staged once for both) when the GQA
@@ -1316,8 +1383,11 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
         return launch_prefill_gh<T, D, 2, 2, 8>(a, mode, s);
     }
     // Short sequences: 16 queries per wave doubles the workgroups (two per CU)
-    // and halves the per-block work on the longest causal row's serial chain.
+    // and halves the per-block work on the longest causal row's serial chain;
+    // without a staged mask the key split halves that chain again (S=2048
+    // causal: 40.1 -> 35.5 us; S=512: 13.1 -> 11.9 us).
     const int64_t wgs = (int64_t)((a.Sq + 127) / 128) * a.B * a.Hq;
+    if (wgs < 512 && mode != 3) return launch_prefill_split<T, D>(a, mode, s);
     if (wgs < 512) return launch_prefill_gh<T, D, 1, 1>(a, mode, s);
     return launch_prefill_gh<T, D, 1, 2>(a, mode, s);
 }
