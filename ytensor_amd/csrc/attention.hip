@@ -301,12 +301,11 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
         const bool need_mask = (MODE == 2) || (MODE == 3 && !tile_all) || (k0 + BKV > a.Skv) ||
                                (MODE == 1 && k0 + BKV - 1 > q0 + off);
         u32x4 pk[QT][NKT / 2];
-        bool rescale = false;
-        float alpha[QT];
+        float lmax[QT];
+        bool trig = false;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             const int qa = q0 + qt * 16 + l16;
-            float v[NKT][4];
             if (need_mask) {
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt)
@@ -331,13 +330,8 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
                             if (vis && a.bias != nullptr)
                                 x += a.bias[(int64_t)qa * a.brs + (int64_t)key * a.bcs] * LOG2E;
                         }
-                        v[kt][r] = vis ? x : -INFINITY;
+                        s[qt][kt][r] = vis ? x : -INFINITY;
                     }
-            } else {
-#pragma unroll
-                for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) v[kt][r] = s[qt][kt][r];
             }
             // IEEE maximum (NaN-propagating) instead of fmaxf: gfx950's v_maximum3_f32
             // takes the MFMA results as they are, where fmaxf first canonicalises
@@ -346,43 +340,52 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, v[kt][r]);
-            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 16, 64));
-            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32, 64));
-            // mx is relative to m. Set m on the first visible block, afterwards
-            // move it only when the block max is far above it.
-            const bool move = mset[qt] ? (mx > LAZY) : (mx != -INFINITY);
-            const float delta = move ? mx : 0.f;
-            const bool moved = move && mset[qt];  // O and l hold terms to rescale
-            alpha[qt] = moved ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
-            rescale |= moved;
-            m[qt] += delta;
-            mset[qt] = mset[qt] || move;
-            if (__ballot(move) != 0) {
+                for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, s[qt][kt][r]);
+            lmax[qt] = mx;
+            // the reference point of a row moves (set on its first visible block,
+            // afterwards only for a block max far above it) iff one of its lanes sees this
+            trig = trig || (mset[qt] ? (mx > LAZY) : (mx != -INFINITY));
+        }
+        auto exps = [&]() {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                for (int kk = 0; kk < NKT / 2; ++kk) {
+                    float e[8];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        e[r] = __builtin_amdgcn_exp2f(s[qt][2 * kk][r]);
+                        e[4 + r] = __builtin_amdgcn_exp2f(s[qt][2 * kk + 1][r]);
+                    }
+                    pk[qt][kk] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
+                                       pack2<T>(e[6], e[7])};
+                }
+        };
+        // p = 2^(s - m) with the current m, issued without waiting for the test;
+        // final unless some row's reference point moves in this block.
+        exps();
+        if (__ballot(trig) != 0) {
+            // Rare: full row max (the row's 16-lane groups), move m, rescale O
+            // and l, exps again -- the same values as deciding before the exps.
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                float mx = lmax[qt];
+                mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 16, 64));
+                mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32, 64));
+                const bool move = mset[qt] ? (mx > LAZY) : (mx != -INFINITY);
+                const float delta = move ? mx : 0.f;
+                const float alpha = (move && mset[qt]) ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
+                m[qt] += delta;
+                mset[qt] = mset[qt] || move;
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) v[kt][r] -= delta;
+                    for (int r = 0; r < 4; ++r) s[qt][kt][r] -= delta;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha;
+                lsum[qt] *= alpha;
             }
-#pragma unroll
-            for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v[kt][r] = __builtin_amdgcn_exp2f(v[kt][r]);
-#pragma unroll
-            for (int kk = 0; kk < NKT / 2; ++kk) {
-                pk[qt][kk] = u32x4{pack2<T>(v[2 * kk][0], v[2 * kk][1]), pack2<T>(v[2 * kk][2], v[2 * kk][3]),
-                                   pack2<T>(v[2 * kk + 1][0], v[2 * kk + 1][1]),
-                                   pack2<T>(v[2 * kk + 1][2], v[2 * kk + 1][3])};
-            }
-        }
-        // O *= alpha only when some lane's reference point moved in this block.
-        if (__ballot(rescale) != 0) {
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha[qt];
-                lsum[qt] *= alpha[qt];
-            }
+            exps();
         }
         const u32x4* cV = sV + (kb & 1) * STG + grp * BKV * KCH;
 #pragma unroll
@@ -494,8 +497,12 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
 //   S(j): mask, row max, reference-point update, exp2 and packing of block j,
 // with group B one phase behind group A and a workgroup barrier per phase, so
 // on every SIMD one wave's MFMA phase runs beside the other wave's softmax.
-// Group B stages K(j+1) and V(j) during its S(j-1) and waits for them at the
-// end of its M(j); A reads them from phase 2j+2 on. The arithmetic per score
+// Group B stages K(j+1) during its S(j-1) (phase 2j) and group A stages V(j)
+// during its S(j) (phase 2j+1); each waits for its own DMA at the end of phase
+// 2j+1, and both are first read in phase 2j+2. A wave issues in order and DMA
+// instructions back to back wait for the address unit (about 30 bytes per
+// clock per CU), so each group issues half of a block's DMA in the phase
+// where it has slack. The arithmetic per score
 // and its order (accumulator started at -m, lazy reference point, packed p,
 // ones-MFMA row sums, O accumulated block by block) are those of
 // attn_fwd_mfma with 64-key blocks.
@@ -695,9 +702,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     auto sphase = [&](int kb) {
         const int k0 = kb * BKV;
         const bool msk = (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off);
-        float delta[QT];
-        bool moved[QT];
-        bool any = false;
+        float lmax[QT];
+        bool trig = false;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             const int qa = q0 + qt * 16 + l16;
@@ -717,46 +723,57 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, s[qt][kt][r]);
-            mx = max_across_rows(mx);
-            const bool move = mset[qt] ? (mx > LAZY) : (mx != -INFINITY);
-            delta[qt] = move ? mx : 0.f;
-            moved[qt] = move && mset[qt];
-            m[qt] += delta[qt];
-            mset[qt] = mset[qt] || move;
-            any = any || delta[qt] != 0.f;
+            lmax[qt] = mx;
+            // a row's reference point moves iff one of its lanes sees this
+            trig = trig || (mset[qt] ? (mx > LAZY) : (mx != -INFINITY));
         }
-        // one wave-uniform branch for both query tiles: rare after the first block
-        if (__ballot(any) != 0) {
+        auto exps = [&]() {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                for (int kk = 0; kk < NKT / 2; ++kk) {
+                    float e[8];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        e[r] = __builtin_amdgcn_exp2f(s[qt][2 * kk][r]);
+                        e[4 + r] = __builtin_amdgcn_exp2f(s[qt][2 * kk + 1][r]);
+                    }
+                    pk[qt][kk] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
+                                       pack2<T>(e[6], e[7])};
+                }
+        };
+        // p = 2^(s - m) with the current m, issued without waiting for the test;
+        // when no lane's row moves its reference point (every block after a
+        // row's first, barring a max more than LAZY above m) these are final.
+        exps();
+        if (__ballot(trig) != 0) {
+            // Rare: full row max across the row's lanes, move m, rescale O and l,
+            // exps again -- the same values as deciding before the exps.
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
+                const float mx = max_across_rows(lmax[qt]);
+                const bool move = mset[qt] ? (mx > LAZY) : (mx != -INFINITY);
+                const float delta = move ? mx : 0.f;
+                const float alpha = (move && mset[qt]) ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
+                m[qt] += delta;
+                mset[qt] = mset[qt] || move;
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) s[qt][kt][r] -= delta[qt];
-                const float alpha = moved[qt] ? __builtin_amdgcn_exp2f(-delta[qt]) : 1.0f;
+                    for (int r = 0; r < 4; ++r) s[qt][kt][r] -= delta;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha;
                 lsum[qt] *= alpha;
             }
+            exps();
         }
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-            for (int kk = 0; kk < NKT / 2; ++kk) {
-                float e[8];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    e[r] = __builtin_amdgcn_exp2f(s[qt][2 * kk][r]);
-                    e[4 + r] = __builtin_amdgcn_exp2f(s[qt][2 * kk + 1][r]);
-                }
-                pk[qt][kk] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
-                                   pack2<T>(e[6], e[7])};
-            }
     };
 
-    // Phase 2j: A runs M(j), B runs S(j-1) and stages K(j+1), V(j).
-    // Phase 2j+1: A runs S(j), B runs M(j). Every wave passes 2 (nkb + 1) + 1
-    // barriers; K(0) is staged by group A before the first one.
+    // Phase 2j: A runs M(j), B stages K(j+1) and runs S(j-1).
+    // Phase 2j+1: A stages V(j) and runs S(j), B runs M(j). The K stage B fills
+    // held K(j-1) and the V stage A fills held V(j-2), both last read in
+    // phases 2j-2 and 2j-1. Every wave passes 2 (nkb + 1) + 1 barriers; K(0) is
+    // staged by group A before the first one.
     if (nkb > 0 && !grpB) issue_k(0);
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_s_barrier();
@@ -765,17 +782,18 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
             mphase(j - 1, j >= 1 && j - 1 < nkw, j, j < nkw);
             __builtin_amdgcn_s_waitcnt(0);
             __builtin_amdgcn_s_barrier();
+            if (j < nkb) issue_v(j);
             if (j < nkw) sphase(j);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's V(j) DMA has landed
             __builtin_amdgcn_s_barrier();
         }
     } else {
         for (int j = 0; j <= nkb; ++j) {
             if (j + 1 < nkb) issue_k(j + 1);
-            if (j < nkb) issue_v(j);
             if (j >= 1 && j - 1 < nkw) sphase(j - 1);
             __builtin_amdgcn_s_barrier();
             mphase(j - 1, j >= 1 && j - 1 < nkw, j, j < nkw);
-            __builtin_amdgcn_s_waitcnt(0);  // this wave's K(j+1) / V(j) DMA has landed
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's K(j+1) DMA has landed
             __builtin_amdgcn_s_barrier();
         }
     }
