@@ -114,7 +114,19 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
     constexpr int MSTG = BQ * MCH;                // mask chunks per stage
     constexpr int MPT = MSTG / THREADS;
     static_assert(MODE != 3 || MPT * THREADS == MSTG, "mask tile / thread mismatch");
-    __shared__ u32x4 sM[MODE == 3 ? 2 * MSTG : 1];
+    // SKIP (staged mask, paired heads): the mask tiles run MAHEAD = 6 blocks
+    // ahead in a ring of 8, each wave tests block kb+2 during step kb and
+    // publishes whether its rows see a key, and after step kb's barrier the
+    // workgroup stages K/V(kb+1) only if some wave does -- an all-false block
+    // costs a tile test and a barrier, no K/V DMA and no MFMA, and no wait on a
+    // DMA of its own step.
+    constexpr bool SKIP = MODE == 3 && GH == 2;
+    constexpr int MAHEAD = 6;
+    constexpr int MRING = SKIP ? 8 : 2;
+    static_assert(!SKIP || THREADS == 512, "one flag byte per wave, 8 waves");
+    __shared__ u32x4 sM[MODE == 3 ? MRING * MSTG : 1];
+    __shared__ uint64_t sflag[2];
+    auto mslot = [](int kb) { return kb & (MRING - 1); };
 
     // (batch, kv head or head pair, query block) from the XCD-remapped id.
     const int G = a.Hq / a.Hkv;
@@ -133,7 +145,10 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
     // a CU pairs a heavy block with a light one. Per unit the order stays a
     // permutation of its query blocks.
     const bool light_first = a.balance && (unit & 1);
-    const int qb = (MODE == 1 && !light_first) ? (a.nqb - 1 - qi) : qi;
+    // the staged-mask kernel with block skipping also starts from the last query
+    // block: in causal-shaped masks (the KV ring's included) later rows see more keys
+    constexpr bool HEAVY_FIRST = MODE == 1 || (MODE == 3 && GH == 2);
+    const int qb = (HEAVY_FIRST && !light_first) ? (a.nqb - 1 - qi) : qi;
     const int b = unit / (a.Hkv * hgroups);
     const int rem = unit % (a.Hkv * hgroups);
     const int kvh = rem / hgroups;
@@ -209,11 +224,9 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
         koff[i] = row * (int)a.ks2 + (ps ^ (row & KMASK)) * 8;
         voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
     }
-    auto issue = [&](int kb) {
-        const int k0 = kb * SBKV;
-        u32x4* dK = sK + (kb & 1) * STG;
-        u32x4* dV = sV + (kb & 1) * STG;
+    auto issue_mask = [&](int kb) {
         if constexpr (MODE == 3) {
+            const int k0 = kb * SBKV;
             if (k0 + BKV <= a.Skv) {
                 // mask rows of the query block (clamped to the last query row)
 #pragma unroll
@@ -222,10 +235,16 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
                     const int r = slot / MCH, c = slot % MCH;
                     const int row = min(qb * BQ + r, a.Sq - 1);
                     dma16_async(a.mask + (int64_t)row * a.mask_ld + k0 + c * 16,
-                                &sM[(kb & 1) * MSTG + i * THREADS + wave * 64]);
+                                &sM[mslot(kb) * MSTG + i * THREADS + wave * 64]);
                 }
             }
         }
+    };
+    auto issue = [&](int kb) {
+        const int k0 = kb * SBKV;
+        u32x4* dK = sK + (kb & 1) * STG;
+        u32x4* dV = sV + (kb & 1) * STG;
+        if (!SKIP) issue_mask(kb);
         const raw* kbase = Kp + (int64_t)k0 * a.ks2;
         const raw* vbase = Vp + (int64_t)k0 * a.vs2;
         if (k0 + SBKV <= a.Skv) {
@@ -275,7 +294,7 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
                 return;
             }
             constexpr int WCH = WQ * MCH;  // 16-byte chunks of this wave's rows
-            const u32x4* t = sM + (kb & 1) * MSTG + ((wave & 3) * WQ) * MCH;
+            const u32x4* t = sM + mslot(kb) * MSTG + ((wave & 3) * WQ) * MCH;
             bool any = false, all = true;
 #pragma unroll
             for (int i = 0; i < (WCH + 63) / 64; ++i) {
@@ -317,7 +336,7 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
                         if (MODE == 1) vis = vis && (key <= qa + off);
                         if (MODE == 3) {
                             if (staged) {
-                                const uint32_t w = reinterpret_cast<const uint32_t*>(sM + (kb & 1) * MSTG)
+                                const uint32_t w = reinterpret_cast<const uint32_t*>(sM + mslot(kb) * MSTG)
                                     [((qa - qb * BQ) * BKV + kt * 16 + g * 4) >> 2];
                                 vis = ((w >> (8 * r)) & 0xffu) != 0u;
                             } else if (vis && qa < a.Sq) {
@@ -414,21 +433,88 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
         return (KSPLIT == 1 || k0 < a.Skv) && ((MODE != 1) || (k0 <= q0 + WQ - 1 + off));
     };
 
-    if (nkb > 0) issue(0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    for (int kb = 0; kb < nkb; ++kb) {
-        if (kb + 1 < nkb) issue(kb + 1);
-        if (active(kb)) {
-            mask_tile(kb);
+    if constexpr (SKIP) {
+        // Flag word kb & 1 holds one byte per wave, "its rows see a key of block
+        // kb": written in step kb-2, read in step kb-1 before K/V(kb) is issued.
+        // A wave computes block kb only when its own test of the tile found a
+        // key, which implies K/V(kb) was staged. Mask tile t is DMA'd in step t-6 into
+        // the slot of tile t-8 (last read in step t-8) and waited for at the end
+        // of step t-3, before the barrier after which step t-2 tests it.
+        // Each wave keeps its own (any, all) for tiles kb, kb+1, kb+2 in
+        // registers: every tile is tested once, two steps before its compute.
+        bool any0 = false, all0 = false, any1 = false, all1 = false;
+        auto publish = [&](int kb, bool& any, bool& all) {
+            any = false;
+            all = false;
+            if (kb < nkb) {
+                mask_tile(kb);
+                any = tile_any;
+                all = tile_all;
+            }
+            if (lane == 0) reinterpret_cast<uint8_t*>(&sflag[kb & 1])[wave] = any ? 1 : 0;
+        };
+        auto wg_vis = [&](int kb) { return kb < nkb && sflag[kb & 1] != 0; };
+        // mask DMAs (MPT per thread) issued for tile t: full blocks only
+        auto staged_tile = [&](int t) { return t < nkb && t * BKV + BKV <= a.Skv; };
+        // wait until at most n * MPT of this wave's DMAs are in flight, LDS reads drained
+        auto wait_masks = [&](int n) {
+            constexpr int L0 = 7 << 4;  // expcnt not waited, lgkmcnt(0)
+            if (n >= 3) __builtin_amdgcn_s_waitcnt(((3 * MPT) & 15) | (((3 * MPT) >> 4) << 14) | L0);
+            else if (n == 2) __builtin_amdgcn_s_waitcnt(((2 * MPT) & 15) | (((2 * MPT) >> 4) << 14) | L0);
+            else if (n == 1) __builtin_amdgcn_s_waitcnt((MPT & 15) | ((MPT >> 4) << 14) | L0);
+            else __builtin_amdgcn_s_waitcnt(L0);
+        };
+#pragma unroll
+        for (int t = 0; t < MAHEAD; ++t) issue_mask(t);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        publish(0, any0, all0);
+        publish(1, any1, all1);
+        __syncthreads();
+        if (wg_vis(0)) issue(0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        for (int kb = 0; kb < nkb; ++kb) {
+            const bool kv = wg_vis(kb + 1);
+            if (kv) issue(kb + 1);                               // the K/V stage read in step kb-1
+            if (kb + MAHEAD < nkb) issue_mask(kb + MAHEAD);      // the slot of tile kb-2
+            bool any2, all2;
+            publish(kb + 2, any2, all2);
+            tile_any = any0;
+            tile_all = all0;
             if (tile_any) {
                 qk(kb);
                 softmax_pv(kb);
             }
+            any0 = any1;
+            all0 = all1;
+            any1 = any2;
+            all1 = all2;
+            // K/V(kb+1) and mask tile kb+3 have landed once only the DMAs
+            // issued after them are in flight: mask tiles kb+4..kb+6 (or only
+            // kb+6 when K/V(kb+1) was issued in this step); DMAs retire in order.
+            const int after = kv ? (int)staged_tile(kb + 6)
+                                 : (int)staged_tile(kb + 4) + (int)staged_tile(kb + 5) + (int)staged_tile(kb + 6);
+            wait_masks(after);
+            __syncthreads();
         }
+    } else {
+        if (nkb > 0) issue(0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+
+        for (int kb = 0; kb < nkb; ++kb) {
+            if (kb + 1 < nkb) issue(kb + 1);
+            if (active(kb)) {
+                mask_tile(kb);
+                if (tile_any) {
+                    qk(kb);
+                    softmax_pv(kb);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
     }
 
     if constexpr (KSPLIT == 2) {
