@@ -282,11 +282,15 @@ def test_linear_bias_rounds_product_first(orc, yt, dtype):
                                                                  ("bf16", torch.bfloat16, 0.0, 2, 12288, "NN"),
                                                                  ("bf16", torch.bfloat16, 1.0, 1, 12176, "NN"),
                                                                  ("bf16", torch.bfloat16, 0.0, 1, 12288, "NT"),
-                                                                 ("f16", torch.float32, 1.0, 2, 12288, "NT")])
+                                                                 ("f16", torch.float32, 1.0, 2, 12288, "NT"),
+                                                                 ("bf16", torch.bfloat16, 1.0, 1, 12432, "NT"),
+                                                                 ("f16", torch.float32, 0.0, 2, 12304, "NT")])
 def test_whole_tile_schedule_bit_identical(yt, dtype, out_dtype, beta, batch, n, layout):
     """256-row tiles run the ping-pong schedule (NN with N = 12176 leaves a
-    partial last column of tiles; NT reads B as a transposed weight [N, K]);
-    the same product with M padded by 16 rows runs the one-phase DMA kernel.
+    partial last column of tiles; NT reads B as a transposed weight [N, K], and
+    with N = 12432 or 12304 its last 144 or 16 columns run as a second, small
+    product); the same product with M padded by 16 rows runs the one-phase DMA
+    kernel.
     Both read the same fragments and issue the same MFMAs in the same order, so
     the shared rows must agree bit for bit (alpha, beta, fp32 output and a
     batch too)."""

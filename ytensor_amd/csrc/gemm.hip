@@ -957,6 +957,25 @@ hipError_t launch_dma(const GemmArgs& a, bool nn, int batch, hipStream_t s) {
             constexpr int64_t es = 2;
             const int64_t span_a = ((int64_t)(a.m - 1) * a.rsa + a.k) * es;
             const int64_t span_b = (nn ? (int64_t)(a.k - 1) * a.rsb + a.n : (int64_t)(a.n - 1) * a.csb + a.k) * es;
+            // NT with a partial last column of tiles: the whole tiles on the
+            // ping-pong kernel, the last N % 256 columns as a product of their own
+            // (disjoint columns of C; B rows and C columns offset).
+            if (!nn && a.m % 256 == 0 && a.n % 256 != 0 && a.n > 256 && span_a < (int64_t(1) << 31) &&
+                span_b < (int64_t(1) << 31)) {
+                using oraw = typename TO::raw;
+                GemmArgs g = a;
+                g.n = a.n / 256 * 256;
+                g.tiles_m = a.m / 256;
+                g.tiles_n = g.n / 256;
+                gemm_pingpong_kernel<T, TO, false><<<dim3(g.tiles_m * g.tiles_n, batch), 512, 0, s>>>(g);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                GemmArgs r = a;
+                r.n = a.n - g.n;
+                r.B = static_cast<const typename T::raw*>(a.B) + (int64_t)g.n * a.csb;
+                r.C = static_cast<oraw*>(a.C) + g.n;
+                return launch_dma<T, TO>(r, nn, batch, s);
+            }
             if (a.m % 256 == 0 && (nn ? a.n % 16 == 0 : a.n % 256 == 0) && span_a < (int64_t(1) << 31) &&
                 span_b < (int64_t(1) << 31)) {
                 GemmArgs g = a;
