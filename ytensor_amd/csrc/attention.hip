@@ -588,12 +588,10 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
 // 2j+1, and both are first read in phase 2j+2. A wave issues in order and DMA
 // instructions back to back wait for the address unit (about 30 bytes per
 // clock per CU), so each group issues half of a block's DMA in the phase
-// where it has slack. The arithmetic per score and its order (accumulator
-// started at -m, lazy reference point, packed p, O accumulated block by block)
-// are those of attn_fwd_mfma with 64-key blocks; the row sums l are fp32 sums
-// of the unrounded p on the VALU (each lane its 16 keys per block, the row's 4
-// lanes added at the end) in place of attn_fwd_mfma's ones-MFMA over the
-// packed p: 4 of 68 MFMAs per block and 19 VGPRs fewer.
+// where it has slack. The arithmetic per score
+// and its order (accumulator started at -m, lazy reference point, packed p,
+// ones-MFMA row sums, O accumulated block by block) are those of
+// attn_fwd_mfma with 64-key blocks.
 template <class T, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     using raw = typename T::raw;
@@ -662,16 +660,16 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     const int nkw = kv_end_w > 0 ? (kv_end_w + BKV - 1) / BKV : 0;  // blocks this wave's rows see
 
     constexpr float LAZY = 8.0f;
+    constexpr uint32_t ONE2 = std::is_same_v<T, BF16> ? 0x3F803F80u : 0x3C003C00u;
+    const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
     float m[QT];
     bool mset[QT];
-    // l: this lane's share of the row sum (its 16 keys of each block), summed
-    // in fp32 as the exps leave the VALU; the row's 4 lanes are added at the end.
-    float lsum[QT];
+    f32x4 lsum[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         m[qt] = 0.f;
         mset[qt] = false;
-        lsum[qt] = 0.f;
+        lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     f32x4 o[QT][DT];
 #pragma unroll
@@ -753,6 +751,10 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                 if constexpr (u + PF < NU) fr[(u + PF) % (PF + 1)] = ldv((u + PF) / DT, (u + PF) % DT);
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_chunk(T{}, fr[u % (PF + 1)], pk[qt][kk], o[qt][dt]);
+                if constexpr (dt == DT - 1) {
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) lsum[qt] = mfma_chunk(T{}, ones, pk[qt][kk], lsum[qt]);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             });
         }
@@ -811,11 +813,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
             // a row's reference point moves iff one of its lanes sees this
             trig = trig || (mset[qt] ? (mx > LAZY) : (mx != -INFINITY));
         }
-        float bsum[QT];
         auto exps = [&]() {
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-                float t = 0.f;
+            for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
                 for (int kk = 0; kk < NKT / 2; ++kk) {
                     float e[8];
@@ -826,10 +826,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                     }
                     pk[qt][kk] = u32x4{pack2<T>(e[0], e[1]), pack2<T>(e[2], e[3]), pack2<T>(e[4], e[5]),
                                        pack2<T>(e[6], e[7])};
-                    t += ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
                 }
-                bsum[qt] = t;
-            }
         };
         // p = 2^(s - m) with the current m, issued without waiting for the test;
         // when no lane's row moves its reference point (every block after a
@@ -856,8 +853,6 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
             }
             exps();
         }
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) lsum[qt] += bsum[qt];
     };
 
     // Phase 2j: A runs M(j), B stages K(j+1) and runs S(j-1).
@@ -892,9 +887,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     raw* Op = static_cast<raw*>(a.O) + b * a.os0 + h * a.os1;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        float L = lsum[qt];
-        L += __shfl_xor(L, 16, 64);  // the row's keys are spread over lanes l16 + 16 g
-        L += __shfl_xor(L, 32, 64);
+        const float L = lsum[qt][0];
         const float inv = L > 0.f ? 1.0f / L : 0.f;
         const int q = q0 + qt * 16 + l16;
         if (q >= a.Sq) continue;
