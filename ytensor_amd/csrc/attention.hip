@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
     constexpr int MRING = SKIP ? 8 : 2;
     static_assert(!SKIP || THREADS == 512, "one flag byte per wave, 8 waves");
     __shared__ u32x4 sM[MODE == 3 ? MRING * MSTG : 1];
-    __shared__ uint64_t sflag[2];
+    __shared__ uint64_t sflag[SKIP ? 2 : 1];
     auto mslot = [](int kb) { return kb & (MRING - 1); };
 
     // (batch, kv head or head pair, query block) from the XCD-remapped id.
