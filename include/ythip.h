@@ -105,6 +105,28 @@ int ythip_attn_prefill(int dtype, int B, int Hq, int Hkv, int q_len, int kv_len,
                        const float* bias, int64_t rs_bias, int64_t cs_bias, void* stream);
 
 /*
+ * ythip_attn_prefill with a device workspace for a bool mask's tile classes
+ * (one byte per 32-row x 64-key tile, ythip_attn_prefill_workspace_size(q_len,
+ * kv_len) bytes; fewer is YTHIP_EINVAL). Same arguments and results as
+ * ythip_attn_prefill, which is this call with no workspace. With one, a bool
+ * mask on the long-sequence paired-head path (d in {64, 128}, Hq / Hkv even)
+ * is classified tile by tile first, and the attention then stages only the key
+ * blocks each 128-row query block sees. Same replaced interface as
+ * ythip_attn_prefill (the bool-mask call of flash_attention,
+ * include/kernel/avx2/flash_attention.hpp:21-69); the workspace is this
+ * library's addition, as for ythip_attn_math.
+ */
+size_t ythip_attn_prefill_workspace_size(int q_len, int kv_len);
+int ythip_attn_prefill_ws(int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv,
+                          const void* Q, const int64_t q_str[4],
+                          const void* K, const int64_t k_str[4],
+                          const void* V, const int64_t v_str[4],
+                          void* O, const int64_t o_str[4],
+                          float scale, int mask_kind, const uint8_t* mask, int64_t mask_ld,
+                          const float* bias, int64_t rs_bias, int64_t cs_bias,
+                          void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * Attention forward with the MATH backend (scaledDotProductAttention with
  * sdpaBackend::MATH, src/function/ops.inl:388-418, 474-490): the score matrix is
  * materialised,

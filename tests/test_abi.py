@@ -86,3 +86,25 @@ def test_cpp_mirror_compiles_and_reports_errors(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "ok:" in out.stdout
+
+
+def test_prefill_workspace_size_and_short_workspace():
+    """ythip_attn_prefill_workspace_size: one byte per 32-row x 64-key tile of
+    the bool mask, in 256-byte units; a bool-mask call given fewer bytes is an
+    argument error before any launch (the pointers are never dereferenced)."""
+    import ytensor_amd
+    from ytensor_amd import _lib
+    lib = ytensor_amd.load()
+    assert lib.ythip_attn_prefill_workspace_size(8192, 8192) == 256 * 128
+    assert lib.ythip_attn_prefill_workspace_size(33, 65) == 256
+    assert lib.ythip_attn_prefill_workspace_size(2000, 2096) == 63 * 33 // 256 * 256 + 256
+    assert lib.ythip_attn_prefill_workspace_size(0, 64) == 0
+    assert lib.ythip_attn_prefill_workspace_size(64, 0) == 0
+    fake = ctypes.c_void_p(256)
+    st4 = _lib.i64array([16 * 64 * 128, 64 * 128, 128, 1])
+    st = lib.ythip_attn_prefill_ws(_lib.BF16, 1, 16, 8, 64, 64, 128, 128, fake, st4, fake,
+                                   _lib.i64array([8 * 64 * 128, 64 * 128, 128, 1]), fake,
+                                   _lib.i64array([8 * 64 * 128, 64 * 128, 128, 1]), fake, st4, 0.0,
+                                   _lib.MASK_BOOL, fake, 64, None, 0, 0, fake, 255, None)
+    assert st == _lib.YTHIP_EINVAL
+    assert b"workspace of 256 bytes" in lib.ythip_last_error()

@@ -139,6 +139,9 @@ STAGED_CASES = [(d, k, sq, skv, hq, hkv, 1) for d in ("bf16", "f16")
 # GQA pairs with >= 512 paired workgroups: two heads per workgroup, the mask staged
 # one key block ahead of K/V, key blocks no row of a workgroup sees skipped whole
 STAGED_CASES += [("bf16", k, 2048, 2048, 16, 8, 4) for k in ("causal", "ring", "wgblocks")]
+# the same shapes through the tile-class list (ops passes the workspace): every
+# tile mixed, a partial last key block and query block, 16-row regions
+STAGED_CASES += [("bf16", "random", 2048, 2096, 16, 8, 4), ("f16", "blocks", 2000, 2096, 16, 8, 4)]
 
 
 @pytest.mark.parametrize("dtype,kind,Sq,Skv,Hq,Hkv,B", STAGED_CASES)
@@ -168,6 +171,54 @@ def test_prefill_bool_mask_staged(orc, yt, dtype, kind, Sq, Skv, Hq, Hkv, B):
     empty = ~m.any(axis=1)
     assert np.all(g[:, :, empty] == 0.0)
     check16(orc, g, r, dtype, True, f"staged mask {kind} B={B} {Hq}/{Hkv} heads {Sq}x{Skv} {dtype}")
+
+
+def _prefill_abi(yt, q, k, v, o, mask, ws):
+    """ythip_attn_prefill (ws None) or ythip_attn_prefill_ws on [B, H, S, D] tensors."""
+    from ytensor_amd import _lib
+    from ytensor_amd.ops import _stream, i64array
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    code = _lib.BF16 if q.dtype == torch.bfloat16 else _lib.F16
+    args = (code, B, Hq, Hkv, Sq, Skv, D, D, q.data_ptr(), i64array(q.stride()), k.data_ptr(),
+            i64array(k.stride()), v.data_ptr(), i64array(v.stride()), o.data_ptr(), i64array(o.stride()),
+            1.0 / math.sqrt(D), _lib.MASK_BOOL, mask.data_ptr(), mask.stride(0), None, 0, 0)
+    if ws is None:
+        return _lib.lib().ythip_attn_prefill(*args, _stream())
+    return _lib.lib().ythip_attn_prefill_ws(*args, ws.data_ptr(), ws.numel(), _stream())
+
+
+@pytest.mark.parametrize("Sq,Skv", [(2048, 2048), (2000, 2096)])
+def test_prefill_bool_tiles_equal_causal(yt, Sq, Skv):
+    """A causal mask given as bytes, through the tile-class list, takes the same
+    blocks, masks and order as the causal kind on the ping-pong kernel: the
+    outputs agree bit for bit. Without the workspace the staged-mask kernel runs
+    (oracle-checked above); it is held to bf16 rounding here, though on these
+    masks it has matched bit for bit too."""
+    B, Hq, Hkv, D = 4, 16, 8, 128
+    g = torch.Generator().manual_seed(Sq + Skv)
+    q = torch.randn(B, Hq, Sq, D, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(B, Hkv, Skv, D, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(B, Hkv, Skv, D, generator=g).to(torch.bfloat16).cuda()
+    mk = torch.ones(Sq, Skv, dtype=torch.bool).tril(Skv - Sq).cuda()
+    ref = yt.scaled_dot_product_attention(q, k, v, 1.0 / math.sqrt(D), "causal")
+    got = yt.scaled_dot_product_attention(q, k, v, 1.0 / math.sqrt(D), mk)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    need = int(__import__("ytensor_amd")._lib.lib().ythip_attn_prefill_workspace_size(Sq, Skv))
+    assert need == -(-((Sq + 31) // 32) * ((Skv + 63) // 64) // 256) * 256
+    m8 = mk.view(torch.uint8)
+    o_ws = torch.empty_like(q)
+    assert _prefill_abi(yt, q, k, v, o_ws, m8, torch.empty(need, dtype=torch.uint8, device="cuda")) == 0
+    o_plain = torch.empty_like(q)
+    assert _prefill_abi(yt, q, k, v, o_plain, m8, None) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(o_ws, ref)
+    d = (o_plain.float() - ref.float()).abs()
+    print(f"bool tiles {Sq}x{Skv}: staged-kernel max|d| {d.max().item():.3e} mean {d.mean().item():.3e}", flush=True)
+    assert d.mean().item() < 1e-3 and d.max().item() < 3e-2
+    # one byte short of the tile table: an argument error, nothing launched
+    assert _prefill_abi(yt, q, k, v, o_ws, m8, torch.empty(need - 1, dtype=torch.uint8, device="cuda")) != 0
 
 
 # Two query heads per workgroup without a byte mask (>= 512 paired workgroups):

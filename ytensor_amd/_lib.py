@@ -48,6 +48,9 @@ SIGNATURES = {
     "ythip_gemm": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _F, _F, _P]),
     "ythip_attn_prefill": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _LP, _P, _LP, _P, _LP, _P, _LP,
                                 _F, _I, _P, _L, _P, _L, _L, _P]),
+    "ythip_attn_prefill_workspace_size": (ctypes.c_size_t, [_I, _I]),
+    "ythip_attn_prefill_ws": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _LP, _P, _LP, _P, _LP, _P, _LP,
+                                   _F, _I, _P, _L, _P, _L, _L, _P, ctypes.c_size_t, _P]),
     "ythip_attn_math_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     "ythip_attn_math": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _LP, _P, _LP, _P, _LP, _P, _LP,
                              _F, _I, _P, _L, _P, _L, _L, _P, ctypes.c_size_t, _P]),

@@ -58,6 +58,8 @@ struct AttnArgs {
     int64_t brs, bcs;
     int nqb;
     int balance;  // causal: the grid is resident at once, two workgroups per CU (see attn_fwd_mfma)
+    uint8_t* tcls;        // byte mask's tile classes (mask_tile_class_kernel), or null
+    int nkbt;             // 64-key blocks of the mask rows: ceil(Skv / 64)
 };
 
 // MODE 0: no mask; 1: causal; 2: byte mask and/or bias read per element;
@@ -592,6 +594,60 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
 // and its order (accumulator started at -m, lazy reference point, packed p,
 // ones-MFMA row sums, O accumulated block by block) are those of
 // attn_fwd_mfma with 64-key blocks.
+// Key blocks a ping-pong workgroup can list under a byte mask (kv_len up to
+// 64 * PP_LIST_MAX); longer masks take the staged-mask kernel.
+constexpr int PP_LIST_MAX = 4096;
+
+// Tile classes of a byte mask [Sq, Skv] (row stride ld, rows 16-byte aligned):
+// for each 32-row group rg and 64-key block kb, cls[rg * nkbt + kb] has bit 0
+// set when some (row, key) of the tile is visible and bit 1 when every one is
+// (rows < Sq, keys < Skv). One workgroup per row group and 16 key blocks; the
+// ping-pong kernel lists its blocks from these instead of reading the mask.
+__global__ __launch_bounds__(256) void mask_tile_class_kernel(const uint8_t* mask, int64_t ld, int Sq, int Skv,
+                                                              int nkbt, uint8_t* cls) {
+    __shared__ uint32_t s_any[16], s_all[16];
+    const int t = threadIdx.x, kbl = t & 15, r0 = t >> 4;
+    const int rg = blockIdx.x, kb = blockIdx.y * 16 + kbl;
+    if (t < 16) {
+        s_any[t] = 0u;
+        s_all[t] = 1u;
+    }
+    __syncthreads();
+    bool any = false, all = true;
+    if (kb < nkbt) {
+        const int k0 = kb * 64;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int row = rg * 32 + r0 + 16 * rr;
+            if (row >= Sq) continue;
+            const uint8_t* mr = mask + (int64_t)row * ld + k0;
+            if (k0 + 64 <= Skv) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const u32x4 w = reinterpret_cast<const u32x4*>(mr)[c];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t x = w[e];
+                        any = any || x != 0u;
+                        all = all && ((x - 0x01010101u) & ~x & 0x80808080u) == 0u;  // no zero byte
+                    }
+                }
+            } else {
+                for (int jj = 0; jj < Skv - k0; ++jj) {
+                    const bool v = mr[jj] != 0;
+                    any = any || v;
+                    all = all && v;
+                }
+            }
+        }
+    }
+    if (any) atomicOr(&s_any[kbl], 1u);
+    if (!all) atomicAnd(&s_all[kbl], 0u);
+    __syncthreads();
+    if (t < 16 && blockIdx.y * 16 + t < nkbt)
+        cls[(int64_t)rg * nkbt + blockIdx.y * 16 + t] = (uint8_t)(s_any[t] | (s_all[t] << 1));
+}
+
 template <class T, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     using raw = typename T::raw;
@@ -618,7 +674,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     if ((total & 7) == 0) w = (w & 7) * (total >> 3) + (w >> 3);
     const int unit = w / a.nqb;
     const int qi = w % a.nqb;
-    const int qb = (MODE == 1) ? (a.nqb - 1 - qi) : qi;
+    const int qb = (MODE == 1 || MODE == 3) ? (a.nqb - 1 - qi) : qi;
     const int b = unit / (a.Hkv * hgroups);
     const int rem = unit % (a.Hkv * hgroups);
     const int kvh = rem / hgroups;
@@ -654,10 +710,61 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     const int off = a.diag_off;  // causal: key j visible to query i iff j <= i + off
     int kv_end = a.Skv;
     if (MODE == 1) kv_end = min(a.Skv, qb * BQ + BQ + off);
-    const int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;  // blocks the workgroup stages
+    int nkb = kv_end > 0 ? (kv_end + BKV - 1) / BKV : 0;  // blocks the workgroup stages
     int kv_end_w = a.Skv;
     if (MODE == 1) kv_end_w = min(a.Skv, q0 + WQ + off);
     const int nkw = kv_end_w > 0 ? (kv_end_w + BKV - 1) / BKV : 0;  // blocks this wave's rows see
+
+    // MODE 3 (byte mask, tile classes from mask_tile_class_kernel): the workgroup
+    // stages, in key order, only the blocks some of its 128 rows see; list
+    // position j holds block slist[j] and the four 32-row groups' classes, 2 bits
+    // each (0 none, 1 some, 3 all). K/V stages follow the position, not the block.
+    constexpr int LMAX = MODE == 3 ? PP_LIST_MAX : 1;
+    __shared__ uint16_t slist[LMAX];
+    __shared__ uint8_t scls[LMAX];
+    __shared__ int scnt[MODE == 3 ? 8 : 1];
+    if constexpr (MODE == 3) {
+        const int nrg = (a.Sq + 31) / 32;
+        int base = 0;
+        for (int c0 = 0; c0 < a.nkbt; c0 += 512) {
+            const int kb = c0 + wave * 64 + lane;
+            uint32_t packed = 0;
+            if (kb < a.nkbt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int rg = qb * 4 + i;
+                    if (rg < nrg) packed |= (uint32_t)a.tcls[(int64_t)rg * a.nkbt + kb] << (2 * i);
+                }
+            }
+            const uint64_t bal = __ballot(packed != 0u);
+            if (lane == 0) scnt[wave] = __popcll(bal);
+            __syncthreads();
+            int before = base, tot = 0;
+#pragma unroll
+            for (int w2 = 0; w2 < 8; ++w2) {
+                before += w2 < wave ? scnt[w2] : 0;
+                tot += scnt[w2];
+            }
+            if (packed != 0u) {
+                const int pos = before + __popcll(bal & ((1ull << lane) - 1ull));
+                slist[pos] = (uint16_t)kb;
+                scls[pos] = (uint8_t)packed;
+            }
+            base += tot;
+            __syncthreads();  // the list is complete; scnt free for the next chunk
+        }
+        nkb = base;
+    }
+    auto kblock = [&](int j) -> int {
+        if constexpr (MODE == 3) return slist[j];
+        else return j;
+    };
+    // this wave's 32 rows: the class of position j (MODE 3), whether they see it
+    auto wcls = [&](int j) -> int { return (scls[MODE == 3 ? j : 0] >> (2 * (wave & 3))) & 3; };
+    auto wsees = [&](int j) -> bool {
+        if constexpr (MODE == 3) return j < nkb && wcls(j) != 0;
+        else return j < nkw;
+    };
 
     constexpr float LAZY = 8.0f;
     constexpr uint32_t ONE2 = std::is_same_v<T, BF16> ? 0x3F803F80u : 0x3C003C00u;
@@ -689,9 +796,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
         voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
     }
     // rows past the end re-read the last key (their scores are masked)
-    auto issue_k = [&](int kb) {
-        const int k0 = kb * BKV;
-        u32x4* dK = sK + (kb & 1) * STG;
+    auto issue_k = [&](int j) {
+        const int k0 = kblock(j) * BKV;
+        u32x4* dK = sK + (j & 1) * STG;
         const raw* kbase = Kp + (int64_t)k0 * a.ks2;
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
@@ -699,9 +806,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
             dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * GT + gw * 64]);
         }
     };
-    auto issue_v = [&](int kb) {
-        const int k0 = kb * BKV;
-        u32x4* dV = sV + (kb & 1) * STG;
+    auto issue_v = [&](int j) {
+        const int k0 = kblock(j) * BKV;
+        u32x4* dV = sV + (j & 1) * STG;
         const raw* vbase = Vp + (int64_t)k0 * a.vs2;
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
@@ -785,9 +892,39 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     // lazy reference point (set by the first visible block, moved only when a
     // block max exceeds it by more than LAZY in log2 units, O and l rescaled
     // then), p = exp2(s - m) packed to T.
-    auto sphase = [&](int kb) {
-        const int k0 = kb * BKV;
-        const bool msk = (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off);
+    auto sphase = [&](int j) {
+        const int k0 = kblock(j) * BKV;
+        const bool mixed = MODE == 3 && wcls(j) == 1;  // some but not all of the tile visible
+        const bool msk = (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off) || mixed;
+        // MODE 3, mixed tile: the mask bytes of this lane's 4 keys per 16-key
+        // tile (rows past Sq see nothing), read straight from the mask
+        uint32_t mw[QT][NKT];
+        if constexpr (MODE == 3) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) mw[qt][kt] = 0xffffffffu;
+            if (mixed) {
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) {
+                    const int qa = q0 + qt * 16 + l16;
+                    const uint8_t* mr = a.mask + (int64_t)(qa < a.Sq ? qa : 0) * a.mask_ld;
+#pragma unroll
+                    for (int kt = 0; kt < NKT; ++kt) {
+                        const int key0 = k0 + kt * 16 + g * 4;
+                        uint32_t w4 = 0u;
+                        if (key0 + 4 <= a.Skv) {
+                            w4 = *reinterpret_cast<const uint32_t*>(mr + key0);
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (key0 + r < a.Skv && mr[key0 + r] != 0) w4 |= 0xffu << (8 * r);
+                        }
+                        mw[qt][kt] = qa < a.Sq ? w4 : 0u;
+                    }
+                }
+            }
+        }
         float lmax[QT];
         bool trig = false;
 #pragma unroll
@@ -801,6 +938,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                         const int key = k0 + kt * 16 + g * 4 + r;
                         bool vis = key < a.Skv;
                         if (MODE == 1) vis = vis && (key <= qa + off);
+                        if constexpr (MODE == 3) vis = vis && ((mw[qt][kt] >> (8 * r)) & 0xffu) != 0u;
                         s[qt][kt][r] = vis ? s[qt][kt][r] : -INFINITY;
                     }
             }
@@ -865,20 +1003,20 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     __builtin_amdgcn_s_barrier();
     if (!grpB) {
         for (int j = 0; j <= nkb; ++j) {
-            mphase(j - 1, j >= 1 && j - 1 < nkw, j, j < nkw);
+            mphase(j - 1, j >= 1 && wsees(j - 1), j, wsees(j));
             __builtin_amdgcn_s_waitcnt(0);
             __builtin_amdgcn_s_barrier();
             if (j < nkb) issue_v(j);
-            if (j < nkw) sphase(j);
+            if (wsees(j)) sphase(j);
             __builtin_amdgcn_s_waitcnt(0);  // this wave's V(j) DMA has landed
             __builtin_amdgcn_s_barrier();
         }
     } else {
         for (int j = 0; j <= nkb; ++j) {
             if (j + 1 < nkb) issue_k(j + 1);
-            if (j >= 1 && j - 1 < nkw) sphase(j - 1);
+            if (j >= 1 && wsees(j - 1)) sphase(j - 1);
             __builtin_amdgcn_s_barrier();
-            mphase(j - 1, j >= 1 && j - 1 < nkw, j, j < nkw);
+            mphase(j - 1, j >= 1 && wsees(j - 1), j, wsees(j));
             __builtin_amdgcn_s_waitcnt(0);  // this wave's K(j+1) DMA has landed
             __builtin_amdgcn_s_barrier();
         }
@@ -1476,6 +1614,16 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     // 128-key blocks K, V and the two mask tiles fill all 160 KB and the kernel
     // spills registers (measured slower).
     if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) {
+        if (mode == 3 && a.tcls != nullptr) {
+            // the mask's tile classes first, then the ping-pong kernel over the
+            // blocks each workgroup's rows see (S=8192 causal bytes: 396 -> 2xx us)
+            dim3 cgrid((a.Sq + 31) / 32, (a.nkbt + 15) / 16);
+            mask_tile_class_kernel<<<cgrid, 256, 0, s>>>(a.mask, a.mask_ld, a.Sq, a.Skv, a.nkbt, a.tcls);
+            a.nqb = (a.Sq + 127) / 128;
+            dim3 grid(a.nqb * a.B * a.Hq / 2);
+            attn_fwd_pingpong<T, D, 3><<<grid, 512, 0, s>>>(a);
+            return hipGetLastError();
+        }
         if (mode == 3) return launch_prefill_gh<T, D, 2, 2, 4>(a, mode, s);
         if (mode == 0 || mode == 1) {
             a.nqb = (a.Sq + 127) / 128;
@@ -1595,11 +1743,32 @@ using namespace ythip;
 
 extern "C" {
 
+__attribute__((visibility("default"))) size_t ythip_attn_prefill_workspace_size(int q_len, int kv_len) {
+    if (q_len <= 0 || kv_len <= 0) return 0;
+    const size_t bytes = (size_t)((q_len + 31) / 32) * (size_t)((kv_len + 63) / 64);
+    return (bytes + 255) / 256 * 256;
+}
+
+__attribute__((visibility("default"))) int ythip_attn_prefill_ws(
+    int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv, const void* Q, const int64_t q_str[4],
+    const void* K, const int64_t k_str[4], const void* V, const int64_t v_str[4], void* O, const int64_t o_str[4],
+    float scale, int mask_kind, const uint8_t* mask, int64_t mask_ld, const float* bias, int64_t rs_bias,
+    int64_t cs_bias, void* workspace, size_t ws_bytes, void* stream);
+
 __attribute__((visibility("default"))) int ythip_attn_prefill(
     int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv, const void* Q, const int64_t q_str[4],
     const void* K, const int64_t k_str[4], const void* V, const int64_t v_str[4], void* O, const int64_t o_str[4],
     float scale, int mask_kind, const uint8_t* mask, int64_t mask_ld, const float* bias, int64_t rs_bias,
     int64_t cs_bias, void* stream) {
+    return ythip_attn_prefill_ws(dtype, B, Hq, Hkv, q_len, kv_len, d, dv, Q, q_str, K, k_str, V, v_str, O, o_str,
+                                 scale, mask_kind, mask, mask_ld, bias, rs_bias, cs_bias, nullptr, 0, stream);
+}
+
+__attribute__((visibility("default"))) int ythip_attn_prefill_ws(
+    int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv, const void* Q, const int64_t q_str[4],
+    const void* K, const int64_t k_str[4], const void* V, const int64_t v_str[4], void* O, const int64_t o_str[4],
+    float scale, int mask_kind, const uint8_t* mask, int64_t mask_ld, const float* bias, int64_t rs_bias,
+    int64_t cs_bias, void* workspace, size_t ws_bytes, void* stream) {
     if (B < 0 || Hq < 0 || Hkv < 0 || q_len < 0 || kv_len < 0 || d < 0 || dv < 0)
         return fail(YTHIP_EINVAL, "ythip_attn_prefill: negative size");
     if ((int64_t)B * Hq * q_len == 0 || dv == 0) return 0;
@@ -1630,6 +1799,17 @@ __attribute__((visibility("default"))) int ythip_attn_prefill(
     a.mask = mask_kind == YTHIP_MASK_BOOL ? mask : nullptr;
     a.mask_ld = mask_ld;
     a.bias = bias; a.brs = rs_bias; a.bcs = cs_bias;
+    if (workspace != nullptr && mask_kind == YTHIP_MASK_BOOL && kv_len > 0) {
+        // room for the mask's tile classes: the long-sequence paired-head path
+        // then runs the ping-pong kernel over listed blocks
+        const size_t need = ythip_attn_prefill_workspace_size(q_len, kv_len);
+        if (ws_bytes < need)
+            return fail(YTHIP_EINVAL, "ythip_attn_prefill_ws: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+        if ((kv_len + 63) / 64 <= PP_LIST_MAX) {
+            a.tcls = static_cast<uint8_t*>(workspace);
+            a.nkbt = (kv_len + 63) / 64;
+        }
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (kv_len == 0) {
         // No key at all: every row is fully masked -> zeros (flash_attention.inl:241-244).

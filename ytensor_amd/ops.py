@@ -223,8 +223,11 @@ def scaled_dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
     visible) or a predicate f(i, j) -> bool (evaluated into a bool mask here).
     bias: optional float32 [Sq, Skv] added after scaling. Rows with no visible
     key come out zero. backend: "flash" (FLASH_AVX2's counterpart, online
-    softmax, no score matrix) or "math" (MATH: materialised scores in a
-    workspace of ythip_attn_math_workspace_size bytes, allocated if not given).
+    softmax, no score matrix; with a bool mask, a workspace of
+    ythip_attn_prefill_workspace_size bytes for the mask's tile classes) or
+    "math" (MATH: materialised scores in a workspace of
+    ythip_attn_math_workspace_size bytes). A workspace not given or too small
+    is allocated.
     """
     _dev(q, k, v)
     if backend not in ("flash", "math"):
@@ -271,6 +274,18 @@ def scaled_dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
                 vt.data_ptr(), i64array(vs), ot.data_ptr(), i64array(os_), float(scale), kind, mptr, mld,
                 bptr, brs, bcs, ws.data_ptr(), ws.numel() * ws.element_size(), _stream())
             check(st, "ythip_attn_math")
+        elif kind == _lib.MASK_BOOL:
+            # room for the mask's tile classes (the long-sequence path lists the
+            # key blocks each query block sees from them)
+            need = int(_lib.lib().ythip_attn_prefill_workspace_size(Sq, Skv))
+            ws = workspace
+            if ws is None or ws.numel() * ws.element_size() < need:
+                ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+            st = _lib.lib().ythip_attn_prefill_ws(
+                _code(q), B, Hq, Hkv, Sq, Skv, D, dv, qt.data_ptr(), i64array(qs), kt.data_ptr(), i64array(ks),
+                vt.data_ptr(), i64array(vs), ot.data_ptr(), i64array(os_), float(scale), kind, mptr, mld,
+                bptr, brs, bcs, ws.data_ptr(), ws.numel() * ws.element_size(), _stream())
+            check(st, "ythip_attn_prefill_ws")
         else:
             st = _lib.lib().ythip_attn_prefill(
                 _code(q), B, Hq, Hkv, Sq, Skv, D, dv, qt.data_ptr(), i64array(qs), kt.data_ptr(), i64array(ks),
