@@ -688,6 +688,22 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     const raw* Kp = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1;
     const raw* Vp = static_cast<const raw*>(a.V) + b * a.vs0 + kvh * a.vs1;
 
+    // MODE 3: the four 32-row groups' tile classes of key block kb, 2 bits each
+    // (issued before the Q loads so that the two latencies overlap)
+    auto tile_classes = [&](int kb) -> uint32_t {
+        uint32_t packed = 0;
+        if (kb < a.nkbt) {
+            const int nrg = (a.Sq + 31) / 32;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rg = qb * 4 + i;
+                if (rg < nrg) packed |= (uint32_t)a.tcls[(int64_t)rg * a.nkbt + kb] << (2 * i);
+            }
+        }
+        return packed;
+    };
+    const uint32_t packed0 = MODE == 3 ? tile_classes(wave * 64 + lane) : 0u;
+
     // Q pre-scaled by scale*log2(e) and rounded back to T, as in attn_fwd_mfma
     const float c = a.scale_log2;
     u32x4 qf[QT][KS];
@@ -720,22 +736,13 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     // position j holds block slist[j] and the four 32-row groups' classes, 2 bits
     // each (0 none, 1 some, 3 all). K/V stages follow the position, not the block.
     constexpr int LMAX = MODE == 3 ? PP_LIST_MAX : 1;
-    __shared__ uint16_t slist[LMAX];
-    __shared__ uint8_t scls[LMAX];
+    __shared__ uint32_t slist[LMAX];  // block | classes << 16
     __shared__ int scnt[MODE == 3 ? 8 : 1];
     if constexpr (MODE == 3) {
-        const int nrg = (a.Sq + 31) / 32;
         int base = 0;
         for (int c0 = 0; c0 < a.nkbt; c0 += 512) {
             const int kb = c0 + wave * 64 + lane;
-            uint32_t packed = 0;
-            if (kb < a.nkbt) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int rg = qb * 4 + i;
-                    if (rg < nrg) packed |= (uint32_t)a.tcls[(int64_t)rg * a.nkbt + kb] << (2 * i);
-                }
-            }
+            const uint32_t packed = c0 == 0 ? packed0 : tile_classes(kb);
             const uint64_t bal = __ballot(packed != 0u);
             if (lane == 0) scnt[wave] = __popcll(bal);
             __syncthreads();
@@ -747,23 +754,29 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
             }
             if (packed != 0u) {
                 const int pos = before + __popcll(bal & ((1ull << lane) - 1ull));
-                slist[pos] = (uint16_t)kb;
-                scls[pos] = (uint8_t)packed;
+                slist[pos] = (uint32_t)kb | (packed << 16);
             }
             base += tot;
             __syncthreads();  // the list is complete; scnt free for the next chunk
         }
         nkb = base;
     }
-    auto kblock = [&](int j) -> int {
-        if constexpr (MODE == 3) return slist[j];
+    // List entry of position j (MODE 3: block | classes << 16; otherwise block j),
+    // read from LDS one step before the loop needs it.
+    auto entry_v = [&](int j) -> uint32_t {  // the LDS read (per lane)
+        if constexpr (MODE == 3) return (j < nkb) ? slist[j] : 0u;
+        else return 0u;
+    };
+    auto entry = [&](int j) -> uint32_t { return __builtin_amdgcn_readfirstlane(entry_v(j)); };
+    auto kblock = [&](int j, uint32_t e) -> int {
+        if constexpr (MODE == 3) return (int)(e & 0xffffu);
         else return j;
     };
-    // this wave's 32 rows: the class of position j (MODE 3), whether they see it
-    auto wcls = [&](int j) -> int { return (scls[MODE == 3 ? j : 0] >> (2 * (wave & 3))) & 3; };
-    auto wsees = [&](int j) -> bool {
-        if constexpr (MODE == 3) return j < nkb && wcls(j) != 0;
-        else return j < nkw;
+    // this wave's 32 rows: the class of an entry (MODE 3), whether they see position j
+    auto wcls = [&](uint32_t e) -> int { return (int)((e >> (16 + 2 * (wave & 3))) & 3u); };
+    auto wsees = [&](int j, uint32_t e) -> bool {
+        if constexpr (MODE == 3) return j >= 0 && j < nkb && wcls(e) != 0;
+        else return j >= 0 && j < nkw;
     };
 
     constexpr float LAZY = 8.0f;
@@ -796,8 +809,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
         voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
     }
     // rows past the end re-read the last key (their scores are masked)
-    auto issue_k = [&](int j) {
-        const int k0 = kblock(j) * BKV;
+    auto issue_k = [&](int j, uint32_t e) {
+        const int k0 = kblock(j, e) * BKV;
         u32x4* dK = sK + (j & 1) * STG;
         const raw* kbase = Kp + (int64_t)k0 * a.ks2;
 #pragma unroll
@@ -806,8 +819,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
             dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * GT + gw * 64]);
         }
     };
-    auto issue_v = [&](int j) {
-        const int k0 = kblock(j) * BKV;
+    auto issue_v = [&](int j, uint32_t e) {
+        const int k0 = kblock(j, e) * BKV;
         u32x4* dV = sV + (j & 1) * STG;
         const raw* vbase = Vp + (int64_t)k0 * a.vs2;
 #pragma unroll
@@ -892,37 +905,36 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     // lazy reference point (set by the first visible block, moved only when a
     // block max exceeds it by more than LAZY in log2 units, O and l rescaled
     // then), p = exp2(s - m) packed to T.
-    auto sphase = [&](int j) {
-        const int k0 = kblock(j) * BKV;
-        const bool mixed = MODE == 3 && wcls(j) == 1;  // some but not all of the tile visible
-        const bool msk = (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off) || mixed;
-        // MODE 3, mixed tile: the mask bytes of this lane's 4 keys per 16-key
-        // tile (rows past Sq see nothing), read straight from the mask
-        uint32_t mw[QT][NKT];
+    // MODE 3, a mixed tile (some but not all of it visible to the wave's rows):
+    // its 32 x 64 mask bytes reach the wave's own LDS slot (row-major) by DMA,
+    // issued with the DMA of the step before the wave's next S phase, so the
+    // step-end wait covers it. kv_len % 16 == 0 on this path: a 16-byte piece
+    // is wholly below kv_len or wholly past it (those re-read key 0 and are
+    // masked by index); rows past Sq re-read the last row (never stored).
+    __shared__ u32x4 smask[MODE == 3 ? 8 * 128 : 1];
+    auto load_mw = [&](int j, uint32_t e) {
         if constexpr (MODE == 3) {
+            if (!(wsees(j, e) && wcls(e) == 1)) return;
+            const int kp = kblock(j, e) * BKV + 16 * (lane & 3);
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-                for (int kt = 0; kt < NKT; ++kt) mw[qt][kt] = 0xffffffffu;
+            for (int i = 0; i < 2; ++i) {
+                const int row = min(q0 + 16 * i + (lane >> 2), a.Sq - 1);
+                dma16_async(a.mask + (int64_t)row * a.mask_ld + (kp < a.Skv ? kp : 0), &smask[wave * 128 + i * 64]);
+            }
+        }
+    };
+    auto sphase = [&](int j, uint32_t e) {
+        const int k0 = kblock(j, e) * BKV;
+        const bool mixed = MODE == 3 && wcls(e) == 1;
+        const bool msk = (k0 + BKV > a.Skv) || (MODE == 1 && k0 + BKV - 1 > q0 + off) || mixed;
+        uint32_t mw[QT][NKT];  // this lane's 4 mask bytes per 16-key tile
+        if constexpr (MODE == 3) {
             if (mixed) {
+                const uint32_t* sm = reinterpret_cast<const uint32_t*>(&smask[wave * 128]);
 #pragma unroll
-                for (int qt = 0; qt < QT; ++qt) {
-                    const int qa = q0 + qt * 16 + l16;
-                    const uint8_t* mr = a.mask + (int64_t)(qa < a.Sq ? qa : 0) * a.mask_ld;
+                for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-                    for (int kt = 0; kt < NKT; ++kt) {
-                        const int key0 = k0 + kt * 16 + g * 4;
-                        uint32_t w4 = 0u;
-                        if (key0 + 4 <= a.Skv) {
-                            w4 = *reinterpret_cast<const uint32_t*>(mr + key0);
-                        } else {
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                if (key0 + r < a.Skv && mr[key0 + r] != 0) w4 |= 0xffu << (8 * r);
-                        }
-                        mw[qt][kt] = qa < a.Sq ? w4 : 0u;
-                    }
-                }
+                    for (int kt = 0; kt < NKT; ++kt) mw[qt][kt] = sm[(qt * 16 + l16) * 16 + kt * 4 + g];
             }
         }
         float lmax[QT];
@@ -938,7 +950,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                         const int key = k0 + kt * 16 + g * 4 + r;
                         bool vis = key < a.Skv;
                         if (MODE == 1) vis = vis && (key <= qa + off);
-                        if constexpr (MODE == 3) vis = vis && ((mw[qt][kt] >> (8 * r)) & 0xffu) != 0u;
+                        if constexpr (MODE == 3) vis = vis && (!mixed || ((mw[qt][kt] >> (8 * r)) & 0xffu) != 0u);
                         s[qt][kt][r] = vis ? s[qt][kt][r] : -INFINITY;
                     }
             }
@@ -998,27 +1010,42 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     // held K(j-1) and the V stage A fills held V(j-2), both last read in
     // phases 2j-2 and 2j-1. Every wave passes 2 (nkb + 1) + 1 barriers; K(0) is
     // staged by group A before the first one.
-    if (nkb > 0 && !grpB) issue_k(0);
+    // em, e0, ep: the entries of positions j - 1, j, j + 1 (MODE 3)
+    uint32_t em = 0u, e0 = entry(0), ep = entry(1);
+    if (nkb > 0 && !grpB) issue_k(0, e0);
+    if (!grpB) load_mw(0, e0);
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_s_barrier();
+    // The entry of position j + 2 is read in step j and made scalar after the
+    // step-end wait, so the read never stalls the step.
     if (!grpB) {
         for (int j = 0; j <= nkb; ++j) {
-            mphase(j - 1, j >= 1 && wsees(j - 1), j, wsees(j));
+            mphase(j - 1, wsees(j - 1, em), j, wsees(j, e0));
             __builtin_amdgcn_s_waitcnt(0);
             __builtin_amdgcn_s_barrier();
-            if (j < nkb) issue_v(j);
-            if (wsees(j)) sphase(j);
+            const uint32_t en = entry_v(j + 2);
+            if (j < nkb) issue_v(j, e0);
+            if (wsees(j, e0)) sphase(j, e0);
+            load_mw(j + 1, ep);
             __builtin_amdgcn_s_waitcnt(0);  // this wave's V(j) DMA has landed
             __builtin_amdgcn_s_barrier();
+            em = e0;
+            e0 = ep;
+            ep = __builtin_amdgcn_readfirstlane(en);
         }
     } else {
         for (int j = 0; j <= nkb; ++j) {
-            if (j + 1 < nkb) issue_k(j + 1);
-            if (j >= 1 && wsees(j - 1)) sphase(j - 1);
+            if (j + 1 < nkb) issue_k(j + 1, ep);
+            const uint32_t en = entry_v(j + 2);
+            if (wsees(j - 1, em)) sphase(j - 1, em);
+            load_mw(j, e0);
             __builtin_amdgcn_s_barrier();
-            mphase(j - 1, j >= 1 && wsees(j - 1), j, wsees(j));
+            mphase(j - 1, wsees(j - 1, em), j, wsees(j, e0));
             __builtin_amdgcn_s_waitcnt(0);  // this wave's K(j+1) DMA has landed
             __builtin_amdgcn_s_barrier();
+            em = e0;
+            e0 = ep;
+            ep = __builtin_amdgcn_readfirstlane(en);
         }
     }
 
@@ -1614,7 +1641,7 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     // 128-key blocks K, V and the two mask tiles fill all 160 KB and the kernel
     // spills registers (measured slower).
     if ((a.Hq / a.Hkv) % 2 == 0 && paired >= 512) {
-        if (mode == 3 && a.tcls != nullptr) {
+        if (mode == 3 && a.tcls != nullptr && a.Skv % 16 == 0) {
             // the mask's tile classes first, then the ping-pong kernel over the
             // blocks each workgroup's rows see (S=8192 causal bytes: 396 -> 2xx us)
             dim3 cgrid((a.Sq + 31) / 32, (a.nkbt + 15) / 16);
