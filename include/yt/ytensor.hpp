@@ -780,6 +780,23 @@ YTensor<T, dim> _sdpa_hip(YTensor<T, dim>& query, YTensor<T, dim>& key, YTensor<
                        "yt::function::scaledDotProductAttention(decode)");
             return;
         }
+        if (mask_kind == YTHIP_MASK_BOOL) {
+            // A bool mask is classified tile by tile into a workspace first (long
+            // prompts then stage only the key blocks each query block sees). The
+            // allocation is stream-ordered, so calls on different streams never
+            // share it; without that allocator the call runs without one.
+            const size_t need = ythip_attn_prefill_workspace_size(Lq, Lkv);
+            void* ws = nullptr;
+            if (need && hipMallocAsync(&ws, need, hip::stream()) == hipSuccess) {
+                const int st = ythip_attn_prefill_ws(code, f.batch, f.heads_q, f.heads_kv, Lq, Lkv, D, Dv, q, qstr, k,
+                                                     kstr, v, vstr, o, ostr, sc, mask_kind, mp, mask_ld, bp, brs, bcs,
+                                                     ws, need, hip::stream());
+                (void)hipFreeAsync(ws, hip::stream());
+                hip::check(st, "yt::function::scaledDotProductAttention");
+                return;
+            }
+            (void)hipGetLastError();
+        }
         hip::check(ythip_attn_prefill(code, f.batch, f.heads_q, f.heads_kv, Lq, Lkv, D, Dv, q, qstr, k, kstr, v, vstr,
                                       o, ostr, sc, mask_kind, mp, mask_ld, bp, brs, bcs, hip::stream()),
                    "yt::function::scaledDotProductAttention");
