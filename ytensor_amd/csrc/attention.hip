@@ -678,7 +678,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     const int b = unit / (a.Hkv * hgroups);
     const int rem = unit % (a.Hkv * hgroups);
     const int kvh = rem / hgroups;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index made scalar: every per-wave test (rows seen, tile class)
+    // is then a scalar branch, not an exec-mask one
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool grpB = wave >= 4;
     const int h = kvh * G + (rem % hgroups) * 2 + (wave >> 2);
     const int l16 = lane & 15, g = lane >> 4;
