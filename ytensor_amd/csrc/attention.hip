@@ -154,7 +154,8 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
     const int b = unit / (a.Hkv * hgroups);
     const int rem = unit % (a.Hkv * hgroups);
     const int kvh = rem / hgroups;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index made scalar: per-wave tests are then scalar branches
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = KSPLIT == 2 ? (wave >> 2) : 0;  // key half of each stage
     const int h = kvh * G + (rem % hgroups) * GH + (KSPLIT == 1 ? (wave >> 2) : 0);
     const int l16 = lane & 15, g = lane >> 4;
