@@ -134,7 +134,7 @@ struct GemvPrologue {
     }
 
     __device__ __forceinline__ void build(const GemvArgs& a, int bz, raw* sAp) {
-        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, total = a.m * a.k;
+        const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), total = a.m * a.k;
         if constexpr (PRO == 1) {
             __shared__ float s_part[GEMV_M][4];
             __shared__ float s_den[GEMV_M];
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     constexpr int UNR = 8;
     static_assert(PRO == 0 || sizeof(raw) == 2, "fused prologues are 16-bit");
     static_assert(EPI == 0 || PRO <= 1, "the SwiGLU epilogue takes prologue 0 or 1");
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar
     const int r = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.x * (EPI ? 8 : 16);
     const int bz = blockIdx.y;
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_row_kernel(GemvArgs a) {
     static_assert(PRO == 0 || sizeof(raw) == 2, "fused prologues are 16-bit");
     static_assert(EPI == 0 || (RPW == 2 && PRO <= 1), "the SwiGLU epilogue pairs a gate and an up row");
     static_assert(PRO == 0 || WAVES >= 4, "the RMSNorm prologue reduces on 256 threads");
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar
     const int nch = a.k / VEC;
     int rows[RPW];
     bool rok[RPW];
