@@ -74,7 +74,9 @@ def test_config2_bf16_sweep(orc, yt, shape, layout):
 
 
 SMALL = [(7, 13, 5), (37, 41, 1001), (64, 64, 64), (130, 260, 96), (1, 33, 72), (5, 1, 40), (256, 512, 128),
-         (300, 200, 64), (2, 2, 2), (17, 520, 1024), (100, 272, 128), (1, 4096, 512), (513, 1040, 192), (16, 200, 256), (9, 3000, 3072)]
+         (300, 200, 64), (2, 2, 2), (17, 520, 1024), (100, 272, 128), (1, 4096, 512), (513, 1040, 192), (16, 200, 256), (9, 3000, 3072),
+         # 2..16 rows, 16-bit NN with aligned rows: one partial 64-row tile on the MFMA DMA path
+         (16, 3072, 1024), (2, 48, 64), (9, 3008, 192)]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
@@ -150,7 +152,7 @@ def test_batched_and_alpha_beta(orc, yt, dtype):
 
 # Grids with fewer 64 x 64 tiles than CUs take 64 x 32 tiles (two waves per
 # workgroup); (1000, 1000, 2048) x 2 batches stays on 64 x 64.
-SHORT_GRID_SHAPES = [(130, 200, 512), (96, 192, 1024), (64, 100, 256), (1000, 1000, 2048)]
+SHORT_GRID_SHAPES = [(130, 200, 512), (96, 192, 1024), (64, 100, 256), (1000, 1000, 2048), (12, 208, 512)]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])

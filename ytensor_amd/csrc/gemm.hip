@@ -739,7 +739,7 @@ constexpr int SKINNY_WAVES = 8;
 template <class T, class TO>
 __global__ __launch_bounds__(64 * SKINNY_WAVES) void gemm_skinny_nn_kernel(GemmArgs a) {
     using raw = typename T::raw;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = blockIdx.x * 64 + lane;
     const int bz = blockIdx.y;
     const raw* __restrict__ Ap = static_cast<const raw*>(a.A) + bz * a.sa_b;
@@ -800,7 +800,7 @@ template <class T, class TO, int CPR>
 __global__ __launch_bounds__(1024) void gemv_nn_kernel(GemmArgs a) {
     using raw = typename T::raw;
     constexpr int VEC = 16 / sizeof(raw), WAVES = 16, UNR = 8, RPI = 64 / CPR;  // k-rows per load
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane % CPR, r = lane / CPR;
     // column tiles t..t+T/8-1 on one XCD (workgroups are dealt to the 8 XCDs
     // round-robin): tiles narrower than a 128-byte line share its fetch in one L2
@@ -1071,6 +1071,13 @@ int gemm_typed(int batch, int m, int n, int k, const void* A, int64_t sa_b, int6
                     gemv_nn_kernel<T, TO, 2><<<dim3((n + 2 * VEC - 1) / (2 * VEC), batch), 1024, 0, s>>>(g);
                 return status_of(hipGetLastError());
             }
+            // 2..16 rows of a row-major, 16-bit B: the MFMA DMA path (one partial
+            // 64-row tile per column tile) streams B at full width; the column-per-
+            // lane kernel below re-reads A per k and issues 2-byte loads of B
+            // ((16, 3072, 1024): ~100 us there)
+            if (es == 2 && (k % (8 * VEC)) == 0 && (rsb % VEC) == 0 && (sb_b % VEC) == 0 && (n % 16) == 0 &&
+                aligned(B, 16))
+                return status_of(launch_dma<T, TO>(g, true, batch, s));
             gemm_skinny_nn_kernel<T, TO><<<dim3((n + 63) / 64, batch), 64 * SKINNY_WAVES, 0, s>>>(g);
             return status_of(hipGetLastError());
         }
