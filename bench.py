@@ -573,6 +573,32 @@ def main() -> int:
             del nxt
             torch.cuda.empty_cache()
         sections["attn_decode_bf16"] = dec
+        # The reference Qwen3's per-token call form (qwen3.cpp:250-264):
+        # scaledDotProductAttention with q_len == 1 and KVCache::get_mask's bool
+        # mask [1, ctx], which the library sends to the same split-K kernel
+        # (flash_attention.inl:469-499 routes every q_len == 1 call to decode).
+        dec_m = []
+        for (Bq, ctx) in [(1, 1024), (1, 8192), (16, 1024), (16, 8192)]:
+            byts = 2.0 * Bq * 8 * ctx * 128 * 2
+            nb = min(64, max(1, int(math.ceil(600e6 / byts))))
+            mk = lambda i: (torch.randn(Bq, 16, 1, 128, device=dev).to(torch.bfloat16),
+                            torch.randn(Bq, 8, ctx, 128, device=dev).to(torch.bfloat16),
+                            torch.randn(Bq, 8, ctx, 128, device=dev).to(torch.bfloat16),
+                            torch.empty(Bq, 16, 1, 128, device=dev, dtype=torch.bfloat16))
+            nxt = rotating(nb, mk)
+            mask = torch.ones(1, ctx, device=dev, dtype=torch.bool)
+            ws = torch.empty(int(yt.lib().ythip_attn_sdpa_workspace_size(Bq, 16, 1, ctx, 128)), dtype=torch.uint8,
+                             device=dev)
+
+            def run():
+                q_, k_, v_, o_ = nxt()
+                ops.scaled_dot_product_attention(q_, k_, v_, 0.0, mask, out=o_, workspace=ws)
+            t = time_launches(run, max(args.steps, 20), args.warmup, torch)
+            dec_m.append({"B": Bq, "ctx": ctx, "ms": round(t, 5), "gbs": round(byts / t / 1e6, 1),
+                          "frac_hbm": round(byts / t / 1e6 / PEAK_HBM_GBS, 4), "rotating_buffers": nb})
+            del nxt
+            torch.cuda.empty_cache()
+        sections["attn_decode_sdpa_bool_mask_bf16"] = dec_m
 
     if want("norm") and not args.quick:
         S = 8192

@@ -26,7 +26,11 @@
 //
 // Streams. Every operator launches on yt::hip::stream() (a per-thread
 // hipStream_t, NULL by default; set it with yt::hip::StreamGuard), which it
-// passes to the C ABI call by call.
+// passes to the C ABI call by call. Device scratch (split-K partials of
+// single-query attention, a bool mask's tile classes, MATH scores) comes from
+// yt::hip::workspace(): one buffer per host thread and (device, stream), kept
+// and grown by the host, so operators on different threads or streams never
+// share one and operators on one stream reuse it in launch order.
 //
 // Errors. Argument problems raise std::invalid_argument, as the reference's
 // L3/L4 callers do (src/function/ops.inl:123-128, 382-387); a failing HIP call
@@ -51,6 +55,7 @@
 #include <cstring>
 #include <functional>
 #include <initializer_list>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <numeric>
@@ -127,6 +132,63 @@ inline void check(int status, const std::string& what) {
 
 inline void check(hipError_t e, const std::string& what) {
     if (e != hipSuccess) throw std::runtime_error(what + ": " + hipGetErrorString(e));
+}
+
+// Device scratch of the calling thread for the current device and stream,
+// at least `bytes` long (grown in 1 MiB steps; the old buffer is freed once
+// the stream has finished with it). Freed when the thread ends.
+struct ThreadWorkspaces {
+    struct Buf {
+        void* p = nullptr;
+        size_t bytes = 0;
+    };
+    std::map<std::pair<int, hipStream_t>, Buf> bufs;
+    ThreadWorkspaces() = default;
+    ThreadWorkspaces(const ThreadWorkspaces&) = delete;
+    ThreadWorkspaces& operator=(const ThreadWorkspaces&) = delete;
+    ~ThreadWorkspaces() {
+        for (auto& kv : bufs)
+            if (kv.second.p) (void)hipFree(kv.second.p);
+    }
+};
+
+inline ThreadWorkspaces& thread_workspaces() {
+    thread_local ThreadWorkspaces w;
+    return w;
+}
+
+inline void* workspace(size_t bytes) {
+    if (bytes == 0) return nullptr;
+    int dev = 0;
+    check(hipGetDevice(&dev), "yt: hipGetDevice");
+    auto& b = thread_workspaces().bufs[{dev, stream()}];
+    if (b.bytes < bytes) {
+        if (b.p) {
+            check(hipStreamSynchronize(stream()), "yt: workspace");
+            check(hipFree(b.p), "yt: hipFree (workspace)");
+            b.p = nullptr;
+            b.bytes = 0;
+        }
+        const size_t step = size_t(1) << 20, sz = (bytes + step - 1) / step * step;
+        check(hipMalloc(&b.p, sz), "yt: hipMalloc (workspace)");
+        b.bytes = sz;
+    }
+    return b.p;
+}
+
+// Frees the calling thread's workspace for the current device and stream
+// (for a stream about to be destroyed).
+inline void releaseWorkspace() {
+    int dev = 0;
+    check(hipGetDevice(&dev), "yt: hipGetDevice");
+    auto& m = thread_workspaces().bufs;
+    auto it = m.find({dev, stream()});
+    if (it == m.end()) return;
+    if (it->second.p) {
+        check(hipStreamSynchronize(stream()), "yt: workspace");
+        check(hipFree(it->second.p), "yt: hipFree (workspace)");
+    }
+    m.erase(it);
 }
 
 template <class T> constexpr int dtype_code() {
@@ -590,34 +652,135 @@ YTensor<T, dim> linear(const YTensor<T, dim>& x, const YTensor<T, 2>& weight, co
     return out;
 }
 
-// yt::function::rmsNorm_ over the last axis (src/function/normalization.inl:
-// 256-277): x <- x / sqrt(mean(x^2) + eps) * weight, in place, on the device.
+namespace detail_norm {
+
+// The reference's _normalizeAxes (src/ytensor_function.inl:60-82): negative
+// axes wrap, duplicates and an empty list are errors; the order is kept.
+template <int dim>
+std::vector<int> normalize_axes(const std::vector<int>& axes) {
+    if (axes.empty()) throw std::invalid_argument("yt::function: axes must not be empty");
+    std::vector<int> out;
+    std::vector<bool> used(dim, false);
+    for (int axis : axes) {
+        const int a = (axis % dim + dim) % dim;
+        if (used[a]) throw std::invalid_argument("yt::function: duplicate axes are not allowed");
+        used[a] = true;
+        out.push_back(a);
+    }
+    return out;
+}
+
+// Size and element stride of the dims `ax` (ascending) read as one axis, or
+// false when their strides do not nest (size-1 dims are ignored).
+inline bool fold_axes(const std::vector<int>& shape, const std::vector<int>& stride, const std::vector<int>& ax,
+                      int64_t& n, int64_t& cs) {
+    n = 1;
+    cs = 1;
+    int prev = -1;
+    for (int i = static_cast<int>(ax.size()) - 1; i >= 0; --i) {
+        const int a = ax[i];
+        n *= shape[a];
+        if (shape[a] == 1) continue;
+        if (prev < 0) cs = stride[a];
+        else if (static_cast<int64_t>(stride[a]) != static_cast<int64_t>(stride[prev]) * shape[prev]) return false;
+        prev = a;
+    }
+    return true;
+}
+
+// y <- x / sqrt(mean(x^2 over axes) + eps) * weight on the device (y may be x).
+// The weight's dims match x's along `axes` in the order given, its elements
+// read row-major over the axes in ascending order (_makeAffineView,
+// src/ytensor_function.inl:136-157). Normalised axes must be neighbouring dims
+// whose strides nest (one strided axis for the kernel); the other dims are rows.
+template <class T, int dim, int weightDim>
+void rms_norm_into(const YTensor<T, dim>& x, const YTensor<T, weightDim>& weight, const std::vector<int>& axes,
+                   float eps, YTensor<T, dim>& y, const std::string& name) {
+    const auto ax = normalize_axes<dim>(axes);
+    if (static_cast<int>(ax.size()) != weightDim)
+        throw std::invalid_argument(name + ": gamma dim must match axes size");
+    for (int i = 0; i < weightDim; ++i)
+        if (weight.shape(i) != x.shape(ax[i])) throw std::invalid_argument(name + ": gamma shape must match affine axes");
+    auto sorted = ax;
+    std::sort(sorted.begin(), sorted.end());
+    for (size_t i = 1; i < sorted.size(); ++i)
+        if (sorted[i] != sorted[i - 1] + 1)
+            throw std::invalid_argument(name + ": the normalised axes must be neighbouring dims on the GPU");
+    int64_t n = 0, csx = 1, csy = 1, ny = 0;
+    if (!fold_axes(x._shape, x._stride, sorted, n, csx) || !fold_axes(y._shape, y._stride, sorted, ny, csy))
+        throw std::invalid_argument(name + ": the normalised axes' strides must nest on the GPU");
+    if (x.size() == 0) return;
+    // the other dims are rows: all but the last looped, the last one launched
+    std::vector<int> lead;
+    std::vector<int64_t> sx, sy;
+    for (int d = 0; d < dim; ++d) {
+        if (std::binary_search(sorted.begin(), sorted.end(), d)) continue;
+        lead.push_back(x._shape[d]);
+        sx.push_back(x._stride[d]);
+        sy.push_back(y._stride[d]);
+    }
+    if (lead.empty()) {
+        lead = {1};
+        sx = {0};
+        sy = {0};
+    }
+    auto w = weight.contiguous();
+    const float* wp = reinterpret_cast<const float*>(w.deviceData());
+    const auto* xb = reinterpret_cast<const char*>(x.deviceData());
+    auto* yb = reinterpret_cast<char*>(y.deviceWrite());
+    const int rows = lead.back();
+    const int64_t es = static_cast<int64_t>(sizeof(T));
+    detail::for_outer(lead, {sx, sy}, [&](const std::vector<int64_t>& off) {
+        const void* xp = xb + off[0] * es;
+        void* yp = yb + off[1] * es;
+        const int64_t ldx = rows == 1 ? n : sx.back(), ldy = rows == 1 ? n : sy.back();
+        int st;
+        if (csx == 1 && csy == 1 && ldx >= n && ldy >= n)
+            st = ythip_rms_norm(YTHIP_F32, YTHIP_F32, rows, static_cast<int>(n), xp, ldx, wp, eps, yp, ldy,
+                                hip::stream());
+        else
+            st = ythip_rms_norm_strided(YTHIP_F32, YTHIP_F32, rows, static_cast<int>(n), xp, sx.back(), csx, wp, eps,
+                                        yp, sy.back(), csy, hip::stream());
+        hip::check(st, name);
+    });
+}
+
+}  // namespace detail_norm
+
+// yt::function::rmsNorm_ (include/function/normalization.hpp:76-89,
+// src/function/normalization.inl:256-277): x <- x / sqrt(mean(x^2) + eps) *
+// weight over `axes`, in place, on the device.
+template <class T, int dim, int weightDim>
+YTensor<T, dim>& rmsNorm_(YTensor<T, dim>& x, const YTensor<T, weightDim>& weight, const std::vector<int>& axes,
+                          T eps = static_cast<T>(1e-5)) {
+    static_assert(std::is_floating_point_v<T>, "T must be floating point type in yt::function::rmsNorm_()");
+    static_assert(std::is_same_v<T, float>, "yt::function::rmsNorm_ runs float on the GPU (no double kernel)");
+    detail_norm::rms_norm_into(x, weight, axes, static_cast<float>(eps), x, "yt::function::rmsNorm_");
+    return x;
+}
+
 template <class T, int dim, int weightDim>
 YTensor<T, dim>& rmsNorm_(YTensor<T, dim>& x, const YTensor<T, weightDim>& weight, int axis = -1,
                           T eps = static_cast<T>(1e-5)) {
+    return rmsNorm_(x, weight, std::vector<int>{axis}, eps);
+}
+
+// yt::function::rmsNorm (include/function/normalization.hpp:59-73,
+// src/function/normalization.inl:233-254): the same into a new tensor.
+template <class T, int dim, int weightDim>
+YTensor<T, dim> rmsNorm(const YTensor<T, dim>& x, const YTensor<T, weightDim>& weight, const std::vector<int>& axes,
+                        T eps = static_cast<T>(1e-5)) {
     static_assert(std::is_floating_point_v<T>, "T must be floating point type in yt::function::rmsNorm_()");
-    if (x._axis(axis) != dim - 1) throw std::invalid_argument("yt::function::rmsNorm_: only the last axis here");
-    const int n = x.shape(-1);
-    if (static_cast<int>(weight.size()) != n || x.stride_(-1) != 1)
-        throw std::invalid_argument("yt::function::rmsNorm_: weight size / last-axis stride");
-    auto w = weight.contiguous();
-    const float* wp = reinterpret_cast<const float*>(w.deviceData());
-    auto* base = reinterpret_cast<char*>(x.deviceWrite());
-    const int rows = dim >= 2 ? x.shape(-2) : 1;
-    const int64_t ld = dim >= 2 ? x.stride_(-2) : n;
-    std::vector<int> lead(x._shape.begin(), x._shape.end() - 1);
-    std::vector<int64_t> ls(x._stride.begin(), x._stride.end() - 1);
-    if (lead.empty()) {
-        lead = {1};
-        ls = {0};
-    }
-    detail::for_outer(lead, {ls}, [&](const std::vector<int64_t>& off) {
-        void* p = base + off[0] * static_cast<int64_t>(sizeof(T));
-        hip::check(ythip_rms_norm(YTHIP_F32, YTHIP_F32, rows, n, p, ld, wp, static_cast<float>(eps), p, ld,
-                                  hip::stream()),
-                   "yt::function::rmsNorm_");
-    });
-    return x;
+    static_assert(std::is_same_v<T, float>, "yt::function::rmsNorm runs float on the GPU (no double kernel)");
+    auto out = YTensor<T, dim>::deviceOutput(x.shape());
+    detail_norm::rms_norm_into(x, weight, axes, static_cast<float>(eps), out, "yt::function::rmsNorm_");
+    return out;
+}
+
+template <class T, int dim, int weightDim>
+YTensor<T, dim> rmsNorm(const YTensor<T, dim>& x, const YTensor<T, weightDim>& weight, int axis = -1,
+                        T eps = static_cast<T>(1e-5)) {
+    return rmsNorm(x, weight, std::vector<int>{axis}, eps);
 }
 
 namespace detail_sdpa {
@@ -754,51 +917,20 @@ YTensor<T, dim> _sdpa_hip(YTensor<T, dim>& query, YTensor<T, dim>& key, YTensor<
                       vstr[4] = {f.bv, f.hv, vs2, vs3}, ostr[4] = {f.bo, f.ho, os2, 1};
         if (backend == sdpaBackend::MATH) {
             const size_t need = ythip_attn_math_workspace_size(code, f.batch, f.heads_q, Lq, Lkv);
-            void* ws = nullptr;
-            if (need) hip::check(hipMalloc(&ws, need), "yt: hipMalloc");
-            const int st = ythip_attn_math(code, f.batch, f.heads_q, f.heads_kv, Lq, Lkv, D, Dv, q, qstr, k, kstr, v,
-                                           vstr, o, ostr, sc, mask_kind, mp, mask_ld, bp, brs, bcs, ws, need,
-                                           hip::stream());
-            if (ws) {
-                (void)hipStreamSynchronize(hip::stream());
-                (void)hipFree(ws);
-            }
-            hip::check(st, "yt::function::scaledDotProductAttention(MATH)");
+            hip::check(ythip_attn_math(code, f.batch, f.heads_q, f.heads_kv, Lq, Lkv, D, Dv, q, qstr, k, kstr, v,
+                                       vstr, o, ostr, sc, mask_kind, mp, mask_ld, bp, brs, bcs, hip::workspace(need),
+                                       need, hip::stream()),
+                       "yt::function::scaledDotProductAttention(MATH)");
             return;
         }
-        // One query row, every key visible: the split-K decode kernel
-        // (the q_len == 1 path, src/kernel/avx2/flash_attention.inl:202-272),
-        // its partials in the library's fixed scratch when they fit.
-        const bool decode = Lq == 1 && mask_kind == YTHIP_MASK_NONE && bias == nullptr && D == Dv && qs3 == 1 &&
-                            ks3 == 1 && vs3 == 1 && kstr[0] == vstr[0] && kstr[1] == vstr[1] && ks2 == vs2 &&
-                            (D == 64 || D == 128);
-        if (decode && ythip_attn_decode_workspace_size(f.batch, f.heads_q, Lkv, D) <=
-                          ythip_attn_decode_noalloc_max_bytes()) {
-            const int64_t q2[2] = {f.bq, f.hq}, kv3[3] = {f.bk, f.hk, ks2}, o2[2] = {f.bo, f.ho};
-            hip::check(ythip_attn_decode_noalloc(code, f.batch, f.heads_q, f.heads_kv, D, Lkv, q, q2, k, v, kv3,
-                                                 nullptr, o, o2, sc, hip::stream()),
-                       "yt::function::scaledDotProductAttention(decode)");
-            return;
-        }
-        if (mask_kind == YTHIP_MASK_BOOL) {
-            // A bool mask is classified tile by tile into a workspace first (long
-            // prompts then stage only the key blocks each query block sees). The
-            // allocation is stream-ordered, so calls on different streams never
-            // share it; without that allocator the call runs without one.
-            const size_t need = ythip_attn_prefill_workspace_size(Lq, Lkv);
-            void* ws = nullptr;
-            if (need && hipMallocAsync(&ws, need, hip::stream()) == hipSuccess) {
-                const int st = ythip_attn_prefill_ws(code, f.batch, f.heads_q, f.heads_kv, Lq, Lkv, D, Dv, q, qstr, k,
-                                                     kstr, v, vstr, o, ostr, sc, mask_kind, mp, mask_ld, bp, brs, bcs,
-                                                     ws, need, hip::stream());
-                (void)hipFreeAsync(ws, hip::stream());
-                hip::check(st, "yt::function::scaledDotProductAttention");
-                return;
-            }
-            (void)hipGetLastError();
-        }
-        hip::check(ythip_attn_prefill(code, f.batch, f.heads_q, f.heads_kv, Lq, Lkv, D, Dv, q, qstr, k, kstr, v, vstr,
-                                      o, ostr, sc, mask_kind, mp, mask_ld, bp, brs, bcs, hip::stream()),
+        // One query row runs the split-K decode kernel for every mask kind and
+        // bias (flash_attention's q_len == 1 branch, src/kernel/avx2/
+        // flash_attention.inl:469-499), its partials in this thread's workspace
+        // for the stream; a bool mask's tile classes use the same workspace.
+        const size_t need = ythip_attn_sdpa_workspace_size(f.batch, f.heads_q, Lq, Lkv, D);
+        hip::check(ythip_attn_prefill_ws(code, f.batch, f.heads_q, f.heads_kv, Lq, Lkv, D, Dv, q, qstr, k, kstr, v,
+                                         vstr, o, ostr, sc, mask_kind, mp, mask_ld, bp, brs, bcs,
+                                         hip::workspace(need), need, hip::stream()),
                    "yt::function::scaledDotProductAttention");
     });
     return out;

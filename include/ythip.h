@@ -95,6 +95,12 @@ int ythip_gemm(int dtype_in, int dtype_out, int batch, int m, int n, int k,
  * Replaces the per-(batch, head) loop of _scaledDotProductAttentionFlash
  * (src/function/ops.inl:109-234) over yt::kernel::avx2::flash_attention
  * (include/kernel/avx2/flash_attention.hpp:21-69). Supported: d == dv in {64, 128}.
+ * q_len == 1 (the reference's decode branch, src/kernel/avx2/flash_attention.inl:
+ * 469-499) runs the split-K decode kernel for every mask kind and bias when
+ * d == dv in {64, 128}, Hq / Hkv in {1, 2, 4, 8}, the head dim is contiguous
+ * and K / V rows are 16-byte aligned; without a workspace (this call) that is
+ * one split per (kv head, batch) -- ythip_attn_prefill_ws with
+ * ythip_attn_sdpa_workspace_size bytes runs the full split count.
  */
 int ythip_attn_prefill(int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv,
                        const void* Q, const int64_t q_str[4],
@@ -117,6 +123,14 @@ int ythip_attn_prefill(int dtype, int B, int Hq, int Hkv, int q_len, int kv_len,
  * library's addition, as for ythip_attn_math.
  */
 size_t ythip_attn_prefill_workspace_size(int q_len, int kv_len);
+/*
+ * Workspace for ythip_attn_prefill_ws that serves every call shape: the bool
+ * mask's tile classes, and for q_len == 1 the split-K partials of the decode
+ * kernel (ythip_attn_decode_workspace_size(B, Hq, kv_len, d)). A smaller
+ * workspace still works (fewer splits). Same replaced interface as
+ * ythip_attn_prefill; the workspace is this library's addition.
+ */
+size_t ythip_attn_sdpa_workspace_size(int B, int Hq, int q_len, int kv_len, int d);
 int ythip_attn_prefill_ws(int dtype, int B, int Hq, int Hkv, int q_len, int kv_len, int d, int dv,
                           const void* Q, const int64_t q_str[4],
                           const void* K, const int64_t k_str[4],
@@ -299,6 +313,19 @@ int ythip_rmsnorm_rope(int dtype, int B, int S, int Hq, int Hkv, int d,
  */
 int ythip_rms_norm(int dtype_in, int dtype_out, int rows, int n, const void* x, int64_t ld_x,
                    const float* w, float eps, void* y, int64_t ld_y, void* stream);
+
+/*
+ * ythip_rms_norm with element strides: element i of row r at x + r*ld_x +
+ * i*cs_x (y likewise), w fp32 [n] contiguous. Normalises over one axis of any
+ * stride -- rmsNorm / rmsNorm_ over an axis other than the last, or over
+ * several neighbouring axes whose strides nest (include/function/
+ * normalization.hpp:59-89, src/function/normalization.inl:33-54, 88-101,
+ * 233-277). Same arithmetic and bits as ythip_rms_norm. In place (x == y)
+ * needs one dtype and one layout.
+ */
+int ythip_rms_norm_strided(int dtype_in, int dtype_out, int rows, int n, const void* x, int64_t ld_x,
+                           int64_t cs_x, const float* w, float eps, void* y, int64_t ld_y, int64_t cs_y,
+                           void* stream);
 
 /*
  * SwiGLU over a fused gate_up projection (Qwen3MLP::forward,

@@ -338,6 +338,94 @@ def test_config4_decode_bf16(orc, yt, B, ctx):
     check16(orc, g.reshape(r.shape), r, "bf16", True, f"decode B={B} ctx={ctx}")
 
 
+def _per_head_flash(orc, Qh, Kh, Vh, mask, bias):
+    """The reference's flash_attention per (batch, head), q head h on kv head h // G."""
+    B, Hq = Qh.shape[:2]
+    G = Hq // Kh.shape[1]
+    out = np.zeros((B, Hq, Qh.shape[2], Vh.shape[3]), np.float32)
+    for b in range(B):
+        for h in range(Hq):
+            out[b, h] = orc.flash_attention(Qh[b, h], Kh[b, h // G], Vh[b, h // G],
+                                            1.0 / math.sqrt(Qh.shape[3]), mask, bias)
+    return out
+
+
+@pytest.mark.parametrize("kind", ["none", "causal", "bool_all", "bool_rand", "bias", "diag"])
+@pytest.mark.parametrize("B,ctx", [(1, 1024), (1, 8192), (16, 1024), (16, 8192)])
+def test_single_query_sdpa_every_mask_kind(orc, yt, B, ctx, kind):
+    """scaled_dot_product_attention with q_len == 1 -- the reference's per-token
+    call (flash_attention.inl:469-499 sends every mask kind to its decode path)
+    -- at configs[3]'s shapes: against the reference's flash_attention per head,
+    and, with every key visible, bit for bit the explicit decode entry point
+    (both run the split-K decode kernel with the same splits)."""
+    Q, K, V = _decode_inputs(orc, B, ctx)
+    Qd, Qh = make_input(orc, Q, "bf16")
+    Kd, Kh = make_input(orc, K, "bf16")
+    Vd, Vh = make_input(orc, V, "bf16")
+    rng = np.random.default_rng(ctx + B)
+    mask = bias = None
+    mnp = bnp = None
+    if kind == "causal":
+        mask = "causal"
+    elif kind == "bool_all":
+        mnp = np.ones((1, ctx), bool)
+        mask = torch.from_numpy(mnp).cuda()
+    elif kind == "bool_rand":
+        mnp = rng.random((1, ctx)) > 0.3
+        mask = torch.from_numpy(mnp).cuda()
+    elif kind == "bias":
+        bnp = rng.standard_normal((1, ctx)).astype(np.float32)
+        bias = torch.from_numpy(bnp).cuda()
+    elif kind == "diag":
+        mask = ("diag", ctx // 3)
+        mnp = np.arange(ctx)[None, :] <= ctx // 3
+    g = yt.scaled_dot_product_attention(Qd, Kd, Vd, 0.0, mask=mask, bias=bias)
+    if mnp is None and bnp is None:
+        r = orc.sdpa_gqa(Qh, Kh, Vh, 0.0, False)
+        ref_dec = yt.decode_attention(Qd, Kd, Vd)
+        assert torch.equal(g.view(torch.int16), ref_dec.view(torch.int16)), "routed != decode entry point bits"
+    else:
+        r = _per_head_flash(orc, Qh, Kh, Vh, mnp, bnp)
+    if kind == "bool_all":
+        ref_dec = yt.decode_attention(Qd, Kd, Vd)
+        assert torch.equal(g.view(torch.int16), ref_dec.view(torch.int16)), "all-true mask != unmasked bits"
+    check16(orc, host_f32(g).reshape(r.shape), r, "bf16", True, f"q_len=1 {kind} B={B} ctx={ctx}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_single_query_sdpa_strided_v_and_no_workspace(orc, yt, dtype):
+    """q_len == 1 with K and V of different layouts (V a [B,S,H,D] view), through
+    ythip_attn_prefill without a workspace (one split per kv head, written
+    straight to O) and with one; fully masked rows stay zero."""
+    B, Hq, Hkv, S, D = 2, 8, 2, 700, 64
+    rng = np.random.default_rng(31)
+    Q = rng.standard_normal((B, Hq, 1, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    V = rng.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, dtype)
+    Kd, Kh = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    Vd = Vd.permute(0, 2, 1, 3)
+    Vh = np.ascontiguousarray(Vh.transpose(0, 2, 1, 3))
+    m = rng.random((1, S)) > 0.5
+    r = _per_head_flash(orc, Qh, Kh, Vh, m, None)
+    md = torch.from_numpy(m.astype(np.uint8)).cuda()
+    g1 = yt.scaled_dot_product_attention(Qd, Kd, Vd, 0.0, mask=md)
+    _check(orc, host_f32(g1), r, dtype, f"q_len=1 strided V {dtype}")
+    from ytensor_amd import _lib
+    from ytensor_amd._lib import i64array
+    out = torch.empty_like(g1)
+    code = {"f32": _lib.F32, "f16": _lib.F16}[dtype]
+    st = _lib.lib().ythip_attn_prefill(code, B, Hq, Hkv, 1, S, D, D, Qd.data_ptr(), i64array(Qd.stride()),
+                                       Kd.data_ptr(), i64array(Kd.stride()), Vd.data_ptr(), i64array(Vd.stride()),
+                                       out.data_ptr(), i64array(out.stride()), 0.0, _lib.MASK_BOOL, md.data_ptr(), S,
+                                       None, 0, 0, torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "ythip_attn_prefill")
+    _check(orc, host_f32(out), r, dtype, f"q_len=1 no workspace {dtype}")
+    z = yt.scaled_dot_product_attention(Qd, Kd, Vd, 0.0, mask=torch.zeros((1, S), dtype=torch.bool).cuda())
+    assert not host_f32(z).any()
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_decode_ragged_lengths(orc, yt, dtype):
     """Per-sequence cache lengths (kv_len[b]); keys past the length are invisible."""

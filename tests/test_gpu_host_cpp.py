@@ -116,3 +116,86 @@ def test_decode_one_query(orc, outputs):
 
 def test_rmsnorm_inplace(outputs, golden):
     assert rel_err(outputs["rmsnorm"], golden["rmsnorm"]) <= 1e-4
+
+
+def _decode_case(orc, B, ctx):
+    orc.seed(2)
+    K = _bf16(orc, orc.randn(B, 8, ctx, 128))
+    V = _bf16(orc, orc.randn(B, 8, ctx, 128))
+    Q = _bf16(orc, orc.randn(B, 16, 1, 128))
+    return Q, K, V
+
+
+@pytest.mark.parametrize("B,ctx", [(1, 1024), (1, 8192), (16, 1024), (16, 8192)])
+def test_decode_qwen3_per_token_call_form(orc, outputs, B, ctx):
+    """configs[3] in the example's per-token form (qwen3.cpp:250-264): 5-D q,
+    repeat_kv'd K/V, the wrapped ring's get_mask bool mask, FLASH_AVX2 -- the
+    q_len == 1 branch of flash_attention (flash_attention.inl:469-499)."""
+    Q, K, V = _decode_case(orc, B, ctx)
+    r = orc.sdpa_gqa(Q, K, V, 1.0 / math.sqrt(128), False)
+    g = outputs[f"dec_B{B}_c{ctx}"]
+    assert g.shape == (B, 8, 2, 1, 128)
+    check16(orc, g.reshape(B, 16, 1, 128), r, "bf16", True, f"C++ decode call form B={B} ctx={ctx}")
+
+
+def _per_head(orc, Q, K, V, mask, bias):
+    """flash_attention per (batch, head) over the GQA mapping h -> h // G."""
+    B, Hq = Q.shape[:2]
+    G = Hq // K.shape[1]
+    out = np.zeros((B, Hq, Q.shape[2], V.shape[3]), np.float32)
+    for b in range(B):
+        for h in range(Hq):
+            out[b, h] = orc.flash_attention(Q[b, h], K[b, h // G], V[b, h // G], 1.0 / math.sqrt(Q.shape[3]),
+                                            mask, bias)
+    return out
+
+
+def test_decode_random_mask_and_bias(orc, outputs):
+    Q, K, V = _decode_case(orc, 1, 1024)
+    orc.seed(21)
+    mask = orc.randn(1, 1024) > np.float32(-0.5)
+    bias = _bf16(orc, orc.randn(1, 1024))
+    assert 0.5 < mask.mean() < 0.9
+    r = _per_head(orc, Q, K, V, mask, bias)
+    check16(orc, outputs["dec_rand"].reshape(1, 16, 1, 128), r, "bf16", True, "C++ decode mask+bias")
+
+
+def test_decode_all_masked_is_zero(outputs):
+    assert not outputs["dec_none"].any()
+
+
+def test_decode_predicate(orc, outputs):
+    Q, K, V = _decode_case(orc, 1, 1024)
+    mask = np.arange(1024)[None, :] <= 512
+    r = _per_head(orc, Q, K, V, mask, None)
+    check16(orc, outputs["dec_pred"].reshape(1, 16, 1, 128), r, "bf16", True, "C++ decode CausalMask{512}")
+
+
+def test_decode_group_of_five_falls_back(orc, outputs):
+    orc.seed(22)
+    K = _bf16(orc, orc.randn(1, 8, 512, 128))
+    V = _bf16(orc, orc.randn(1, 8, 512, 128))
+    Q = _bf16(orc, orc.randn(1, 40, 1, 128))
+    r = orc.sdpa_gqa(Q, K, V, 1.0 / math.sqrt(128), False)
+    check16(orc, outputs["dec_g5"].reshape(1, 40, 1, 128), r, "bf16", True, "C++ decode G=5")
+
+
+def test_decode_two_threads_two_streams(outputs):
+    """Two std::threads, each with its own stream, decoding at once: every one of
+    their 24 results has the serial bits (each thread and stream has its own
+    split-K workspace)."""
+    assert outputs["concurrent"][0] == 0
+
+
+def test_rmsnorm_out_of_place_and_axes(orc, outputs, golden):
+    assert np.array_equal(outputs["rmsnorm_oop"], outputs["rmsnorm"])
+    assert rel_err(outputs["rmsnorm_oop"], golden["rmsnorm"]) <= 1e-4
+    orc.seed(13)
+    x, w = orc.randn(2, 64, 3), orc.randn(64)
+    r = orc.rms_norm(np.ascontiguousarray(x.transpose(0, 2, 1)).reshape(-1, 64), w, 1e-6)
+    r = r.reshape(2, 3, 64).transpose(0, 2, 1)
+    assert rel_err(outputs["rmsnorm_ax1"], r) <= 1e-4
+    orc.seed(14)
+    x, w = orc.randn(2, 4, 32), orc.randn(4, 32)
+    r = orc.rms_norm(x.reshape(2, 128), w.reshape(128), 1e-6).reshape(2, 4, 32)
+    assert rel_err(outputs["rmsnorm_ax12"], r) <= 1e-4

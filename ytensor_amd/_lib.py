@@ -49,6 +49,7 @@ SIGNATURES = {
     "ythip_attn_prefill": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _LP, _P, _LP, _P, _LP, _P, _LP,
                                 _F, _I, _P, _L, _P, _L, _L, _P]),
     "ythip_attn_prefill_workspace_size": (ctypes.c_size_t, [_I, _I]),
+    "ythip_attn_sdpa_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     "ythip_attn_prefill_ws": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _LP, _P, _LP, _P, _LP, _P, _LP,
                                    _F, _I, _P, _L, _P, _L, _L, _P, ctypes.c_size_t, _P]),
     "ythip_attn_math_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
@@ -68,6 +69,7 @@ SIGNATURES = {
     "ythip_rmsnorm_rope": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _P, _L, _I, _I,
                                 _P, _LP, _P, _LP, _P, _LP, _I, _I, _P, _P]),
     "ythip_rms_norm": (_I, [_I, _I, _I, _I, _P, _L, _P, _F, _P, _L, _P]),
+    "ythip_rms_norm_strided": (_I, [_I, _I, _I, _I, _P, _L, _L, _P, _F, _P, _L, _L, _P]),
     "ythip_silu_mul": (_I, [_I, _I, _I, _I, _P, _L, _P, _L, _P]),
     "ythip_embedding": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _L, _P]),
     "ythip_add_bias": (_I, [_I, _I, _I, _P, _L, _P, _P]),

@@ -1134,8 +1134,16 @@ struct DecodeArgs {
     const void* K;
     const void* V;
     void* O;
-    int64_t qs0, qs1, os0, os1, ks0, ks1, ks2;
+    int64_t qs0, qs1, os0, os1, ks0, ks1, ks2, vs0, vs1, vs2;
     const int32_t* kv_len;
+    // Masked single-query calls routed from ythip_attn_prefill (the q_len == 1
+    // branch of flash_attention, src/kernel/avx2/flash_attention.inl:469-499):
+    // key j is visible iff mask[j] != 0 (row 0 of a bool mask; NULL = all) and
+    // bias[j * bcs] (fp32; NULL = none) is added to its scaled score. Only the
+    // MK instantiations read them.
+    const uint8_t* mask;
+    const float* bias;
+    int64_t bcs;
     int B, Hq, Hkv, max_ctx, splits, chunk;
     float scale_log2;
     float* ws;  // [B, Hq, splits, D + 2]
@@ -1188,8 +1196,10 @@ __device__ __forceinline__ void store8_raw(typename T::raw* p, const float (&x)[
 // ythip_rmsnorm_rope followed by ythip_attn_decode.
 // NTH threads per workgroup: 512 (twice the keys in flight, so a split of up to
 // 128 keys is one batch) when the grid is too small to cover the CUs.
-template <class T, int D, int G, bool FUSED, int NTH>
+// MK: a per-key byte mask and / or bias (DecodeArgs::mask, ::bias) take part.
+template <class T, int D, int G, bool FUSED, int NTH, bool MK = false>
 __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
+    static_assert(!(FUSED && MK), "the fused decode step takes no mask");
     using raw = typename T::raw;
     constexpr int LPK = D / 8;          // lanes per key
     constexpr int SLOTS = NTH / LPK;    // keys in flight per workgroup
@@ -1257,7 +1267,7 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
         for (int e = 0; e < 8; ++e) o[gi][e] = 0.f;
     }
     const raw* Kb = static_cast<const raw*>(a.K) + b * a.ks0 + kvh * a.ks1 + part * 8;
-    const raw* Vb = static_cast<const raw*>(a.V) + b * a.ks0 + kvh * a.ks1 + part * 8;
+    const raw* Vb = static_cast<const raw*>(a.V) + b * a.vs0 + kvh * a.vs1 + part * 8;
 
     // K/V of keys [k0, k0 + SLOTS * UNR) (this lane's 8 elements), clamped rows for
     // keys past the end (loaded but never used). The batch stays in its raw form
@@ -1267,6 +1277,8 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     u32x4 kr[UNR][KW], vr[UNR][KW];
     float kx[UNR][8], vx[UNR][8];
     bool ok[UNR];
+    uint8_t mkb[UNR];  // MK: the keys' mask bytes
+    float bsv[UNR];    // MK: the keys' bias values
     auto load_batch = [&](int k0) {
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
@@ -1274,7 +1286,11 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
             ok[u] = key < kend;
             const int kk = ok[u] ? key : kbeg;
             const raw* kp = Kb + (int64_t)kk * a.ks2;
-            const raw* vp = Vb + (int64_t)kk * a.ks2;
+            const raw* vp = Vb + (int64_t)kk * a.vs2;
+            if constexpr (MK) {
+                mkb[u] = a.mask != nullptr ? a.mask[kk] : (uint8_t)1;
+                bsv[u] = a.bias != nullptr ? a.bias[(int64_t)kk * a.bcs] : 0.f;
+            }
 #pragma unroll
             for (int i = 0; i < KW; ++i) {
                 // streamed once: non-temporal loads (measured ~10% more HBM read rate)
@@ -1384,8 +1400,10 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
                 s_new[r * D + HALF + 8 * j + e] = x2[e];
             }
             if (r >= G) {  // append k (r == G) or v to the cache at `pos`
-                raw* dst = static_cast<raw*>(const_cast<void*>(r == G ? a.K : a.V)) + b * a.ks0 + kvh * a.ks1 +
-                           (int64_t)pos * a.ks2;
+                raw* dst = r == G ? static_cast<raw*>(const_cast<void*>(a.K)) + b * a.ks0 + kvh * a.ks1 +
+                                        (int64_t)pos * a.ks2
+                                  : static_cast<raw*>(const_cast<void*>(a.V)) + b * a.vs0 + kvh * a.vs1 +
+                                        (int64_t)pos * a.vs2;
                 store8_raw<T>(dst + 8 * j, x1);
                 store8_raw<T>(dst + HALF + 8 * j, x2);
             }
@@ -1430,7 +1448,12 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) sv = fmaf(q[gi][e], kx[u][e], sv);
                 sv = dpp_sum_group<LPK>(sv);
-                sc[u] = ok[u] ? sv : -INFINITY;
+                if constexpr (MK) {
+                    // the bias is added after scaling, in the kernel's log2 units
+                    sc[u] = ok[u] && mkb[u] != 0 ? fmaf(bsv[u], LOG2E, sv) : -INFINITY;
+                } else {
+                    sc[u] = ok[u] ? sv : -INFINITY;
+                }
                 mx = fmaxf(mx, sc[u]);
             }
             // One correction per UNR keys; the running max stays finite once any key was seen.
@@ -1731,14 +1754,17 @@ template <class T, int D, int G>
 hipError_t launch_decode_g(const DecodeArgs& a, hipStream_t s) {
     dim3 grid(a.splits, a.Hkv, a.B);
     const bool wide = decode_wide(a.B, a.Hkv, a.splits, G, D);
+    const bool mk = a.mask != nullptr || a.bias != nullptr;
     if constexpr ((512 / (D / 8)) * G * D * 4 <= 64 * 1024) {
         if (wide) {
             if (a.fused) attn_decode_split<T, D, G, true, 512><<<grid, 512, 0, s>>>(a);
+            else if (mk) attn_decode_split<T, D, G, false, 512, true><<<grid, 512, 0, s>>>(a);
             else attn_decode_split<T, D, G, false, 512><<<grid, 512, 0, s>>>(a);
         }
     }
     if (!wide) {
         if (a.fused) attn_decode_split<T, D, G, true, 256><<<grid, 256, 0, s>>>(a);
+        else if (mk) attn_decode_split<T, D, G, false, 256, true><<<grid, 256, 0, s>>>(a);
         else attn_decode_split<T, D, G, false, 256><<<grid, 256, 0, s>>>(a);
     }
     hipError_t e = hipGetLastError();
@@ -1763,6 +1789,55 @@ template <class T>
 hipError_t launch_decode(const DecodeArgs& a, int D, int G, hipStream_t s) {
     if (D == 128) return launch_decode_d<T, 128>(a, G, s);
     return launch_decode_d<T, 64>(a, G, s);
+}
+
+// The q_len == 1 branch of flash_attention (src/kernel/avx2/flash_attention.inl:
+// 469-499): every single-query call -- no mask, causal, diagonal predicate,
+// bool mask, bias -- goes to the split-K decode kernel when its layout fits it
+// (d == dv in {64, 128}, Hq / Hkv in {1, 2, 4, 8}, contiguous head dim,
+// 16-byte aligned K / V rows). Split-K partials go to the caller's workspace:
+// as many splits as it holds, up to decode_splits (none: one split per
+// (kv head, batch), written straight to O). Returns -1 when the call does not
+// fit (the caller runs the prefill kernels), else the call's status.
+int decode_route(int dtype, const AttnArgs& p, int mask_kind, const uint8_t* mask, int64_t mask_ld,
+                 void* workspace, size_t ws_bytes, hipStream_t s) {
+    if (p.Sq != 1 || p.Skv <= 0 || p.D != p.Dv || (p.D != 64 && p.D != 128)) return -1;
+    const int G = p.Hq / p.Hkv;
+    if (G != 1 && G != 2 && G != 4 && G != 8) return -1;
+    if (p.qs3 != 1 || p.ks3 != 1 || p.vs3 != 1 || p.os3 != 1) return -1;
+    const int es = dtype == YTHIP_F32 ? 4 : 2, ev = 16 / es;
+    if (!al(p.K, 16) || !al(p.V, 16) || !al(p.Q, es) || !al(p.O, es)) return -1;
+    if (p.ks0 % ev || p.ks1 % ev || p.ks2 % ev || p.vs0 % ev || p.vs1 % ev || p.vs2 % ev) return -1;
+    // visible keys [0, n): a causal mask's single row sees every key
+    // (offset kv_len - 1); a diagonal predicate j <= off sees off + 1 of them
+    int64_t n = p.Skv;
+    if (mask_kind == YTHIP_MASK_DIAG) n = std::max<int64_t>(0, std::min<int64_t>(mask_ld + 1, p.Skv));
+    if (n == 0) return -1;  // no visible key: the prefill path writes the zero rows
+    DecodeArgs a{};
+    a.Q = p.Q; a.K = p.K; a.V = p.V; a.O = p.O;
+    a.qs0 = p.qs0; a.qs1 = p.qs1; a.os0 = p.os0; a.os1 = p.os1;
+    a.ks0 = p.ks0; a.ks1 = p.ks1; a.ks2 = p.ks2;
+    a.vs0 = p.vs0; a.vs1 = p.vs1; a.vs2 = p.vs2;
+    a.kv_len = nullptr;
+    a.B = p.B; a.Hq = p.Hq; a.Hkv = p.Hkv; a.max_ctx = (int)n;
+    const size_t per_split = (size_t)p.B * p.Hq * (p.D + 2) * sizeof(float);
+    int splits = decode_splits(p.B, p.Hq, (int)n);
+    if (workspace == nullptr || !al(workspace, 4)) splits = 1;
+    else splits = (int)std::min<size_t>((size_t)splits, ws_bytes / per_split);
+    if (splits < 1) splits = 1;
+    a.splits = splits;
+    a.direct = splits == 1;  // one split: the split kernel stores O, no merge
+    a.chunk = (int)((n + splits - 1) / splits);
+    a.scale_log2 = p.scale_log2;
+    a.ws = splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    a.mask = mask_kind == YTHIP_MASK_BOOL ? mask : nullptr;
+    a.bias = p.bias;
+    a.bcs = p.bcs;
+    switch (dtype) {
+        case YTHIP_F32: return status_of(launch_decode<F32>(a, p.D, G, s));
+        case YTHIP_F16: return status_of(launch_decode<F16>(a, p.D, G, s));
+        default: return status_of(launch_decode<BF16>(a, p.D, G, s));
+    }
 }
 
 }  // namespace
@@ -1829,6 +1904,13 @@ __attribute__((visibility("default"))) int ythip_attn_prefill_ws(
     a.mask = mask_kind == YTHIP_MASK_BOOL ? mask : nullptr;
     a.mask_ld = mask_ld;
     a.bias = bias; a.brs = rs_bias; a.bcs = cs_bias;
+    if (dtype != YTHIP_F32 && dtype != YTHIP_F16 && dtype != YTHIP_BF16)
+        return fail(YTHIP_EINVAL, "ythip_attn_prefill: invalid dtype %d", dtype);
+    if (q_len == 1) {
+        const int st = decode_route(dtype, a, mask_kind, mask, mask_ld, workspace, ws_bytes,
+                                    static_cast<hipStream_t>(stream));
+        if (st != -1) return st;
+    }
     if (workspace != nullptr && mask_kind == YTHIP_MASK_BOOL && kv_len > 0) {
         // room for the mask's tile classes: the long-sequence paired-head path
         // then runs the ping-pong kernel over listed blocks
@@ -1856,6 +1938,13 @@ __attribute__((visibility("default"))) int ythip_attn_prefill_ws(
 __attribute__((visibility("default"))) size_t ythip_attn_decode_workspace_size(int B, int Hq, int max_ctx, int d) {
     if (B <= 0 || Hq <= 0 || max_ctx <= 0 || d <= 0) return 0;
     return (size_t)B * Hq * decode_splits(B, Hq, max_ctx) * (d + 2) * sizeof(float);
+}
+
+__attribute__((visibility("default"))) size_t ythip_attn_sdpa_workspace_size(int B, int Hq, int q_len, int kv_len,
+                                                                             int d) {
+    const size_t tiles = ythip_attn_prefill_workspace_size(q_len, kv_len);
+    const size_t dec = q_len == 1 ? ythip_attn_decode_workspace_size(B, Hq, kv_len, d) : 0;
+    return std::max(tiles, dec);
 }
 
 __attribute__((visibility("default"))) int ythip_attn_decode(int dtype, int B, int Hq, int Hkv, int d, int max_ctx,
@@ -1887,6 +1976,7 @@ __attribute__((visibility("default"))) int ythip_attn_decode(int dtype, int B, i
     a.Q = Q; a.K = Kc; a.V = Vc; a.O = O;
     a.qs0 = q_str[0]; a.qs1 = q_str[1]; a.os0 = o_str[0]; a.os1 = o_str[1];
     a.ks0 = kv_str[0]; a.ks1 = kv_str[1]; a.ks2 = kv_str[2];
+    a.vs0 = kv_str[0]; a.vs1 = kv_str[1]; a.vs2 = kv_str[2];
     a.kv_len = kv_len;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_ctx = max_ctx;
     a.splits = decode_splits(B, Hq, max_ctx > 0 ? max_ctx : 1);
@@ -2012,6 +2102,7 @@ __attribute__((visibility("default"))) int ythip_attn_decode_rope(
         a.os1 = o_str[1];
     }
     a.ks0 = kv_str[0]; a.ks1 = kv_str[1]; a.ks2 = kv_str[2];
+    a.vs0 = kv_str[0]; a.vs1 = kv_str[1]; a.vs2 = kv_str[2];
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_ctx = max_ctx;
     a.splits = decode_splits(B, Hq, max_ctx);
     a.direct = O != nullptr && a.splits == 1;  // one split: no merge launch

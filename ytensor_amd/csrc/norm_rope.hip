@@ -191,6 +191,31 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void* x, int64_t ld
     for (int i = threadIdx.x; i < n; i += 256) store_from_f32<TO>(yr, i, (load_as_f32<T>(xr, i) / den) * w[i]);
 }
 
+// rms_norm_kernel with element strides (one normalised axis of any stride, the
+// axes overloads of rmsNorm / rmsNorm_): the same element-to-thread assignment
+// and operation order, so the same bits as the contiguous kernels.
+template <class T, class TO>
+__global__ __launch_bounds__(256) void rms_norm_strided_kernel(const void* x, int64_t ldx, int64_t csx,
+                                                               const float* w, float eps, void* y, int64_t ldy,
+                                                               int64_t csy, int n) {
+    const int64_t row = blockIdx.x;
+    const auto* xr = static_cast<const typename T::raw*>(x) + row * ldx;
+    auto* yr = static_cast<typename TO::raw*>(y) + row * ldy;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = load_as_f32<T>(xr, i * csx);
+        ss = fmaf(v, v, ss);
+    }
+    __shared__ float part[4];
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float den = sqrtf(tot / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256)
+        store_from_f32<TO>(yr, i * csy, (load_as_f32<T>(xr, i * csx) / den) * w[i]);
+}
+
 // rms_norm_kernel for n <= 256 * J: the same element-to-thread assignment and
 // operation order (so the same bits), with every load of the row and its
 // weights issued up front and the row kept in registers for the second pass
@@ -239,7 +264,11 @@ hipError_t launch_norm_rope(const NormRopeArgs& a, int d, hipStream_t s) {
 
 template <class T, class TO>
 hipError_t launch_rms(int rows, int n, const void* x, int64_t ldx, const float* w, float eps, void* y, int64_t ldy,
-                      hipStream_t s) {
+                      hipStream_t s, int64_t csx = 1, int64_t csy = 1) {
+    if (csx != 1 || csy != 1) {
+        rms_norm_strided_kernel<T, TO><<<rows, 256, 0, s>>>(x, ldx, csx, w, eps, y, ldy, csy, n);
+        return hipGetLastError();
+    }
     if (n <= 1024) rms_norm_reg_kernel<T, TO, 4><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
     else if (n <= 2048) rms_norm_reg_kernel<T, TO, 8><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
     else if (n <= 4096) rms_norm_reg_kernel<T, TO, 16><<<rows, 256, 0, s>>>(x, ldx, w, eps, y, ldy, n);
@@ -333,6 +362,28 @@ __attribute__((visibility("default"))) int ythip_rms_norm(int dtype_in, int dtyp
     if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F32) YTHIP_RMS(F16, F32);
 #undef YTHIP_RMS
     return fail(YTHIP_EINVAL, "ythip_rms_norm: invalid dtype pair %d/%d", dtype_in, dtype_out);
+}
+
+__attribute__((visibility("default"))) int ythip_rms_norm_strided(int dtype_in, int dtype_out, int rows, int n,
+                                                                  const void* x, int64_t ld_x, int64_t cs_x,
+                                                                  const float* w, float eps, void* y, int64_t ld_y,
+                                                                  int64_t cs_y, void* stream) {
+    if (rows < 0 || n < 0) return fail(YTHIP_EINVAL, "ythip_rms_norm_strided: negative size");
+    if (rows == 0 || n == 0) return 0;
+    if (x == nullptr || y == nullptr || w == nullptr) return fail(YTHIP_EINVAL, "ythip_rms_norm_strided: NULL pointer");
+    if (x == y && (dtype_in != dtype_out || ld_x != ld_y || cs_x != cs_y))
+        return fail(YTHIP_EINVAL, "ythip_rms_norm_strided: in place needs one dtype and one layout");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+#define YTHIP_RMS(TI, TOUT) return status_of(launch_rms<TI, TOUT>(rows, n, x, ld_x, w, eps, y, ld_y, s, cs_x, cs_y))
+    if (dtype_in == YTHIP_F32 && dtype_out == YTHIP_F32) YTHIP_RMS(F32, F32);
+    if (dtype_in == YTHIP_F32 && dtype_out == YTHIP_BF16) YTHIP_RMS(F32, BF16);
+    if (dtype_in == YTHIP_F32 && dtype_out == YTHIP_F16) YTHIP_RMS(F32, F16);
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_BF16) YTHIP_RMS(BF16, BF16);
+    if (dtype_in == YTHIP_BF16 && dtype_out == YTHIP_F32) YTHIP_RMS(BF16, F32);
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F16) YTHIP_RMS(F16, F16);
+    if (dtype_in == YTHIP_F16 && dtype_out == YTHIP_F32) YTHIP_RMS(F16, F32);
+#undef YTHIP_RMS
+    return fail(YTHIP_EINVAL, "ythip_rms_norm_strided: invalid dtype pair %d/%d", dtype_in, dtype_out);
 }
 
 }  // extern "C"

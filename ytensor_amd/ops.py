@@ -223,8 +223,10 @@ def scaled_dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
     visible) or a predicate f(i, j) -> bool (evaluated into a bool mask here).
     bias: optional float32 [Sq, Skv] added after scaling. Rows with no visible
     key come out zero. backend: "flash" (FLASH_AVX2's counterpart, online
-    softmax, no score matrix; with a bool mask, a workspace of
-    ythip_attn_prefill_workspace_size bytes for the mask's tile classes) or
+    softmax, no score matrix; Sq == 1 runs the split-K decode kernel for every
+    mask kind, as flash_attention's q_len == 1 branch does; with a bool mask or
+    Sq == 1, a workspace of ythip_attn_sdpa_workspace_size bytes for the mask's
+    tile classes or the decode partials) or
     "math" (MATH: materialised scores in a workspace of
     ythip_attn_math_workspace_size bytes). A workspace not given or too small
     is allocated.
@@ -274,10 +276,11 @@ def scaled_dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
                 vt.data_ptr(), i64array(vs), ot.data_ptr(), i64array(os_), float(scale), kind, mptr, mld,
                 bptr, brs, bcs, ws.data_ptr(), ws.numel() * ws.element_size(), _stream())
             check(st, "ythip_attn_math")
-        elif kind == _lib.MASK_BOOL:
+        elif kind == _lib.MASK_BOOL or Sq == 1:
             # room for the mask's tile classes (the long-sequence path lists the
-            # key blocks each query block sees from them)
-            need = int(_lib.lib().ythip_attn_prefill_workspace_size(Sq, Skv))
+            # key blocks each query block sees from them) and, for one query
+            # row, the split-K partials of the decode kernel that row runs on
+            need = int(_lib.lib().ythip_attn_sdpa_workspace_size(B, Hq, Sq, Skv, D))
             ws = workspace
             if ws is None or ws.numel() * ws.element_size() < need:
                 ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
