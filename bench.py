@@ -358,6 +358,29 @@ def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=No
                     "projection's prologue)"}
 
 
+def bench_qwen3_cpp(prompt_len: int = 512, n_tokens: int = 256) -> dict:
+    """configs[4] through the C++ host (include/yt/qwen3.hpp, the example's
+    Qwen3ForCausalLM over libythip.so; tests/cpp/qwen3_host.cpp built into
+    ytensor_amd/bin/yt_qwen3): seed-3 randn * 0.02 weights drawn by YTensor's
+    own RNG, the same 512-token prompt, the prompt as one graph replay, then
+    n_tokens - 2 timed replays of the captured decode step (HIP events). Run as
+    a child process; its JSON line is returned."""
+    import subprocess
+    import tempfile
+
+    import numpy as np
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ytensor_amd", "bin", "yt_qwen3")
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, 151936, prompt_len).astype(np.int32)
+    with tempfile.TemporaryDirectory() as d:
+        pf = os.path.join(d, "prompt.i32")
+        prompt.tofile(pf)
+        p = subprocess.run([exe, "bench", pf, str(n_tokens)], capture_output=True, text=True, timeout=300)
+    if p.returncode != 0:
+        return {"error": p.stderr.strip()[-400:]}
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
 def bench_yt_load(torch, dev, reps: int = 3) -> dict:
     """.yt checkpoint to device: a Qwen3-0.6B-shaped checkpoint (the example's
     tensor names, bf16 matrices, fp32 norms, random device weights) written by
@@ -652,6 +675,7 @@ def main() -> int:
     if want("qwen3") and not args.quick:
         sections["qwen3_0p6b_decode"] = bench_qwen3(torch, dev)
         torch.cuda.empty_cache()
+        sections["qwen3_0p6b_decode_cpp_host"] = bench_qwen3_cpp()
         sections["qwen3_0p6b_decode_fp16"] = bench_qwen3(torch, dev, dtype=torch.float16)
         torch.cuda.empty_cache()
 

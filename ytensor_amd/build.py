@@ -45,25 +45,31 @@ def _compile(src: str, resource: bool) -> tuple[str, str]:
 
 ROOT = os.path.dirname(HERE)
 BIN = os.path.join(HERE, "bin")
-HOST_PROGRAMS = {"yt_host_parity": os.path.join(ROOT, "tests", "cpp", "host_parity.cpp")}
+HOST_PROGRAMS = {"yt_host_parity": os.path.join(ROOT, "tests", "cpp", "host_parity.cpp"),
+                 "yt_qwen3": os.path.join(ROOT, "tests", "cpp", "qwen3_host.cpp")}
+
+
+def _build_host(name: str, src: str) -> str:
+    exe = os.path.join(BIN, name)
+    # -ffp-contract=off: host float expressions (the weight recipe's 1 + x * s)
+    # round each operation, as the numpy restatement does
+    cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-ffp-contract=off", f"-I{os.path.join(ROOT, 'include')}",
+           "-I/opt/rocm/include",
+           "-D__HIP_PLATFORM_AMD__", src, "-o", exe + ".tmp", f"-L{HERE}", "-lythip", "-L/opt/rocm/lib",
+           "-lamdhip64", "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,/opt/rocm/lib"]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"g++ failed for {src}:\n{p.stderr}")
+    os.replace(exe + ".tmp", exe)
+    return exe
 
 
 def build_host_programs() -> list[str]:
-    """C++ programs over the host API (include/yt/ytensor.hpp) linked against
-    libythip.so, built with the host compiler into ytensor_amd/bin/."""
+    """C++ programs over the host API (include/yt/ytensor.hpp, include/yt/qwen3.hpp)
+    linked against libythip.so, built with the host compiler into ytensor_amd/bin/."""
     os.makedirs(BIN, exist_ok=True)
-    out = []
-    for name, src in HOST_PROGRAMS.items():
-        exe = os.path.join(BIN, name)
-        cmd = ["g++", "-std=c++20", "-O2", "-Wall", f"-I{os.path.join(ROOT, 'include')}", "-I/opt/rocm/include",
-               "-D__HIP_PLATFORM_AMD__", src, "-o", exe + ".tmp", f"-L{HERE}", "-lythip", "-L/opt/rocm/lib",
-               "-lamdhip64", "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,/opt/rocm/lib"]
-        p = subprocess.run(cmd, capture_output=True, text=True)
-        if p.returncode != 0:
-            raise RuntimeError(f"g++ failed for {src}:\n{p.stderr}")
-        os.replace(exe + ".tmp", exe)
-        out.append(exe)
-    return out
+    with cf.ThreadPoolExecutor(max_workers=len(HOST_PROGRAMS)) as ex:
+        return list(ex.map(lambda kv: _build_host(*kv), HOST_PROGRAMS.items()))
 
 
 def build(resource: bool = False, verbose: bool = False) -> str:
