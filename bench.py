@@ -157,6 +157,22 @@ def read_port_ratio(path: str):
     return None
 
 
+def read_row_ratios(path: str) -> dict:
+    """{cpu row: port / reference time} from the `ratio <row>: <value>` lines
+    oracle/time_port_vs_ref.py writes."""
+    out = {}
+    try:
+        with open(path) as f:
+            for line in f:
+                t = line.strip()
+                if t.startswith("ratio ") and ":" in t:
+                    k, v = t[len("ratio "):].split(":", 1)
+                    out[k.strip()] = float(v)
+    except (OSError, ValueError):
+        pass
+    return out
+
+
 def cpu_baseline(M: int, N: int, K: int, budget_s: float = 12.0) -> dict:
     """YTensor's CPU path for the headline shape: the bf16 inputs are up-converted
     and multiplied by the fp32 sgemm (src/ytensor_base_math.inl:689-700), with
@@ -216,15 +232,20 @@ def cpu_rows(path, kind: str) -> dict:
     threading defaults (the GEMM's thread count left at 1; the attention and
     normalisation loops' OpenMP pools sized by OMP_NUM_THREADS), on bounded
     samples of the same shapes (a few seconds in all):
-      prefill   yt::function::scaled_dot_product_attention causal GQA,
-                16 q / 8 kv heads, D=128, S=2048 (src/function/attention.inl:1-200)
+      prefill   yt::function::scaledDotProductAttention (FLASH_AVX2) causal GQA,
+                16 q / 8 kv heads, D=128, S=2048 (src/function/ops.inl:109-234,
+                src/kernel/avx2/flash_attention.inl:274-443)
       decode    the same with one query row per batch entry, B=16, ctx=8192
+                (flash_attention.inl:202-272)
       norm_rope rmsNorm_ of the q and k heads + RoPE of both, S=8192
-                (src/function/normalization.inl:256-277, example/qwen3/qwen3.cpp:101-133)
+                (src/function/normalization.inl:256-277, example/qwen3/src/qwen3.cpp:522-559)
       math      scaledDotProductAttention(MATH), causal, S=2048 (src/function/ops.inl:388-418)
       masked    YTensor::masked_matmul 2048^3 with a causal predicate (src/ytensor_math.inl:372-410)
       yt_load   YTensorIO::load of a 256 MiB bf16 tensor (src/ytensor_io.inl:785-830)
-    Inputs are N(0,1) (weights N(0,0.02)) rounded to bf16, as on the GPU."""
+    Inputs are N(0,1) (weights N(0,0.02)) rounded to bf16, as on the GPU.
+    Every row carries port_over_reference_time (the port's time / the compiled
+    reference's on the same call, measured where the reference is built:
+    profiles/cpu_port_vs_reference.md) and the reference-equivalent rate."""
     import numpy as np
     import oracle
     o = oracle.oracle()
@@ -293,6 +314,18 @@ def cpu_rows(path, kind: str) -> dict:
         rows["yt_load_256MiB_bf16"] = {"s_per_call": round(t, 4), "gbs": round(w.nbytes / t / 1e9, 3)}
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
+    ratios = read_row_ratios(PORT_RATIO_FILE)
+    for key, row in rows.items():
+        if not isinstance(row, dict):
+            continue
+        r = ratios.get(key)
+        row["port_over_reference_time"] = r
+        if r:
+            row["reference_equivalent_s_per_call"] = round(row["s_per_call"] / r, 4)
+            rate = next((k for k in row if k not in ("s_per_call", "port_over_reference_time",
+                                                     "reference_equivalent_s_per_call")), None)
+            if rate:
+                row["reference_equivalent_" + rate] = round(row[rate] * r, 4)
     return rows
 
 

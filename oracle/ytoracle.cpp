@@ -461,6 +461,7 @@ void flash_prefill(const float* Q, const float* K, const float* V, float* O, int
                    int64_t csb) {
     if (q_len == 0 || kv_len == 0 || hd == 0 || dv == 0) return;
     const float NEG_INF = -std::numeric_limits<float>::infinity();
+    constexpr int MR = 6;  // include/kernel/avx2/gemm_utils.hpp:47 (MR_ROW): query rows per block
     // K packed per 16-key tile as [d][16] (pack_b_generic, flash_attention.inl:302-305)
     // so each score chain over d runs for 16 keys side by side.
     const int ntiles = (kv_len + NR - 1) / NR;
@@ -469,66 +470,102 @@ void flash_prefill(const float* Q, const float* K, const float* V, float* O, int
         for (int j = 0; j < NR && t * NR + j < kv_len; ++j)
             for (int d = 0; d < hd; ++d)
                 kp[(static_cast<size_t>(t) * hd + d) * NR + j] = K[static_cast<int64_t>(t * NR + j) * rsk + d * csk];
-    std::vector<float> acc(dv);
-    for (int i = 0; i < q_len; ++i) {
-        float* orow = O + i * rso;
-        for (int d = 0; d < dv; ++d) orow[d * cso] = 0.0f;
-        const float* q = Q + i * rsq;
-        float row_max = NEG_INF, row_l = 0.0f;
-        float score[NR], prob[NR];
-        bool vis[NR];
+    std::vector<float> qp(static_cast<size_t>(MR) * hd), acc(dv);
+    // one block of MR query rows at a time, as _flashAttentionImpl's q_block loop
+    // (flash_attention.inl:309-443): every key tile's 6 x 16 score tile comes from
+    // one pass over the packed K (dispatch_fma_row: per element an FMA chain over
+    // d from 0, here eight lanes at a time), then each row's online-softmax step.
+    for (int qi = 0; qi < q_len; qi += MR) {
+        const int mr = std::min(MR, q_len - qi);
+        for (int i = 0; i < MR; ++i)
+            for (int d = 0; d < hd; ++d)
+                qp[static_cast<size_t>(i) * hd + d] = i < mr ? Q[static_cast<int64_t>(qi + i) * rsq + d * csq] : 0.0f;
+        float row_max[MR], row_l[MR];
+        for (int i = 0; i < mr; ++i) {
+            row_max[i] = NEG_INF;
+            row_l[i] = 0.0f;
+            float* orow = O + static_cast<int64_t>(qi + i) * rso;
+            for (int d = 0; d < dv; ++d) orow[d * cso] = 0.0f;
+        }
         for (int kj = 0; kj < kv_len; kj += NR) {
             const int nr = std::min(NR, kv_len - kj);
-            bool any_vis = false;
-            for (int j = 0; j < nr; ++j) {
-                vis[j] = mask(i, kj + j);
-                any_vis |= vis[j];
+            bool vis[MR][NR];
+            bool any_block = false;
+            for (int i = 0; i < mr; ++i)
+                for (int j = 0; j < nr; ++j) {
+                    vis[i][j] = mask(qi + i, kj + j);
+                    any_block |= vis[i][j];
+                }
+            if (!any_block) continue;  // _flashTileAllFalse (flash_attention.inl:334-336)
+            alignas(32) float score[MR][NR];
+            {
+                const float* kt = &kp[static_cast<size_t>(kj / NR) * hd * NR];
+                __m256 c[MR][2];
+                for (int i = 0; i < MR; ++i) c[i][0] = c[i][1] = _mm256_setzero_ps();
+                for (int d = 0; d < hd; ++d) {
+                    const __m256 b0 = _mm256_loadu_ps(kt + d * NR), b1 = _mm256_loadu_ps(kt + d * NR + 8);
+                    for (int i = 0; i < MR; ++i) {
+                        const __m256 a = _mm256_set1_ps(qp[static_cast<size_t>(i) * hd + d]);
+                        c[i][0] = _mm256_fmadd_ps(a, b0, c[i][0]);
+                        c[i][1] = _mm256_fmadd_ps(a, b1, c[i][1]);
+                    }
+                }
+                for (int i = 0; i < MR; ++i) {
+                    _mm256_store_ps(&score[i][0], c[i][0]);
+                    _mm256_store_ps(&score[i][8], c[i][1]);
+                }
             }
-            if (!any_vis) continue;  // the row contributes nothing to this tile (flash_attention.inl:377-379)
-            // Score tile: FMA chain over d from 0 (dispatch_fma_row, gemm_utils.inl:225-260).
-            for (int j = 0; j < NR; ++j) score[j] = 0.0f;
-            const float* kt = &kp[static_cast<size_t>(kj / NR) * hd * NR];
-            for (int d = 0; d < hd; ++d) {
-                const float qd = q[d * csq];
-                for (int j = 0; j < NR; ++j) score[j] = std::fma(qd, kt[d * NR + j], score[j]);
+            for (int i = 0; i < mr; ++i) {
+                float* orow = O + static_cast<int64_t>(qi + i) * rso;
+                float prob[NR];
+                bool any_vis = false;
+                for (int j = 0; j < nr; ++j) any_vis |= vis[i][j];
+                if (!any_vis) continue;  // the row contributes nothing to this tile (flash_attention.inl:377-379)
+                // flash_attention.inl:361-398: scale (+bias), running max, exp, new l.
+                float tile_max = NEG_INF;
+                for (int j = 0; j < nr; ++j) {
+                    if (!vis[i][j]) { prob[j] = 0.0f; continue; }
+                    const float sc = bias ? score[i][j] * scale + bias[(qi + i) * rsb + (kj + j) * csb]
+                                          : score[i][j] * scale;
+                    prob[j] = sc;
+                    tile_max = std::max(tile_max, sc);
+                }
+                const float prev_max = row_max[i];
+                const float new_max = std::max(prev_max, tile_max);
+                const float prev_scale = std::isfinite(prev_max) ? std::exp(prev_max - new_max) : 0.0f;
+                float tile_sum = 0.0f;
+                for (int j = 0; j < nr; ++j) {
+                    if (!vis[i][j]) continue;
+                    const float p = std::exp(prob[j] - new_max);
+                    prob[j] = p;
+                    tile_sum += p;
+                }
+                const float l_scaled = row_l[i] * prev_scale;  // shared with the rescale below
+                const float new_l = l_scaled + tile_sum;
+                if (new_l == 0.0f) continue;
+                const float rescale = row_l[i] == 0.0f ? 0.0f : (l_scaled / new_l);
+                // flash_attention.inl:402-404: rows whose (l, max) did not change are skipped.
+                if (new_l == row_l[i] && new_max == row_max[i]) continue;
+                const float inv_new_l = 1.0f / new_l;
+                // _flashAccumulateRowContiguous (160-200): O = O*rescale, then FMA of
+                // (p_j * inv_new_l) * v_j over the tile's keys in key order, skipping p_j == 0.
+                for (int d = 0; d < dv; ++d) acc[d] = (rescale == 0.0f) ? 0.0f : orow[d * cso] * rescale;
+                for (int j = 0; j < nr; ++j) {
+                    if (prob[j] == 0.0f) continue;
+                    const float w = prob[j] * inv_new_l;
+                    const float* vr = V + static_cast<int64_t>(kj + j) * rsv;
+                    int d = 0;
+                    if (csv == 1) {
+                        const __m256 wv = _mm256_set1_ps(w);
+                        for (; d + 8 <= dv; d += 8)
+                            _mm256_storeu_ps(&acc[d], _mm256_fmadd_ps(wv, _mm256_loadu_ps(vr + d), _mm256_loadu_ps(&acc[d])));
+                    }
+                    for (; d < dv; ++d) acc[d] = std::fma(w, vr[d * csv], acc[d]);
+                }
+                for (int d = 0; d < dv; ++d) orow[d * cso] = acc[d];
+                row_max[i] = new_max;
+                row_l[i] = new_l;
             }
-            // flash_attention.inl:361-398: scale (+bias), running max, exp, new l.
-            float tile_max = NEG_INF;
-            for (int j = 0; j < nr; ++j) {
-                if (!vis[j]) { prob[j] = 0.0f; continue; }
-                const float sc = bias ? score[j] * scale + bias[i * rsb + (kj + j) * csb] : score[j] * scale;
-                prob[j] = sc;
-                tile_max = std::max(tile_max, sc);
-            }
-            const float prev_max = row_max;
-            const float new_max = std::max(prev_max, tile_max);
-            const float prev_scale = std::isfinite(prev_max) ? std::exp(prev_max - new_max) : 0.0f;
-            float tile_sum = 0.0f;
-            for (int j = 0; j < nr; ++j) {
-                if (!vis[j]) continue;
-                const float p = std::exp(prob[j] - new_max);
-                prob[j] = p;
-                tile_sum += p;
-            }
-            const float l_scaled = row_l * prev_scale;  // shared with the rescale below
-            const float new_l = l_scaled + tile_sum;
-            if (new_l == 0.0f) continue;
-            const float rescale = row_l == 0.0f ? 0.0f : (l_scaled / new_l);
-            // flash_attention.inl:402-404: rows whose (l, max) did not change are skipped.
-            if (new_l == row_l && new_max == row_max) continue;
-            const float inv_new_l = 1.0f / new_l;
-            // _flashAccumulateRowContiguous (160-200): O = O*rescale, then FMA of
-            // (p_j * inv_new_l) * v_j over the tile's keys in key order, skipping p_j == 0.
-            for (int d = 0; d < dv; ++d) acc[d] = (rescale == 0.0f) ? 0.0f : orow[d * cso] * rescale;
-            for (int j = 0; j < nr; ++j) {
-                if (prob[j] == 0.0f) continue;
-                const float w = prob[j] * inv_new_l;
-                const float* vr = V + static_cast<int64_t>(kj + j) * rsv;
-                for (int d = 0; d < dv; ++d) acc[d] = std::fma(w, vr[d * csv], acc[d]);
-            }
-            for (int d = 0; d < dv; ++d) orow[d * cso] = acc[d];
-            row_max = new_max;
-            row_l = new_l;
         }
     }
 }
