@@ -607,6 +607,21 @@ def main() -> int:
                           "frac_bf16_peak": round(fl / t / 1e9 / PEAK_BF16_TFLOPS, 4)})
             del q, k, v, o, mk
         sections["attn_prefill_bool_mask_bf16"] = pre_b
+        # fp32, the dtype of the reference's flash backend (src/function/ops.inl:
+        # 119-121), on v_mfma_f32_16x16x4_f32; fraction of the fp32 MFMA peak
+        pre32 = []
+        for S in (2048, 8192):
+            q = torch.randn(1, 16, S, 128, device=dev)
+            k = torch.randn(1, 8, S, 128, device=dev)
+            v = torch.randn(1, 8, S, 128, device=dev)
+            o = torch.empty_like(q)
+            fl = 4.0 * 1 * 16 * 128 * S * (S + 1) / 2
+            t = time_launches(lambda: ops.scaled_dot_product_attention(q, k, v, 1 / math.sqrt(128), "causal", out=o),
+                              max(args.steps // 4, 5), min(args.warmup, 3), torch)
+            pre32.append({"S": S, "ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                          "frac_fp32_peak": round(fl / t / 1e9 / PEAK_FP32_TFLOPS, 4)})
+            del q, k, v, o
+        sections["attn_prefill_causal_fp32"] = pre32
 
     if want("decode") and not args.quick:
         dec = []

@@ -44,6 +44,84 @@ def test_config3_causal_prefill_bf16(orc, yt, S):
     check16(orc, g, r, "bf16", True, f"prefill S={S}")
 
 
+def _causal_rows_ref(orc, Qh, Kh, Vh, rows, diag_off):
+    """The reference's flash_attention on a subset of query rows of every head
+    (rows i see keys j <= i + diag_off), q head h on kv head h // G."""
+    B, Hq, S, D = Qh.shape
+    G = Hq // Kh.shape[1]
+    Skv = Kh.shape[2]
+    m = np.arange(Skv)[None, :] <= (rows[:, None] + diag_off)
+    out = np.zeros((B, Hq, len(rows), D), np.float32)
+    for b in range(B):
+        for h in range(Hq):
+            out[b, h] = orc.flash_attention(Qh[b, h, rows], Kh[b, h // G], Vh[b, h // G], 1.0 / math.sqrt(D), m)
+    return out
+
+
+@pytest.mark.parametrize("S", [2048, 8192])
+def test_config3_causal_prefill_fp32_mfma(orc, yt, S):
+    """configs[2]'s shapes in fp32 -- the dtype of the reference's flash path
+    (src/function/ops.inl:119-121) -- on the v_mfma_f32_16x16x4_f32 kernel: Q,
+    K, V ~ N(0,1) from seed 1 in that order, causal, rel <= 1e-4 against the
+    reference's fp32 flash_attention. S=2048: every row; S=8192: the first and
+    last 96 rows and 96 rows around the middle of every head."""
+    orc.seed(1)
+    Q = orc.randn(1, 16, S, 128)
+    K = orc.randn(1, 8, S, 128)
+    V = orc.randn(1, 8, S, 128)
+    g = host_f32(yt.scaled_dot_product_attention(dev_f32(Q), dev_f32(K), dev_f32(V), 1.0 / math.sqrt(128),
+                                                 mask="causal"))
+    if S <= 2048:
+        r = orc.sdpa_gqa(Q, K, V, 1.0 / math.sqrt(128), True)
+        e = rel_err(g, r)
+    else:
+        rows = np.concatenate([np.arange(96), np.arange(S // 2 - 48, S // 2 + 48), np.arange(S - 96, S)])
+        r = _causal_rows_ref(orc, Q, K, V, rows, 0)
+        e = rel_err(g[:, :, rows], r)
+    print(f"fp32 causal prefill S={S}: rel={e:.3e}", flush=True)
+    assert e <= 1e-4
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("kind", ["none", "diag", "bool", "bias", "bool_bias"])
+def test_prefill_fp32_mfma_mask_kinds(orc, yt, D, kind):
+    """The fp32 MFMA kernel's mask forms against the reference's flash_attention:
+    ragged q / kv lengths (not multiples of the 128-query and 64-key blocks),
+    GQA 4:1, B = 2; a diagonal predicate with a negative offset (leading rows see
+    no key -> zeros), a bool mask with a fully masked row, an additive bias."""
+    B, Hq, Hkv, Sq, Skv = 2, 8, 2, 201, 333
+    rng = np.random.default_rng(D + len(kind))
+    Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    mask = bias = None
+    mnp = bnp = None
+    if kind == "none":
+        mnp = None
+    elif kind == "diag":
+        mask = ("diag", -5)
+        mnp = np.arange(Skv)[None, :] <= np.arange(Sq)[:, None] - 5
+    if kind in ("bool", "bool_bias"):
+        mnp = rng.random((Sq, Skv)) > 0.35
+        mnp[7] = False
+        mask = torch.from_numpy(mnp).cuda()
+    if kind in ("bias", "bool_bias"):
+        bnp = rng.standard_normal((Sq, Skv)).astype(np.float32)
+        bias = torch.from_numpy(bnp).cuda()
+    g = host_f32(yt.scaled_dot_product_attention(dev_f32(Q), dev_f32(K), dev_f32(V), 0.0, mask=mask, bias=bias))
+    r = np.zeros_like(g)
+    for b in range(B):
+        for h in range(Hq):
+            r[b, h] = orc.flash_attention(Q[b, h], K[b, h // 4], V[b, h // 4], 1.0 / math.sqrt(D), mnp, bnp)
+    e = rel_err(g, r)
+    print(f"fp32 mfma {kind} D={D}: rel={e:.3e}", flush=True)
+    assert e <= 1e-4
+    if kind in ("bool", "bool_bias"):
+        assert not g[:, :, 7].any()
+    if kind == "diag":
+        assert not g[:, :, :5].any()
+
+
 CASES = [
     # (B, Hq, Hkv, Sq, Skv, D, mask)
     (1, 2, 1, 5, 9, 64, None),

@@ -1127,6 +1127,215 @@ __global__ __launch_bounds__(64) void attn_rowwise(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// fp32 prefill on the matrix cores. The reference's flash backend is fp32-only
+// (src/function/ops.inl:119-121; _flashAttentionImpl, src/kernel/avx2/
+// flash_attention.inl:274-443), so this is its call's native dtype.
+// ---------------------------------------------------------------------------
+// v_mfma_f32_16x16x4_f32; workgroup = 8 waves x 16 queries = 128 queries of one
+// (batch, head); 64-key blocks of K and V double-buffered in LDS by DMA, one
+// barrier per block. Lane l: query r = l % 16 of its wave, lane group g = l / 16.
+//   S^T = K . Q^T: src0 = K[key l%16][d], src1 = Q[query l%16][d] (pre-scaled by
+//     scale * log2 e), d = 16b + 4g + j at step (b, j): lane l receives
+//     S[query r][keys 4g .. 4g+3] of each 16-key tile, so a query's 64 scores of
+//     a block sit in its 4 lanes (l, l^16, l^32, l^48) and its block maximum is
+//     two row swaps (max_across_rows).
+//   O^T += V^T . P^T: step (tile, j) takes the keys 16 tile + 4g + j of the four
+//     lane groups, src0 = V[that key][d = 16t + l%16], src1 = the lane's own
+//     probability j: lane l accumulates O[query r][d = 16t + 4g + i], so the
+//     rescale by 2^(m_old - m_new) is per lane, and the softmax denominator is a
+//     per-lane partial summed over the query's 4 lanes at the end.
+//   LDS: K chunk c (16 bytes) of a row stored at c ^ (key & 7) -- each score
+//     step is one conflict-free ds_read_b128; V chunk c at c ^ (((key>>2)&3)<<2)
+//     -- the four lane groups' ds_read_b32 of four different keys fall in four
+//     bank ranges.
+// MODE 0: no mask; 1: causal / diagonal (key j visible to query i iff j <= i +
+// diag_off; key blocks past the workgroup's last visible key are never loaded,
+// the heaviest query blocks launch first); 2: byte mask and / or bias read per
+// element. Keys at or past kv_len are masked; a query with no visible key
+// gets zeros (flash_attention.inl:241-244, 327-331).
+template <int D, int MODE>
+__global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
+    constexpr int NW = 8, BQ = 16 * NW, BKV = 64;
+    constexpr int KCH = D / 4;          // 16-byte chunks per K / V row
+    constexpr int STG = BKV * KCH;      // chunks per stage of K (or V)
+    constexpr int PT = STG / (64 * NW); // DMA chunks per thread per stage
+    constexpr int NB = D / 16;          // 16-wide k blocks of S, 16-wide d tiles of O
+    static_assert(PT * 64 * NW == STG, "whole DMA rounds");
+    __shared__ u32x4 sK[2 * STG];
+    __shared__ u32x4 sV[2 * STG];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int nqb = (a.Sq + BQ - 1) / BQ;
+    const int nbh = a.B * a.Hq;
+    const int rank = blockIdx.x / nbh, bh = blockIdx.x % nbh;
+    const int qb = MODE == 1 ? nqb - 1 - rank : rank;
+    const int b = bh / a.Hq, h = bh % a.Hq, kvh = h / (a.Hq / a.Hkv);
+    const float* Qp = static_cast<const float*>(a.Q) + b * a.qs0 + h * a.qs1;
+    const float* Kp = static_cast<const float*>(a.K) + b * a.ks0 + kvh * a.ks1;
+    const float* Vp = static_cast<const float*>(a.V) + b * a.vs0 + kvh * a.vs1;
+    float* Op = static_cast<float*>(a.O) + b * a.os0 + h * a.os1;
+    const int q0 = qb * BQ + wave * 16;  // this wave's first query
+    const int qrow = q0 + r;             // this lane's query
+    const bool wave_rows = q0 < a.Sq;
+
+    // key blocks the workgroup reads
+    const int nkb_all = (a.Skv + BKV - 1) / BKV;
+    int nkb = nkb_all;
+    if constexpr (MODE == 1) {
+        const int last = min(qb * BQ + BQ - 1, a.Sq - 1) + a.diag_off;
+        nkb = last < 0 ? 0 : min(nkb_all, last / BKV + 1);
+    }
+
+    // Q fragments, pre-scaled into log2 units: qf[bb][j] = Q[qrow][16 bb + 4 g + j]
+    f32x4 qf[NB];
+    {
+        const float* qp = Qp + (int64_t)min(qrow, a.Sq - 1) * a.qs2 + 4 * g;
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) qf[bb] = *reinterpret_cast<const f32x4*>(qp + 16 * bb) * a.scale_log2;
+    }
+
+    // DMA offsets (elements) within a block; the block base moves by BKV rows
+    int koff[PT], voff[PT], krow[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        const int slot = i * 64 * NW + wave * 64 + lane;
+        const int row = slot / KCH, c = slot % KCH;
+        krow[i] = row;
+        koff[i] = row * (int)a.ks2 + (c ^ (row & 7)) * 4;
+        voff[i] = row * (int)a.vs2 + (c ^ (((row >> 2) & 3) << 2)) * 4;
+    }
+    auto issue = [&](int kb) {
+        const int k0 = kb * BKV;
+        u32x4* dK = sK + (kb & 1) * STG;
+        u32x4* dV = sV + (kb & 1) * STG;
+        const float* kbase = Kp + (int64_t)k0 * a.ks2;
+        const float* vbase = Vp + (int64_t)k0 * a.vs2;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            // rows past the end re-read the last key (masked, never used)
+            const int sh = min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
+            dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * 64 * NW + wave * 64]);
+            dma16_async(vbase + voff[i] + sh * (int)a.vs2, &dV[i * 64 * NW + wave * 64]);
+        }
+    };
+
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 o[NB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if (nkb > 0) issue(0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (kb + 1 < nkb) issue(kb + 1);
+        const int k0 = kb * BKV;
+        if (!wave_rows) continue;
+        if constexpr (MODE == 1) {
+            if (k0 > q0 + 15 + a.diag_off) continue;  // past every row of this wave
+        }
+        // per-element inputs of MODE 2, issued before the score MFMAs
+        uint8_t mk[4][4];
+        float bv[4][4];
+        if constexpr (MODE == 2) {
+            const int qr = min(qrow, a.Sq - 1);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = min(k0 + kt * 16 + 4 * g + i, a.Skv - 1);
+                    mk[kt][i] = a.mask != nullptr ? a.mask[(int64_t)qr * a.mask_ld + key] : (uint8_t)1;
+                    bv[kt][i] = a.bias != nullptr ? a.bias[(int64_t)qr * a.brs + (int64_t)key * a.bcs] * LOG2E : 0.f;
+                }
+        }
+        const u32x4* cK = sK + (kb & 1) * STG;
+        const float* cV = reinterpret_cast<const float*>(sV + (kb & 1) * STG);
+        f32x4 s[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+            f32x4 kf[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                const int key = kt * 16 + r;
+                kf[kt] = __builtin_bit_cast(f32x4, cK[key * KCH + ((4 * bb + g) ^ (key & 7))]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kt][j], qf[bb][j], s[kt], 0, 0, 0);
+        }
+        // visibility, the block's row maximum, probabilities
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = k0 + kt * 16 + 4 * g + i;
+                bool vis = key < a.Skv;
+                if constexpr (MODE == 1) vis = vis && key <= qrow + a.diag_off;
+                float x = s[kt][i];
+                if constexpr (MODE == 2) {
+                    vis = vis && mk[kt][i] != 0;
+                    x += bv[kt][i];
+                }
+                s[kt][i] = vis ? x : -INFINITY;
+                mx = fmaxf(mx, s[kt][i]);
+            }
+        mx = max_across_rows(mx);
+        const float m_new = fmaxf(m, mx);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2f(m - m_use);  // 0 while no key was visible
+        float psum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = exp2f(s[kt][i] - m_use);  // masked: exp2(-inf) = 0
+                s[kt][i] = p;
+                psum += p;
+            }
+        lsum = fmaf(lsum, alpha, psum);
+        m = m_new;
+#pragma unroll
+        for (int t = 0; t < NB; ++t) o[t] *= alpha;
+        // O^T += V^T . P^T over the block's 64 keys
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int key = kt * 16 + 4 * g + j;
+                const float* vrow = cV + key * D + r;
+#pragma unroll
+                for (int t = 0; t < NB; ++t) {
+                    const float vf = vrow[((t ^ g) << 4)];
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, s[kt][j], o[t], 0, 0, 0);
+                }
+            }
+    }
+    if (!wave_rows || qrow >= a.Sq) return;
+    // the query's denominator: the sum of its 4 lanes' partials
+    float lt = lsum;
+    {
+        const uint32_t u = __float_as_uint(lt);
+        const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        lt = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+        const uint32_t w = __float_as_uint(lt);
+        const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+        lt = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+    }
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    float* orow = Op + (int64_t)qrow * a.os2;
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) orow[(16 * t + 4 * g + i) * a.os3] = lt > 0.f ? o[t][i] * inv : 0.f;
+}
+
+// ---------------------------------------------------------------------------
 // Decode
 // ---------------------------------------------------------------------------
 struct DecodeArgs {
@@ -1697,6 +1906,16 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
     return launch_prefill_gh<T, D, 1, 2>(a, mode, s);
 }
 
+template <int D>
+hipError_t launch_prefill_f32(const AttnArgs& a, int mode, hipStream_t s) {
+    const int64_t nqb = (a.Sq + 127) / 128;
+    dim3 grid((unsigned)(nqb * a.B * a.Hq));
+    if (mode == 1) attn_fwd_f32<D, 1><<<grid, 512, 0, s>>>(a);
+    else if (mode == 0) attn_fwd_f32<D, 0><<<grid, 512, 0, s>>>(a);
+    else attn_fwd_f32<D, 2><<<grid, 512, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 template <class T>
 hipError_t launch_rowwise(const AttnArgs& a, hipStream_t s) {
     dim3 grid(a.Sq, a.Hq, a.B);
@@ -1725,6 +1944,20 @@ int prefill_typed(AttnArgs a, hipStream_t s) {
         if constexpr (es == 2) {
             if (a.D == 128) return status_of(launch_prefill_mfma<T, 128>(a, mode, s));
             return status_of(launch_prefill_mfma<T, 64>(a, mode, s));
+        }
+    }
+    if constexpr (es == 4) {
+        // fp32 on v_mfma_f32_16x16x4_f32: 16-byte aligned rows of Q, K and V
+        // (K / V reach LDS by 16-byte DMA), 64 K / V rows within 2^31 elements
+        const bool f32_ok = unit_d && (a.D == 64 || a.D == 128) && a.Dv == a.D && (int64_t)a.B * a.Hq < (1 << 30) &&
+                            al(a.Q, 16) && al(a.K, 16) && al(a.V, 16) && a.qs0 % 4 == 0 && a.qs1 % 4 == 0 &&
+                            a.qs2 % 4 == 0 && a.ks0 % 4 == 0 && a.ks1 % 4 == 0 && a.ks2 % 4 == 0 &&
+                            a.vs0 % 4 == 0 && a.vs1 % 4 == 0 && a.vs2 % 4 == 0 && a.ks2 >= 0 && a.vs2 >= 0 &&
+                            a.ks2 < (1 << 24) && a.vs2 < (1 << 24);
+        if (f32_ok) {
+            const int fmode = a.causal ? 1 : (simple_mask ? 0 : 2);
+            if (a.D == 128) return status_of(launch_prefill_f32<128>(a, fmode, s));
+            return status_of(launch_prefill_f32<64>(a, fmode, s));
         }
     }
     if (a.Skv > ROW_MAX)
