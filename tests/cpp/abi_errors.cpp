@@ -1,9 +1,10 @@
-// CPU-side check of the C++ mirror (include/ythip.hpp): argument errors are
-// reported as exceptions before anything touches a GPU.
+// CPU-side check of the C++ host's kernel-level API (yt::kernel::hip in
+// include/yt/ytensor.hpp): argument errors are reported as exceptions before
+// anything touches a GPU.
 #include <cstdio>
 #include <stdexcept>
 
-#include "../../include/ythip.hpp"
+#include "yt/ytensor.hpp"
 
 int main() {
     int fails = 0;
@@ -11,7 +12,7 @@ int main() {
         yt::kernel::hip::sgemm(nullptr, nullptr, nullptr, -1, 2, 2, 1.0f, 0.0f, 2, 1, 2, 1, 2, 1);
         std::puts("no exception for m = -1");
         fails++;
-    } catch (const std::runtime_error& e) {
+    } catch (const std::invalid_argument& e) {
         std::printf("ok: %s\n", e.what());
     }
     try {

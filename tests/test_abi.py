@@ -71,8 +71,9 @@ def test_decode_noalloc_rejects_oversize_without_a_launch():
 
 
 def test_cpp_mirror_compiles_and_reports_errors(tmp_path):
-    """include/ythip.hpp (yt::kernel::hip) builds with the host C++ compiler
-    against libythip.so and maps argument errors to exceptions."""
+    """The C++ host's kernel-level API (yt::kernel::hip in include/yt/ytensor.hpp)
+    builds with the host C++ compiler against libythip.so and maps argument
+    errors to exceptions."""
     import shutil
     import subprocess
     from ytensor_amd import _lib
@@ -81,8 +82,10 @@ def test_cpp_mirror_compiles_and_reports_errors(tmp_path):
         pytest.skip("g++ not available")
     exe = tmp_path / "abi_errors"
     lib_dir = os.path.dirname(_lib.LIB_PATH)
-    subprocess.check_call([gxx, "-std=c++17", "-O1", os.path.join(ROOT, "tests", "cpp", "abi_errors.cpp"),
-                           "-o", str(exe), f"-L{lib_dir}", "-lythip", f"-Wl,-rpath,{lib_dir}"])
+    subprocess.check_call([gxx, "-std=c++20", "-O1", f"-I{os.path.join(ROOT, 'include')}", "-I/opt/rocm/include",
+                           "-D__HIP_PLATFORM_AMD__", os.path.join(ROOT, "tests", "cpp", "abi_errors.cpp"),
+                           "-o", str(exe), f"-L{lib_dir}", "-lythip", f"-Wl,-rpath,{lib_dir}", "-L/opt/rocm/lib",
+                           "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"])
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "ok:" in out.stdout

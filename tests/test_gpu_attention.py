@@ -220,16 +220,18 @@ STAGED_CASES += [("bf16", k, 2048, 2048, 16, 8, 4) for k in ("causal", "ring", "
 # the same shapes through the tile-class list (ops passes the workspace): every
 # tile mixed, a partial last key block and query block, 16-row regions
 STAGED_CASES += [("bf16", "random", 2048, 2096, 16, 8, 4), ("f16", "blocks", 2000, 2096, 16, 8, 4)]
+STAGED_CASES = [c + (128,) for c in STAGED_CASES]
+# the tile-class path at head dim 64 (its DMA slot count and swizzle masks differ)
+STAGED_CASES += [("bf16", "random", 2048, 2096, 16, 8, 4, 64), ("f16", "blocks", 2000, 2096, 16, 8, 4, 64)]
 
 
-@pytest.mark.parametrize("dtype,kind,Sq,Skv,Hq,Hkv,B", STAGED_CASES)
-def test_prefill_bool_mask_staged(orc, yt, dtype, kind, Sq, Skv, Hq, Hkv, B):
+@pytest.mark.parametrize("dtype,kind,Sq,Skv,Hq,Hkv,B,D", STAGED_CASES)
+def test_prefill_bool_mask_staged(orc, yt, dtype, kind, Sq, Skv, Hq, Hkv, B, D):
     """Bool masks with 16-byte aligned rows take the staged MFMA path (mask tile
     per key block in LDS, all-false blocks skipped, all-true blocks unmasked; a
     partial last key block reads its bytes directly): against the oracle's
     flash_attention with the same mask (src/kernel/avx2/flash_attention.inl:
     335-379), fully masked rows zero."""
-    D = 128
     rng = np.random.default_rng(Sq + Skv)
     Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
     K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)

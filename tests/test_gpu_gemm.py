@@ -278,6 +278,25 @@ def test_linear_bias_rounds_product_first(orc, yt, dtype):
         yt.linear(xd, Wd, bd[:-1])
 
 
+def test_linear_bias_and_embedding_past_65535_rows(orc, yt):
+    """linear(x, W, b) and the embedding gather over more rows than one grid
+    dimension holds (70000): every row gets its bias / its table row."""
+    from ytensor_amd import ops
+    rows = 70000
+    rng = np.random.default_rng(23)
+    x = torch.from_numpy(rng.standard_normal((rows, 32)).astype(np.float32)).cuda()
+    W = torch.from_numpy(rng.standard_normal((24, 32)).astype(np.float32)).cuda()
+    b = torch.from_numpy(rng.standard_normal(24).astype(np.float32)).cuda()
+    plain = yt.linear(x, W)
+    biased = yt.linear(x, W, b)
+    assert torch.equal(biased, plain + b[None, :])
+    table = torch.from_numpy(rng.standard_normal((500, 64)).astype(np.float32)).cuda()
+    ids = torch.from_numpy(rng.integers(0, 500, rows).astype(np.int32)).cuda()
+    out = torch.empty(rows, 64, device="cuda")
+    ops.embedding(table, ids, out)
+    assert torch.equal(out, table[ids.long()])
+
+
 @pytest.mark.parametrize("dtype,out_dtype,beta,batch,n,layout", [("bf16", torch.bfloat16, 0.0, 1, 12288, "NN"),
                                                                  ("f16", torch.float16, 0.0, 1, 12288, "NN"),
                                                                  ("bf16", torch.float32, 1.0, 1, 12288, "NN"),

@@ -13,6 +13,8 @@
 
 #include <cfloat>
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -80,26 +82,29 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const void* gu, int64
 }
 
 // Rows whose id is outside [0, vocab) get zeros: the id is never used as an
-// address.
+// address. Rows beyond the grid's 65535 y-blocks are taken in a row-stride loop.
 template <class T, class TO>
 __global__ __launch_bounds__(256) void embedding_kernel(const void* table, const int32_t* ids, void* out,
-                                                        int64_t ld_out, int n, int vocab) {
-    const int r = blockIdx.y;
-    const int64_t row = ids[r];
-    const bool valid = row >= 0 && row < vocab;
-    for (int j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256)
-        store_from_f32<TO>(out, (int64_t)r * ld_out + j, valid ? load_as_f32<T>(table, row * n + j) : 0.0f);
+                                                        int64_t ld_out, int n, int vocab, int rows) {
+    for (int r = blockIdx.y; r < rows; r += gridDim.y) {
+        const int64_t row = ids[r];
+        const bool valid = row >= 0 && row < vocab;
+        for (int j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256)
+            store_from_f32<TO>(out, (int64_t)r * ld_out + j, valid ? load_as_f32<T>(table, row * n + j) : 0.0f);
+    }
 }
 
 // linear's bias (src/function/ops.inl:93-104): the product is already stored
 // (rounded to T); the bias is then added in T, out = T(out + bias).
 template <class T>
-__global__ __launch_bounds__(256) void add_bias_kernel(void* out, int64_t ld_out, const void* bias, int n) {
-    const int r = blockIdx.y;
+__global__ __launch_bounds__(256) void add_bias_kernel(void* out, int64_t ld_out, const void* bias, int n, int rows) {
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= n) return;
-    const int64_t i = (int64_t)r * ld_out + j;
-    store_from_f32<T>(out, i, load_as_f32<T>(out, i) + load_as_f32<T>(bias, j));
+    const float b = load_as_f32<T>(bias, j);
+    for (int r = blockIdx.y; r < rows; r += gridDim.y) {  // rows past 65535 y-blocks: row-stride loop
+        const int64_t i = (int64_t)r * ld_out + j;
+        store_from_f32<T>(out, i, load_as_f32<T>(out, i) + b);
+    }
 }
 
 // One workgroup scans all n logits; ties resolve to the lowest index (the
@@ -155,8 +160,8 @@ hipError_t launch_silu(int rows, int n, const void* gu, int64_t ld_gu, void* out
 template <class T, class TO>
 hipError_t launch_embed(int rows, int n, int vocab, const void* table, const int32_t* ids, void* out,
                         int64_t ld_out, hipStream_t s) {
-    dim3 grid((unsigned)((n + 255) / 256), rows);
-    embedding_kernel<T, TO><<<grid, 256, 0, s>>>(table, ids, out, ld_out, n, vocab);
+    dim3 grid((unsigned)((n + 255) / 256), (unsigned)std::min(rows, 65535));
+    embedding_kernel<T, TO><<<grid, 256, 0, s>>>(table, ids, out, ld_out, n, vocab, rows);
     return hipGetLastError();
 }
 
@@ -196,7 +201,6 @@ __attribute__((visibility("default"))) int ythip_embedding(int dtype_table, int 
                                                            void* out, int64_t ld_out, void* stream) {
     if (rows < 0 || n < 0 || vocab < 0) return fail(YTHIP_EINVAL, "ythip_embedding: negative size");
     if ((int64_t)rows * n == 0) return 0;
-    if (rows > 65535) return fail(YTHIP_EUNSUPPORTED, "ythip_embedding: %d rows (at most 65535 per call)", rows);
     if (!table || !ids || !out || ld_out < n)
         return fail(YTHIP_EINVAL, "ythip_embedding: NULL pointer or leading dimension too small");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -208,14 +212,13 @@ __attribute__((visibility("default"))) int ythip_add_bias(int dtype, int rows, i
                                                           const void* bias, void* stream) {
     if (rows < 0 || n < 0) return fail(YTHIP_EINVAL, "ythip_add_bias: negative size");
     if ((int64_t)rows * n == 0) return 0;
-    if (rows > 65535) return fail(YTHIP_EUNSUPPORTED, "ythip_add_bias: %d rows (at most 65535 per call)", rows);
     if (!out || !bias || ld_out < n) return fail(YTHIP_EINVAL, "ythip_add_bias: NULL pointer or ld_out < n");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    dim3 grid((unsigned)((n + 255) / 256), rows);
+    dim3 grid((unsigned)((n + 255) / 256), (unsigned)std::min(rows, 65535));
     switch (dtype) {
-        case YTHIP_F32: add_bias_kernel<F32><<<grid, 256, 0, s>>>(out, ld_out, bias, n); break;
-        case YTHIP_F16: add_bias_kernel<F16><<<grid, 256, 0, s>>>(out, ld_out, bias, n); break;
-        case YTHIP_BF16: add_bias_kernel<BF16><<<grid, 256, 0, s>>>(out, ld_out, bias, n); break;
+        case YTHIP_F32: add_bias_kernel<F32><<<grid, 256, 0, s>>>(out, ld_out, bias, n, rows); break;
+        case YTHIP_F16: add_bias_kernel<F16><<<grid, 256, 0, s>>>(out, ld_out, bias, n, rows); break;
+        case YTHIP_BF16: add_bias_kernel<BF16><<<grid, 256, 0, s>>>(out, ld_out, bias, n, rows); break;
         default: return fail(YTHIP_EINVAL, "ythip_add_bias: invalid dtype %d", dtype);
     }
     return status_of(hipGetLastError());
