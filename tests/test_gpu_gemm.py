@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from conftest import rel_err
-from helpers import TORCH_DT, check16, host_f32, make_input
+from helpers import TORCH_DT, check16, dev_f32, host_f32, make_input
 
 pytestmark = pytest.mark.gpu
 
@@ -276,6 +276,29 @@ def test_linear_bias_rounds_product_first(orc, yt, dtype):
     assert np.array_equal(host_f32(biased).view(np.uint32), expect.view(np.uint32))
     with pytest.raises(ValueError):
         yt.linear(xd, Wd, bd[:-1])
+
+
+@pytest.mark.parametrize("layout", ["NN", "NT"])
+def test_fp32_dma_kernel_large_tiles_edges(orc, yt, layout):
+    """fp32 on the DMA-staged v_mfma_f32_16x16x4_f32 kernel with 128 x 128 tiles
+    (>= 512 tiles): partial last tiles in m and n, alpha / beta, rel <= 1e-4
+    against the reference's fp32 sgemm."""
+    m, n, k = 3000, 2820, 96
+    rng = np.random.default_rng(41)
+    A = rng.standard_normal((m, k)).astype(np.float32)
+    Bm = rng.standard_normal((k, n)).astype(np.float32)
+    C0 = rng.standard_normal((m, n)).astype(np.float32)
+    Ad, Cd = dev_f32(A), dev_f32(C0)
+    if layout == "NN":
+        Bd = dev_f32(Bm)
+        r = orc.sgemm(A, Bm, alpha=0.75, beta=-0.5, C=C0)
+    else:
+        Bd = dev_f32(np.ascontiguousarray(Bm.T)).t()
+        r = orc.sgemm(A, np.ascontiguousarray(Bm.T), b_trans=True, alpha=0.75, beta=-0.5, C=C0)
+    yt.ops.gemm(Ad, Bd, Cd, alpha=0.75, beta=-0.5)
+    e = rel_err(host_f32(Cd), r)
+    print(f"fp32 {layout} {m}x{n}x{k}: rel={e:.3e}", flush=True)
+    assert e <= REL_F32
 
 
 def test_linear_bias_and_embedding_past_65535_rows(orc, yt):

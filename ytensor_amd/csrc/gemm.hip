@@ -865,6 +865,175 @@ __global__ __launch_bounds__(1024) void gemv_nn_kernel(GemmArgs a) {
     store_from_f32<TO>(crow, n, v);
 }
 
+// fp32 GEMM on v_mfma_f32_16x16x4_f32 with DMA-staged tiles (configs[0], the
+// reference's sgemm_rowmajor, src/kernel/avx2/sgemm.inl:268-340, and its
+// transposed-B forms). Block tile BM x BN, k step BK = 32 (one 128-byte row of
+// fp32), an LDS ring of STAGES steps filled by global_load_lds (two in flight
+// ahead of the one being computed with 4 stages). Operands are swapped
+// (src0 = B^T fragment, src1 = A fragment) so lane l holds C[m = l % 16][n =
+// 4 g + 0..3], g = l / 16: one 16-byte store per output fragment.
+//   A tile [BM rows][8 chunks of 16 B]: chunk c of row r at c ^ (r & 7); the
+//     fragment of a 16-wide k block kb is one ds_read_b128 (chunk 4 kb + g) per
+//     lane feeding 4 MFMAs.
+//   B, NT (B = W^T, W [n][k] rows): the same layout as A.
+//   B, NN (row-major [k][n]): [BK rows][BN / 4 chunks], chunk c of k-row r at
+//     c ^ (((r >> 2) & 3) << 2); MFMA step j of lane group g reads k-row
+//     16 kb + 4 g + j, one ds_read_b32 of n = 16 fn + l % 16: the four groups'
+//     rows land in four bank ranges.
+// Rows of A / B past m / n re-read the last row (never stored); k % 32 == 0.
+template <int BM, int BN, int WM, int WN, bool NN, int STAGES>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_f32_kernel(GemmArgs a) {
+    constexpr int THREADS = 64 * WM * WN;
+    constexpr int BK = 32;
+    static_assert(STAGES >= 3, "the ring keeps two k steps in flight");
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int FM = WTM / 16, FN = WTN / 16;
+    constexpr int STA = BM * 8;                        // 16-byte chunks of an A stage
+    constexpr int STB = NN ? BK * (BN / 4) : BN * 8;   // ... of a B stage
+    constexpr int A_PT = STA / THREADS, B_PT = STB / THREADS;
+    static_assert(A_PT * THREADS == STA && B_PT * THREADS == STB, "tile / thread mismatch");
+    static_assert(!NN || BN >= 64, "the NN swizzle needs 16 chunks per k-row");
+    constexpr int PER = A_PT + B_PT;
+    __shared__ u32x4 sA[STAGES * STA];
+    __shared__ u32x4 sB[STAGES * STB];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+    const int bz = blockIdx.y;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const float* Ap = static_cast<const float*>(a.A) + bz * a.sa_b;
+    const float* Bp = static_cast<const float*>(a.B) + bz * a.sb_b;
+
+    // DMA element offsets within a k step (the base moves by BK along k)
+    int aoff[A_PT], boff[B_PT];  // source chunk of each DMA slot
+    int64_t arow[A_PT];
+#pragma unroll
+    for (int i = 0; i < A_PT; ++i) {
+        const int slot = i * THREADS + tid;
+        const int row = slot / 8, c = slot % 8;
+        aoff[i] = c ^ (row & 7);
+        arow[i] = (int64_t)min(m0 + row, a.m - 1) * a.rsa;
+    }
+    int64_t bbase[B_PT];
+#pragma unroll
+    for (int i = 0; i < B_PT; ++i) {
+        const int slot = i * THREADS + tid;
+        if constexpr (NN) {
+            constexpr int BCH = BN / 4;
+            const int row = slot / BCH, c = slot % BCH;   // k-row, n chunk
+            const int src = c ^ (((row >> 2) & 3) << 2);
+            const int nn = min(n0 + 4 * src, a.n - 4);    // n % 4 == 0 on this path
+            bbase[i] = (int64_t)row * a.rsb + nn;
+            boff[i] = 0;
+        } else {
+            const int row = slot / 8, c = slot % 8;       // n-row, k chunk
+            bbase[i] = (int64_t)min(n0 + row, a.n - 1) * a.csb;
+            boff[i] = (c ^ (row & 7)) * 4;
+        }
+    }
+    auto issue = [&](int ks) {
+        const int k0 = ks * BK;
+        u32x4* dA = sA + (ks % STAGES) * STA;
+        u32x4* dB = sB + (ks % STAGES) * STB;
+#pragma unroll
+        for (int i = 0; i < A_PT; ++i) dma16_async(Ap + arow[i] + k0 + aoff[i] * 4, &dA[i * THREADS + wave * 64]);
+#pragma unroll
+        for (int i = 0; i < B_PT; ++i) {
+            if constexpr (NN) dma16_async(Bp + bbase[i] + (int64_t)k0 * a.rsb, &dB[i * THREADS + wave * 64]);
+            else dma16_async(Bp + bbase[i] + k0 + boff[i], &dB[i * THREADS + wave * 64]);
+        }
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nks = a.k / BK;
+    constexpr int AHEAD = STAGES - 1;  // steps issued before the first one is computed
+#pragma unroll
+    for (int i = 0; i < AHEAD; ++i)
+        if (i < nks) issue(i);
+    for (int ks = 0; ks < nks; ++ks) {
+        // this thread's DMA of step ks has landed (the later steps' may still fly)
+        const int later = min(nks - 1 - ks, AHEAD - 1);
+        if (later >= 2) wait_vmcnt<2 * PER>();
+        else if (later == 1) wait_vmcnt<PER>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        if (ks + AHEAD < nks) issue(ks + AHEAD);
+        const u32x4* cA = sA + (ks % STAGES) * STA;
+        const u32x4* cB = sB + (ks % STAGES) * STB;
+        const float* cBf = reinterpret_cast<const float*>(cB);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x4 af[FM];
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm) {
+                const int row = wm * WTM + fm * 16 + r16;
+                af[fm] = __builtin_bit_cast(f32x4, cA[row * 8 + ((4 * kb + g) ^ (row & 7))]);
+            }
+            if constexpr (!NN) {
+                f32x4 bf[FN];
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    const int row = wn * WTN + fn * 16 + r16;
+                    bf[fn] = __builtin_bit_cast(f32x4, cB[row * 8 + ((4 * kb + g) ^ (row & 7))]);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn)
+                            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[fn][j], af[fm][j], acc[fm][fn], 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int krow = 16 * kb + 4 * g + j;  // (krow >> 2) & 3 == g
+                    float bf[FN];
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn) {
+                        const int nl = wn * WTN + fn * 16 + r16;  // n within the tile
+                        const int ch = (nl >> 2) ^ (g << 2);
+                        bf[fn] = cBf[krow * BN + ch * 4 + (nl & 3)];
+                    }
+#pragma unroll
+                    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn)
+                            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[fn], af[fm][j], acc[fm][fn], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // epilogue: lane holds C[m0 + wm WTM + 16 fm + l % 16][n0 + wn WTN + 16 fn + 4 g + i]
+    float* Cp = static_cast<float*>(a.C) + bz * a.sc_b;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+        const int m = m0 + wm * WTM + fm * 16 + r16;
+        if (m >= a.m) continue;
+        float* crow = Cp + (int64_t)m * a.rsc;
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const int n = n0 + wn * WTN + fn * 16 + 4 * g;
+            f32x4 v = acc[fm][fn] * a.alpha;
+            if (a.c_vec_ok && n + 3 < a.n) {
+                if (a.beta != 0.0f) v += a.beta * *reinterpret_cast<const f32x4*>(crow + n);
+                *reinterpret_cast<f32x4*>(crow + n) = v;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (n + i < a.n) crow[n + i] = a.beta != 0.0f ? v[i] + a.beta * crow[n + i] : v[i];
+            }
+        }
+    }
+}
+
 // Any-stride fallback: one output per thread, fp32 accumulation in k order.
 struct GenericArgs {
     const void* A;
@@ -1080,6 +1249,29 @@ int gemm_typed(int batch, int m, int n, int k, const void* A, int64_t sa_b, int6
                 return status_of(launch_dma<T, TO>(g, true, batch, s));
             gemm_skinny_nn_kernel<T, TO><<<dim3((n + 63) / 64, batch), 64 * SKINNY_WAVES, 0, s>>>(g);
             return status_of(hipGetLastError());
+        }
+        if constexpr (std::is_same_v<T, F32> && std::is_same_v<TO, F32>) {
+            // fp32 on the DMA-staged fp32 MFMA kernel: k a multiple of its 32-wide
+            // step, 16-byte aligned rows of A and of B (NT) or B's k-rows (NN)
+            const bool f_nn = nn && (rsb % 4) == 0 && (sb_b % 4) == 0 && aligned(B, 16) && n >= 4;
+            if (k % 32 == 0 && (nt || f_nn)) {
+                auto ntiles = [&](int bm, int bn) { return (int64_t)((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch; };
+                const bool big = ntiles(128, 128) >= 512;
+                GemmArgs f = g;
+                f.tiles_m = (m + (big ? 127 : 63)) / (big ? 128 : 64);
+                f.tiles_n = (n + (big ? 127 : 63)) / (big ? 128 : 64);
+                const dim3 grid(f.tiles_m * f.tiles_n, batch);
+                // 1024^3 (256 tiles of 64 x 64): 8 waves of 32 x 16 and a 4-step ring,
+                // 99 TFLOP/s NN; 4 waves or 3 steps 86-98, 32 x 64 or 64 x 128 tiles <= 92
+                if (big) {
+                    if (f_nn) gemm_f32_kernel<128, 128, 2, 4, true, 3><<<grid, 512, 0, s>>>(f);
+                    else gemm_f32_kernel<128, 128, 2, 4, false, 3><<<grid, 512, 0, s>>>(f);
+                } else {
+                    if (f_nn) gemm_f32_kernel<64, 64, 2, 4, true, 4><<<grid, 512, 0, s>>>(f);
+                    else gemm_f32_kernel<64, 64, 2, 4, false, 4><<<grid, 512, 0, s>>>(f);
+                }
+                return status_of(hipGetLastError());
+            }
         }
         // DMA-staged fast path: whole k steps, 16-byte aligned rows everywhere.
         const bool dma_k = (k % (8 * VEC)) == 0;
