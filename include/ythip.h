@@ -97,7 +97,7 @@ int ythip_gemm(int dtype_in, int dtype_out, int batch, int m, int n, int k,
  * (include/kernel/avx2/flash_attention.hpp:21-69). Supported: d == dv in {64, 128}.
  * q_len == 1 (the reference's decode branch, src/kernel/avx2/flash_attention.inl:
  * 469-499) runs the split-K decode kernel for every mask kind and bias when
- * d == dv in {64, 128}, Hq / Hkv in {1, 2, 4, 8}, the head dim is contiguous
+ * d == dv in {64, 128}, Hq / Hkv in {1, 2, 4, 5, 8}, the head dim is contiguous
  * and K / V rows are 16-byte aligned; without a workspace (this call) that is
  * one split per (kv head, batch) -- ythip_attn_prefill_ws with
  * ythip_attn_sdpa_workspace_size bytes runs the full split count.

@@ -218,8 +218,7 @@ int main(int argc, char** argv) {
                                                                  sdpaBackend::FLASH_HIP));
     }
     {
-        // repeat_kv by 5 (Qwen3-14B's 40 / 8 heads): a group size the decode kernel
-        // does not take runs the prefill kernels
+        // repeat_kv by 5 (Qwen3-14B's 40 / 8 heads) on the decode kernel
         YTensor<float, 4>::seed(22);
         auto K5 = to_bf16(YTensor<float, 4>::randn(1, 8, 512, 128));
         auto V5 = to_bf16(YTensor<float, 4>::randn(1, 8, 512, 128));

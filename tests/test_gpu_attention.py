@@ -527,6 +527,28 @@ def test_decode_ragged_lengths(orc, yt, dtype):
     _check(orc, g.reshape(r.shape), r, dtype, f"ragged {dtype}")
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_decode_group_of_five_vs_oracle(orc, yt, dtype):
+    """GQA group 5 (Qwen3-14B's 40 q / 8 kv heads) on the split-K decode kernel,
+    ragged per-sequence lengths, against the reference's flash_attention."""
+    B, Hq, Hkv, ctx, D = 2, 40, 8, 700, 128
+    lens = np.array([700, 333], np.int32)
+    rng = np.random.default_rng(55)
+    Q = rng.standard_normal((B, Hq, 1, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, ctx, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, ctx, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, dtype)
+    Kd, Kh = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    g = host_f32(yt.decode_attention(Qd, Kd, Vd, kv_len=torch.from_numpy(lens).cuda()))
+    r = np.zeros_like(Q)
+    for b in range(B):
+        L = int(lens[b])
+        r[b] = orc.sdpa_gqa(Qh[b:b + 1], np.ascontiguousarray(Kh[b:b + 1, :, :L]),
+                            np.ascontiguousarray(Vh[b:b + 1, :, :L]), 0.0, True)[0]
+    _check(orc, g.reshape(r.shape), r, dtype, f"decode G=5 {dtype}")
+
+
 def test_decode_equals_last_prefill_row(orc, yt):
     """Decode of the last query == the last row of causal prefill (same inputs)."""
     rng = np.random.default_rng(12)
@@ -561,7 +583,7 @@ def test_single_visible_key_and_zero_query(orc, yt):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
-@pytest.mark.parametrize("Hq,Hkv,d", [(16, 8, 128), (8, 8, 64), (16, 4, 128), (32, 4, 64)])
+@pytest.mark.parametrize("Hq,Hkv,d", [(16, 8, 128), (8, 8, 64), (16, 4, 128), (32, 4, 64), (40, 8, 128)])
 def test_decode_attention_rope_equals_unfused(orc, yt, dtype, Hq, Hkv, d):
     """ythip_attn_decode_rope == ythip_rmsnorm_rope (S = 1, dev_state) followed
     by ythip_attn_decode (kv_len = the record's KV_LEN): the same bits in the

@@ -171,7 +171,7 @@ def test_decode_predicate(orc, outputs):
     check16(orc, outputs["dec_pred"].reshape(1, 16, 1, 128), r, "bf16", True, "C++ decode CausalMask{512}")
 
 
-def test_decode_group_of_five_falls_back(orc, outputs):
+def test_decode_group_of_five(orc, outputs):
     orc.seed(22)
     K = _bf16(orc, orc.randn(1, 8, 512, 128))
     V = _bf16(orc, orc.randn(1, 8, 512, 128))

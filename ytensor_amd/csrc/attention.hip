@@ -2013,6 +2013,7 @@ hipError_t launch_decode_d(const DecodeArgs& a, int G, hipStream_t s) {
         case 1: return launch_decode_g<T, D, 1>(a, s);
         case 2: return launch_decode_g<T, D, 2>(a, s);
         case 4: return launch_decode_g<T, D, 4>(a, s);
+        case 5: return launch_decode_g<T, D, 5>(a, s);  // e.g. Qwen3-14B, 40 q / 8 kv heads
         case 8: return launch_decode_g<T, D, 8>(a, s);
         default: return hipErrorInvalidValue;
     }
@@ -2027,7 +2028,7 @@ hipError_t launch_decode(const DecodeArgs& a, int D, int G, hipStream_t s) {
 // The q_len == 1 branch of flash_attention (src/kernel/avx2/flash_attention.inl:
 // 469-499): every single-query call -- no mask, causal, diagonal predicate,
 // bool mask, bias -- goes to the split-K decode kernel when its layout fits it
-// (d == dv in {64, 128}, Hq / Hkv in {1, 2, 4, 8}, contiguous head dim,
+// (d == dv in {64, 128}, Hq / Hkv in {1, 2, 4, 5, 8}, contiguous head dim,
 // 16-byte aligned K / V rows). Split-K partials go to the caller's workspace:
 // as many splits as it holds, up to decode_splits (none: one split per
 // (kv head, batch), written straight to O). Returns -1 when the call does not
@@ -2036,7 +2037,7 @@ int decode_route(int dtype, const AttnArgs& p, int mask_kind, const uint8_t* mas
                  void* workspace, size_t ws_bytes, hipStream_t s) {
     if (p.Sq != 1 || p.Skv <= 0 || p.D != p.Dv || (p.D != 64 && p.D != 128)) return -1;
     const int G = p.Hq / p.Hkv;
-    if (G != 1 && G != 2 && G != 4 && G != 8) return -1;
+    if (G != 1 && G != 2 && G != 4 && G != 5 && G != 8) return -1;
     if (p.qs3 != 1 || p.ks3 != 1 || p.vs3 != 1 || p.os3 != 1) return -1;
     const int es = dtype == YTHIP_F32 ? 4 : 2, ev = 16 / es;
     if (!al(p.K, 16) || !al(p.V, 16) || !al(p.Q, es) || !al(p.O, es)) return -1;
@@ -2191,8 +2192,8 @@ __attribute__((visibility("default"))) int ythip_attn_decode(int dtype, int B, i
     if (Hkv == 0 || Hq % Hkv != 0) return fail(YTHIP_EINVAL, "ythip_attn_decode: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
     const int G = Hq / Hkv;
     if (d != 64 && d != 128) return fail(YTHIP_EUNSUPPORTED, "ythip_attn_decode: head dim %d (supported: 64, 128)", d);
-    if (G != 1 && G != 2 && G != 4 && G != 8)
-        return fail(YTHIP_EUNSUPPORTED, "ythip_attn_decode: group size %d (supported: 1, 2, 4, 8)", G);
+    if (G != 1 && G != 2 && G != 4 && G != 5 && G != 8)
+        return fail(YTHIP_EUNSUPPORTED, "ythip_attn_decode: group size %d (supported: 1, 2, 4, 5, 8)", G);
     if (!Q || !Kc || !Vc || !O || !q_str || !kv_str || !o_str)
         return fail(YTHIP_EINVAL, "ythip_attn_decode: NULL tensor or stride array");
     const size_t need = ythip_attn_decode_workspace_size(B, Hq, max_ctx > 0 ? max_ctx : 1, d);
@@ -2311,8 +2312,8 @@ __attribute__((visibility("default"))) int ythip_attn_decode_rope(
     if (Hkv == 0 || Hq % Hkv != 0) return fail(YTHIP_EINVAL, "%s: Hq=%d not a multiple of Hkv=%d", who, Hq, Hkv);
     const int G = Hq / Hkv;
     if (d != 64 && d != 128) return fail(YTHIP_EUNSUPPORTED, "%s: head dim %d (supported: 64, 128)", who, d);
-    if (G != 1 && G != 2 && G != 4 && G != 8)
-        return fail(YTHIP_EUNSUPPORTED, "%s: group size %d (supported: 1, 2, 4, 8)", who, G);
+    if (G != 1 && G != 2 && G != 4 && G != 5 && G != 8)
+        return fail(YTHIP_EUNSUPPORTED, "%s: group size %d (supported: 1, 2, 4, 5, 8)", who, G);
     if (!qkv || !dev_state || !Kc || !Vc || !kv_str || (O && !o_str) || (cos_tab == nullptr) != (sin_tab == nullptr))
         return fail(YTHIP_EINVAL, "%s: NULL pointer", who);
     if (cos_tab != nullptr && (tab_rows <= 0 || ld_tab < d)) return fail(YTHIP_EINVAL, "%s: bad table args", who);
