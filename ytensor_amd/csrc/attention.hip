@@ -811,24 +811,47 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
         koff[i] = row * (int)a.ks2 + (ps ^ (row & KMASK)) * 8;
         voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
     }
-    // rows past the end re-read the last key (their scores are masked)
+    // Whole blocks: the DMA goes from the block's scalar base plus this lane's
+    // fixed 32-bit byte offset (no VALU address work inside the loop); the LDS
+    // destinations of the two stages are scalar too. A partial last block
+    // clamps its rows past the end to the last key (their scores are masked).
+    uint32_t kbo[PT], vbo[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        kbo[i] = (uint32_t)koff[i] * (uint32_t)sizeof(raw);
+        vbo[i] = (uint32_t)voff[i] * (uint32_t)sizeof(raw);
+    }
+    const uint32_t ldsK0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sK[gw * 64]);
+    const uint32_t ldsV0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sV[gw * 64]);
     auto issue_k = [&](int j, uint32_t e) {
         const int k0 = kblock(j, e) * BKV;
-        u32x4* dK = sK + (j & 1) * STG;
         const raw* kbase = Kp + (int64_t)k0 * a.ks2;
+        if (k0 + BKV <= a.Skv) {
+            const uint32_t l0 = ldsK0 + (uint32_t)((j & 1) * STG) * 16u;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) dma16_soff(kbase, kbo[i], l0 + (uint32_t)(i * GT) * 16u);
+            return;
+        }
+        u32x4* dK = sK + (j & 1) * STG;
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
-            const int sh = (k0 + BKV <= a.Skv) ? 0 : min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
+            const int sh = min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
             dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * GT + gw * 64]);
         }
     };
     auto issue_v = [&](int j, uint32_t e) {
         const int k0 = kblock(j, e) * BKV;
-        u32x4* dV = sV + (j & 1) * STG;
         const raw* vbase = Vp + (int64_t)k0 * a.vs2;
+        if (k0 + BKV <= a.Skv) {
+            const uint32_t l0 = ldsV0 + (uint32_t)((j & 1) * STG) * 16u;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) dma16_soff(vbase, vbo[i], l0 + (uint32_t)(i * GT) * 16u);
+            return;
+        }
+        u32x4* dV = sV + (j & 1) * STG;
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
-            const int sh = (k0 + BKV <= a.Skv) ? 0 : min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
+            const int sh = min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
             dma16_async(vbase + voff[i] + sh * (int)a.vs2, &dV[i * GT + gw * 64]);
         }
     };
