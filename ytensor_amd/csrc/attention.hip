@@ -216,17 +216,17 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Per-thread DMA offsets (elements) within a block; the block base moves by BKV keys.
-    int koff[PT], voff[PT];  // the host guarantees 64 rows of K and V span < 2^31 elements
-    int krow[PT];
-#pragma unroll
-    for (int i = 0; i < PT; ++i) {
-        const int slot = i * THREADS + wave * 64 + lane;
-        const int row = slot / KCH, ps = slot % KCH;
-        krow[i] = row;
-        koff[i] = row * (int)a.ks2 + (ps ^ (row & KMASK)) * 8;
-        voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
-    }
+    // This thread's DMA slots within a stage: row and swizzled chunk, as element
+    // offsets from the stage's first key (64-row spans are < 2^31 elements).
+    auto slot_row = [&](int i) { return (i * THREADS + wave * 64 + lane) / KCH; };
+    auto koff = [&](int i) {
+        const int slot = i * THREADS + wave * 64 + lane, row = slot / KCH, ps = slot % KCH;
+        return row * (int)a.ks2 + (ps ^ (row & KMASK)) * 8;
+    };
+    auto voff = [&](int i) {
+        const int slot = i * THREADS + wave * 64 + lane, row = slot / KCH, ps = slot % KCH;
+        return row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
+    };
     auto issue_mask = [&](int kb) {
         if constexpr (MODE == 3) {
             const int k0 = kb * SBKV;
@@ -243,6 +243,19 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
             }
         }
     };
+    // Whole stages whose lane offsets fit 31 bits (every layout but huge row
+    // strides) go from the stage's scalar base plus this lane's fixed byte
+    // offset, kept in registers: no VALU address work per DMA. Other stages
+    // recompute the offsets.
+    const bool soff = (int64_t)SBKV * (a.ks2 > a.vs2 ? a.ks2 : a.vs2) * (int64_t)sizeof(raw) < (1ll << 31);
+    uint32_t kbo[PT], vbo[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        kbo[i] = (uint32_t)koff(i) * (uint32_t)sizeof(raw);
+        vbo[i] = (uint32_t)voff(i) * (uint32_t)sizeof(raw);
+    }
+    const uint32_t ldsK0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sK[wave * 64]);
+    const uint32_t ldsV0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sV[wave * 64]);
     auto issue = [&](int kb) {
         const int k0 = kb * SBKV;
         u32x4* dK = sK + (kb & 1) * STG;
@@ -250,19 +263,22 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
         if (!SKIP) issue_mask(kb);
         const raw* kbase = Kp + (int64_t)k0 * a.ks2;
         const raw* vbase = Vp + (int64_t)k0 * a.vs2;
-        if (k0 + SBKV <= a.Skv) {
+        if (k0 + SBKV <= a.Skv && soff) {
+            const uint32_t lk = ldsK0 + (uint32_t)((kb & 1) * STG) * 16u;
+            const uint32_t lv = ldsV0 + (uint32_t)((kb & 1) * STG) * 16u;
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
-                dma16_async(kbase + koff[i], &dK[i * THREADS + wave * 64]);
-                dma16_async(vbase + voff[i], &dV[i * THREADS + wave * 64]);
+                dma16_soff(kbase, kbo[i], lk + (uint32_t)(i * THREADS) * 16u);
+                dma16_soff(vbase, vbo[i], lv + (uint32_t)(i * THREADS) * 16u);
             }
         } else {
-            // tail block: rows past the end re-read the last key (never used)
+            // a tail stage's rows past the end re-read the last key (never used)
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
-                const int sh = min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
-                dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * THREADS + wave * 64]);
-                dma16_async(vbase + voff[i] + sh * (int)a.vs2, &dV[i * THREADS + wave * 64]);
+                const int row = slot_row(i);
+                const int sh = k0 + SBKV <= a.Skv ? 0 : min(k0 + row, a.Skv - 1) - k0 - row;
+                dma16_async(kbase + koff(i) + sh * (int)a.ks2, &dK[i * THREADS + wave * 64]);
+                dma16_async(vbase + voff(i) + sh * (int)a.vs2, &dV[i * THREADS + wave * 64]);
             }
         }
     };
@@ -800,26 +816,28 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // DMA slots of this thread within its wave group
+    // DMA slots of this thread within its wave group: row and swizzled chunk, as
+    // element offsets from the block's first key
     const int gw = (tid & (GT - 1)) >> 6;
-    int koff[PT], voff[PT], krow[PT];
-#pragma unroll
-    for (int i = 0; i < PT; ++i) {
-        const int slot = i * GT + gw * 64 + lane;
-        const int row = slot / KCH, ps = slot % KCH;
-        krow[i] = row;
-        koff[i] = row * (int)a.ks2 + (ps ^ (row & KMASK)) * 8;
-        voff[i] = row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
-    }
+    auto slot_row = [&](int i) { return (i * GT + gw * 64 + lane) / KCH; };
+    auto koff = [&](int i) {
+        const int slot = i * GT + gw * 64 + lane, row = slot / KCH, ps = slot % KCH;
+        return row * (int)a.ks2 + (ps ^ (row & KMASK)) * 8;
+    };
+    auto voff = [&](int i) {
+        const int slot = i * GT + gw * 64 + lane, row = slot / KCH, ps = slot % KCH;
+        return row * (int)a.vs2 + ((ps >> 1) ^ (row & BMASK)) * 16 + (ps & 1) * 8;
+    };
     // Whole blocks: the DMA goes from the block's scalar base plus this lane's
-    // fixed 32-bit byte offset (no VALU address work inside the loop); the LDS
+    // fixed 32-bit byte offset (no VALU address work inside the loop; 64 rows
+    // at a row stride below 2^24 elements span < 2^31 bytes); the LDS
     // destinations of the two stages are scalar too. A partial last block
     // clamps its rows past the end to the last key (their scores are masked).
     uint32_t kbo[PT], vbo[PT];
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
-        kbo[i] = (uint32_t)koff[i] * (uint32_t)sizeof(raw);
-        vbo[i] = (uint32_t)voff[i] * (uint32_t)sizeof(raw);
+        kbo[i] = (uint32_t)koff(i) * (uint32_t)sizeof(raw);
+        vbo[i] = (uint32_t)voff(i) * (uint32_t)sizeof(raw);
     }
     const uint32_t ldsK0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sK[gw * 64]);
     const uint32_t ldsV0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sV[gw * 64]);
@@ -835,8 +853,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
         u32x4* dK = sK + (j & 1) * STG;
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
-            const int sh = min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
-            dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * GT + gw * 64]);
+            const int row = slot_row(i);
+            const int sh = min(k0 + row, a.Skv - 1) - k0 - row;
+            dma16_async(kbase + koff(i) + sh * (int)a.ks2, &dK[i * GT + gw * 64]);
         }
     };
     auto issue_v = [&](int j, uint32_t e) {
@@ -851,8 +870,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
         u32x4* dV = sV + (j & 1) * STG;
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
-            const int sh = min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
-            dma16_async(vbase + voff[i] + sh * (int)a.vs2, &dV[i * GT + gw * 64]);
+            const int row = slot_row(i);
+            const int sh = min(k0 + row, a.Skv - 1) - k0 - row;
+            dma16_async(vbase + voff(i) + sh * (int)a.vs2, &dV[i * GT + gw * 64]);
         }
     };
 
@@ -1218,28 +1238,51 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
         for (int bb = 0; bb < NB; ++bb) qf[bb] = *reinterpret_cast<const f32x4*>(qp + 16 * bb) * a.scale_log2;
     }
 
-    // DMA offsets (elements) within a block; the block base moves by BKV rows
-    int koff[PT], voff[PT], krow[PT];
+    // DMA slots (row and swizzled chunk) as element offsets from the block's first key
+    auto slot_row = [&](int i) { return (i * 64 * NW + wave * 64 + lane) / KCH; };
+    auto koff = [&](int i) {
+        const int slot = i * 64 * NW + wave * 64 + lane, row = slot / KCH, c = slot % KCH;
+        return row * (int)a.ks2 + (c ^ (row & 7)) * 4;
+    };
+    auto voff = [&](int i) {
+        const int slot = i * 64 * NW + wave * 64 + lane, row = slot / KCH, c = slot % KCH;
+        return row * (int)a.vs2 + (c ^ (((row >> 2) & 3) << 2)) * 4;
+    };
+    // Whole blocks whose lane offsets fit 31 bits go from the block's scalar
+    // base plus this lane's fixed byte offset, kept in registers: no VALU
+    // address work per DMA. Other blocks recompute the offsets.
+    const bool soff = (int64_t)BKV * (a.ks2 > a.vs2 ? a.ks2 : a.vs2) * 4 < (1ll << 31);
+    uint32_t kbo[PT], vbo[PT];
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
-        const int slot = i * 64 * NW + wave * 64 + lane;
-        const int row = slot / KCH, c = slot % KCH;
-        krow[i] = row;
-        koff[i] = row * (int)a.ks2 + (c ^ (row & 7)) * 4;
-        voff[i] = row * (int)a.vs2 + (c ^ (((row >> 2) & 3) << 2)) * 4;
+        kbo[i] = (uint32_t)koff(i) * 4u;
+        vbo[i] = (uint32_t)voff(i) * 4u;
     }
+    const uint32_t ldsK0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sK[wave * 64]);
+    const uint32_t ldsV0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sV[wave * 64]);
     auto issue = [&](int kb) {
         const int k0 = kb * BKV;
         u32x4* dK = sK + (kb & 1) * STG;
         u32x4* dV = sV + (kb & 1) * STG;
         const float* kbase = Kp + (int64_t)k0 * a.ks2;
         const float* vbase = Vp + (int64_t)k0 * a.vs2;
+        if (k0 + BKV <= a.Skv && soff) {
+            const uint32_t lk = ldsK0 + (uint32_t)((kb & 1) * STG) * 16u;
+            const uint32_t lv = ldsV0 + (uint32_t)((kb & 1) * STG) * 16u;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                dma16_soff(kbase, kbo[i], lk + (uint32_t)(i * 64 * NW) * 16u);
+                dma16_soff(vbase, vbo[i], lv + (uint32_t)(i * 64 * NW) * 16u);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
             // rows past the end re-read the last key (masked, never used)
-            const int sh = min(k0 + krow[i], a.Skv - 1) - k0 - krow[i];
-            dma16_async(kbase + koff[i] + sh * (int)a.ks2, &dK[i * 64 * NW + wave * 64]);
-            dma16_async(vbase + voff[i] + sh * (int)a.vs2, &dV[i * 64 * NW + wave * 64]);
+            const int row = slot_row(i);
+            const int sh = min(k0 + row, a.Skv - 1) - k0 - row;
+            dma16_async(kbase + koff(i) + sh * (int)a.ks2, &dK[i * 64 * NW + wave * 64]);
+            dma16_async(vbase + voff(i) + sh * (int)a.vs2, &dV[i * 64 * NW + wave * 64]);
         }
     };
 
