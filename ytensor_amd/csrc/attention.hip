@@ -804,11 +804,15 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     float m[QT];
     bool mset[QT];
     f32x4 lsum[QT];
+    // per row: the block max above which the reference point moves (any
+    // visible key before the first move, LAZY after)
+    float thr[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         m[qt] = 0.f;
         mset[qt] = false;
         lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        thr[qt] = -INFINITY;
     }
     f32x4 o[QT][DT];
 #pragma unroll
@@ -941,7 +945,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                 constexpr int ks = u / NKT, kt = u % NKT;
                 if constexpr (u + PF < NU) fr[(u + PF) % (PF + 1)] = ldk((u + PF) / NKT, (u + PF) % NKT);
 #pragma unroll
-                for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma_chunk(T{}, fr[u % (PF + 1)], qf[qt][ks], s[qt][kt]);
+                for (int qt = 0; qt < QT; ++qt)
+                    s[qt][kt] = mfma_chunk(T{}, fr[u % (PF + 1)], qf[qt][ks], s[qt][kt]);
                 __builtin_amdgcn_sched_barrier(0);
             });
         }
@@ -1007,7 +1012,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                 for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, s[qt][kt][r]);
             lmax[qt] = mx;
             // a row's reference point moves iff one of its lanes sees this
-            trig = trig || (mset[qt] ? (mx > LAZY) : (mx != -INFINITY));
+            trig = trig || mx > thr[qt];
         }
         auto exps = [&]() {
 #pragma unroll
@@ -1039,6 +1044,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
                 const float alpha = (move && mset[qt]) ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
                 m[qt] += delta;
                 mset[qt] = mset[qt] || move;
+                thr[qt] = mset[qt] ? LAZY : -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
