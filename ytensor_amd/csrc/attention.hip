@@ -204,11 +204,15 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
     float m[QT];
     bool mset[QT];
     f32x4 lsum[QT];
+    // per row: the block max above which the reference point moves (any
+    // visible key before the first move, LAZY after)
+    float thr[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         m[qt] = 0.f;
         mset[qt] = false;
         lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        thr[qt] = -INFINITY;
     }
     f32x4 o[QT][DT];
 #pragma unroll
@@ -382,7 +386,7 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
             lmax[qt] = mx;
             // the reference point of a row moves (set on its first visible block,
             // afterwards only for a block max far above it) iff one of its lanes sees this
-            trig = trig || (mset[qt] ? (mx > LAZY) : (mx != -INFINITY));
+            trig = trig || mx > thr[qt];
         }
         auto exps = [&]() {
 #pragma unroll
@@ -415,6 +419,7 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
                 const float alpha = (move && mset[qt]) ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
                 m[qt] += delta;
                 mset[qt] = mset[qt] || move;
+                thr[qt] = mset[qt] ? LAZY : -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
