@@ -397,6 +397,36 @@ def test_prefill_strided_views(orc, yt):
     check16(orc, g, r, "bf16", True, "strided")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_prefill_huge_key_row_stride(orc, yt, dtype):
+    """K rows 2^23 + 8 (bf16) / 2^23 + 4 (fp32) elements apart: one stage of K
+    spans more than 2^31 bytes, so the MFMA prefill kernels take their DMA
+    path with per-stage offsets instead of the fixed 32-bit lane offsets. The
+    output must equal the contiguous-K call bit for bit, and the oracle."""
+    S = 256 if dtype == "bf16" else 128
+    ks2 = (1 << 23) + (8 if dtype == "bf16" else 4)
+    rng = np.random.default_rng(23)
+    Q = rng.standard_normal((1, 2, S, 128)).astype(np.float32)
+    K = rng.standard_normal((1, 1, S, 128)).astype(np.float32)
+    V = rng.standard_normal((1, 1, S, 128)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, dtype)
+    Kd, Kh = make_input(orc, K, dtype)
+    Vd, Vh = make_input(orc, V, dtype)
+    buf = torch.zeros((S - 1) * ks2 + 128, dtype=Kd.dtype, device=Kd.device)
+    Kw = torch.as_strided(buf, (1, 1, S, 128), (0, 0, ks2, 1))
+    Kw.copy_(Kd)
+    esz = 2 if dtype == "bf16" else 4
+    rows = 128 if dtype == "bf16" else 64  # K rows per DMA stage of the kernel this shape runs
+    assert rows * ks2 * esz >= 1 << 31
+    g_wide = host_f32(yt.scaled_dot_product_attention(Qd, Kw, Vd, 0.0, mask="causal"))
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, 0.0, mask="causal"))
+    del Kw, buf
+    torch.cuda.empty_cache()
+    assert np.array_equal(g_wide, g)
+    r = orc.sdpa_gqa(Qh, Kh, Vh, 0.0, True)
+    _check(orc, g, r, dtype, f"huge key row stride {dtype}")
+
+
 def _decode_inputs(orc, B, ctx, seed=2):
     orc.seed(seed)
     K = orc.randn(B, 8, ctx, 128)
