@@ -1198,8 +1198,10 @@ __global__ __launch_bounds__(64) void attn_rowwise(AttnArgs a) {
 //     probability j: lane l accumulates O[query r][d = 16t + 4g + i], so the
 //     rescale by 2^(m_old - m_new) is per lane, and the softmax denominator is a
 //     per-lane partial summed over the query's 4 lanes at the end.
-//   LDS: K chunk c (16 bytes) of a row stored at c ^ (key & 7) -- each score
-//     step is one conflict-free ds_read_b128; V chunk c at c ^ (((key>>2)&3)<<2)
+//   LDS: K chunk c (16 bytes) of a row stored at c ^ (key & 15) -- the 16 keys
+//     a quarter-wave's ds_read_b128 serves land on 16 distinct 16-byte bank
+//     groups (with key & 7 they share 8: a 2-way conflict on every score
+//     step); V chunk c at c ^ (((key>>2)&3)<<2)
 //     -- the four lane groups' ds_read_b32 of four different keys fall in four
 //     bank ranges.
 // MODE 0: no mask; 1: causal / diagonal (key j visible to query i iff j <= i +
@@ -1253,7 +1255,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
     auto slot_row = [&](int i) { return (i * 64 * NW + wave * 64 + lane) / KCH; };
     auto koff = [&](int i) {
         const int slot = i * 64 * NW + wave * 64 + lane, row = slot / KCH, c = slot % KCH;
-        return row * (int)a.ks2 + (c ^ (row & 7)) * 4;
+        return row * (int)a.ks2 + (c ^ (row & 15)) * 4;
     };
     auto voff = [&](int i) {
         const int slot = i * 64 * NW + wave * 64 + lane, row = slot / KCH, c = slot % KCH;
@@ -1337,7 +1339,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
                 const int key = kt * 16 + r;
-                kf[kt] = __builtin_bit_cast(f32x4, cK[key * KCH + ((4 * bb + g) ^ (key & 7))]);
+                kf[kt] = __builtin_bit_cast(f32x4, cK[key * KCH + ((4 * bb + g) ^ (key & 15))]);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
