@@ -84,12 +84,19 @@ def test_config3_causal_prefill_fp32_mfma(orc, yt, S):
 
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("kind", ["none", "diag", "bool", "bias", "bool_bias"])
-def test_prefill_fp32_mfma_mask_kinds(orc, yt, D, kind):
+@pytest.mark.parametrize("grid", ["split", "whole"])
+def test_prefill_fp32_mfma_mask_kinds(orc, yt, D, kind, grid):
     """The fp32 MFMA kernel's mask forms against the reference's flash_attention:
-    ragged q / kv lengths (not multiples of the 128-query and 64-key blocks),
-    GQA 4:1, B = 2; a diagonal predicate with a negative offset (leading rows see
-    no key -> zeros), a bool mask with a fully masked row, an additive bias."""
-    B, Hq, Hkv, Sq, Skv = 2, 8, 2, 201, 333
+    ragged q / kv lengths (not multiples of the query and 64-key blocks), GQA
+    4:1, B = 2; a diagonal predicate with a negative offset (leading rows see no
+    key -> zeros), a bool mask with a fully masked row, an additive bias. "split":
+    a grid short of two 128-query blocks per CU, which runs 64-query blocks with
+    each staged key block split between the two wave groups; "whole": 640
+    128-query blocks, one wave group per query block."""
+    if grid == "split":
+        B, Hq, Hkv, Sq, Skv = 2, 8, 2, 201, 333
+    else:
+        B, Hq, Hkv, Sq, Skv = 2, 64, 16, 520, 601
     rng = np.random.default_rng(D + len(kind))
     Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
     K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)

@@ -1209,9 +1209,15 @@ __global__ __launch_bounds__(64) void attn_rowwise(AttnArgs a) {
 // the heaviest query blocks launch first); 2: byte mask and / or bias read per
 // element. Keys at or past kv_len are masked; a query with no visible key
 // gets zeros (flash_attention.inl:241-244, 327-331).
-template <int D, int MODE>
+// KS = 2 (short prompts): 64-query blocks, twice the workgroups. Waves w and
+// w + 4 own the same 16 queries; wave group g = w / 4 takes keys [32 g, 32 g +
+// 32) of every staged block, and at the end group 1 hands its O, m and l to
+// group 0 through LDS, which merges them with the log-sum-exp rule.
+template <int D, int MODE, int KS = 1>
 __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
-    constexpr int NW = 8, BQ = 16 * NW, BKV = 64;
+    static_assert(KS == 1 || KS == 2, "key split 1 or 2");
+    constexpr int NW = 8, BQ = 16 * NW / KS, BKV = 64;
+    constexpr int NKT = 4 / KS;         // 16-key tiles of a block per wave
     constexpr int KCH = D / 4;          // 16-byte chunks per K / V row
     constexpr int STG = BKV * KCH;      // chunks per stage of K (or V)
     constexpr int PT = STG / (64 * NW); // DMA chunks per thread per stage
@@ -1231,7 +1237,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
     const float* Kp = static_cast<const float*>(a.K) + b * a.ks0 + kvh * a.ks1;
     const float* Vp = static_cast<const float*>(a.V) + b * a.vs0 + kvh * a.vs1;
     float* Op = static_cast<float*>(a.O) + b * a.os0 + h * a.os1;
-    const int q0 = qb * BQ + wave * 16;  // this wave's first query
+    const int wl = KS == 2 ? (wave & 3) : wave;  // row group of this wave
+    const int kofs = KS == 2 ? (wave >> 2) * 32 : 0;  // first key of a block this wave takes
+    const int q0 = qb * BQ + wl * 16;  // this wave's first query
     const int qrow = q0 + r;             // this lane's query
     const bool wave_rows = q0 < a.Sq;
 
@@ -1312,48 +1320,48 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
         const int k0 = kb * BKV;
         if (!wave_rows) continue;
         if constexpr (MODE == 1) {
-            if (k0 > q0 + 15 + a.diag_off) continue;  // past every row of this wave
+            if (k0 + kofs > q0 + 15 + a.diag_off) continue;  // past every row of this wave
         }
         // per-element inputs of MODE 2, issued before the score MFMAs
-        uint8_t mk[4][4];
-        float bv[4][4];
+        uint8_t mk[NKT][4];
+        float bv[NKT][4];
         if constexpr (MODE == 2) {
             const int qr = min(qrow, a.Sq - 1);
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int key = min(k0 + kt * 16 + 4 * g + i, a.Skv - 1);
+                    const int key = min(k0 + kofs + kt * 16 + 4 * g + i, a.Skv - 1);
                     mk[kt][i] = a.mask != nullptr ? a.mask[(int64_t)qr * a.mask_ld + key] : (uint8_t)1;
                     bv[kt][i] = a.bias != nullptr ? a.bias[(int64_t)qr * a.brs + (int64_t)key * a.bcs] * LOG2E : 0.f;
                 }
         }
         const u32x4* cK = sK + (kb & 1) * STG;
         const float* cV = reinterpret_cast<const float*>(sV + (kb & 1) * STG);
-        f32x4 s[4];
+        f32x4 s[NKT];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < NKT; ++kt) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb) {
-            f32x4 kf[4];
+            f32x4 kf[NKT];
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                const int key = kt * 16 + r;
+            for (int kt = 0; kt < NKT; ++kt) {
+                const int key = kofs + kt * 16 + r;
                 kf[kt] = __builtin_bit_cast(f32x4, cK[key * KCH + ((4 * bb + g) ^ (key & 15))]);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
+                for (int kt = 0; kt < NKT; ++kt)
                     s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kt][j], qf[bb][j], s[kt], 0, 0, 0);
         }
         // visibility, the block's row maximum, probabilities
         float mx = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int key = k0 + kt * 16 + 4 * g + i;
+                const int key = k0 + kofs + kt * 16 + 4 * g + i;
                 bool vis = key < a.Skv;
                 if constexpr (MODE == 1) vis = vis && key <= qrow + a.diag_off;
                 float x = s[kt][i];
@@ -1370,7 +1378,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
         const float alpha = exp2f(m - m_use);  // 0 while no key was visible
         float psum = 0.f;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float p = exp2f(s[kt][i] - m_use);  // masked: exp2(-inf) = 0
@@ -1381,12 +1389,12 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
         m = m_new;
 #pragma unroll
         for (int t = 0; t < NB; ++t) o[t] *= alpha;
-        // O^T += V^T . P^T over the block's 64 keys
+        // O^T += V^T . P^T over this wave's keys of the block
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int key = kt * 16 + 4 * g + j;
+                const int key = kofs + kt * 16 + 4 * g + j;
                 const float* vrow = cV + key * D + r;
 #pragma unroll
                 for (int t = 0; t < NB; ++t) {
@@ -1394,6 +1402,33 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
                     o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, s[kt][j], o[t], 0, 0, 0);
                 }
             }
+    }
+    if constexpr (KS == 2) {
+        // Every wave is past the last barrier's reads: the K stages are free.
+        // Group 1 leaves O, m and l of each lane; group 0 merges them.
+        __syncthreads();
+        float* xo = reinterpret_cast<float*>(sK);
+        const int slot = (wl * 64 + lane) * (4 * NB + 2);
+        if (wave >= 4) {
+#pragma unroll
+            for (int t = 0; t < NB; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xo[slot + 4 * t + i] = o[t][i];
+            xo[slot + 4 * NB] = m;
+            xo[slot + 4 * NB + 1] = lsum;
+        }
+        __syncthreads();
+        if (wave >= 4) return;
+        const float m1 = xo[slot + 4 * NB], l1 = xo[slot + 4 * NB + 1];
+        // a group that saw no visible key has m = -inf and weight 0
+        const float mt = fmaxf(m, m1);
+        const float a0 = m == -INFINITY ? 0.f : exp2f(m - mt);
+        const float a1 = m1 == -INFINITY ? 0.f : exp2f(m1 - mt);
+#pragma unroll
+        for (int t = 0; t < NB; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[t][i] = o[t][i] * a0 + xo[slot + 4 * t + i] * a1;
+        lsum = lsum * a0 + l1 * a1;
     }
     if (!wave_rows || qrow >= a.Sq) return;
     // the query's denominator: the sum of its 4 lanes' partials
@@ -1988,6 +2023,15 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
 template <int D>
 hipError_t launch_prefill_f32(const AttnArgs& a, int mode, hipStream_t s) {
     const int64_t nqb = (a.Sq + 127) / 128;
+    if (nqb * a.B * a.Hq < 2 * (int64_t)device_cus()) {
+        // fewer than two 128-query blocks per CU: 64-query blocks with the
+        // keys of each staged block split between the two wave groups
+        dim3 grid((unsigned)((a.Sq + 63) / 64 * a.B * a.Hq));
+        if (mode == 1) attn_fwd_f32<D, 1, 2><<<grid, 512, 0, s>>>(a);
+        else if (mode == 0) attn_fwd_f32<D, 0, 2><<<grid, 512, 0, s>>>(a);
+        else attn_fwd_f32<D, 2, 2><<<grid, 512, 0, s>>>(a);
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)(nqb * a.B * a.Hq));
     if (mode == 1) attn_fwd_f32<D, 1><<<grid, 512, 0, s>>>(a);
     else if (mode == 0) attn_fwd_f32<D, 0><<<grid, 512, 0, s>>>(a);
