@@ -8,6 +8,8 @@ through the C ABI (ythip_gemm); inputs are resident in HBM before timing.
 
 Also reported in the same JSON line (each timed with HIP events on the stream
 the kernels are launched on):
+  gemm_4096_ceilings  the headline kernel's MFMA stream alone (register
+                  operands) and its global -> LDS operand stream alone, same grid
   gemm_sweep      the other configs[1] shapes (NN and the W^T "linear" layout)
   gemm_fp32       configs[0] (fp32 1024^3)
   attn_prefill    configs[2] causal flash prefill S = 512/2048/8192 (TFLOP/s)
@@ -67,7 +69,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only (no sweep, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list of sections to run "
-                                               "(gemm,sweep,fp32,prefill,decode,norm,math,qwen3,ytload)")
+                                               "(gemm,ceiling,sweep,fp32,prefill,decode,norm,math,qwen3,ytload)")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain conversion-copy kernel of known size (HBM counter calibration)")
     return ap.parse_args()
@@ -541,6 +543,31 @@ def main() -> int:
                                       "torch_hipblaslt_NN_tflops": round(flops / ms_torch / 1e9, 2),
                                       "NN_fp16_tflops": round(flops / ms_f16 / 1e9, 2)}
         del Wt
+
+    if want("ceiling") and not args.quick:
+        # The headline GEMM's two resources, each alone, with its grid (256
+        # workgroups of 8 waves, one per CU) and per-CU work (64 k steps): the
+        # MFMA stream on register operands (the same 137.4 GFLOP and 32 MiB bf16
+        # epilogue) and the global -> LDS operand stream (64 KiB per CU per k
+        # step, 1.07 GB per launch, no MFMA). libythip_probe.so, built from
+        # ytensor_amd/csrc/probe/ceiling.hip.
+        from ytensor_amd import probe
+        wg, ksteps = (M // 256) * (N // 256), K // 64
+        pa = torch.randn(8 * wg, 128, 64, device=dev).to(torch.bfloat16)
+        pb = torch.randn(8 * wg, 64, 64, device=dev).to(torch.bfloat16)
+        po = torch.empty(8 * wg, 128, 64, device=dev, dtype=torch.bfloat16)
+        ms_mfma = time_launches(lambda: probe.mfma_ceiling(pa, pb, po, wg, ksteps), args.steps, args.warmup, torch)
+        psum = torch.empty(wg, 512, 16, dtype=torch.uint8, device=dev)
+        ms_dma = time_launches(lambda: probe.dma_ceiling(A, B, psum), args.steps, args.warmup, torch)
+        dma_bytes = wg * ksteps * 65536
+        sections["gemm_4096_ceilings"] = {
+            "mfma_register_operands": {"ms": round(ms_mfma, 5), "tflops": round(flops / ms_mfma / 1e9, 2),
+                                       "frac_bf16_peak": round(flops / ms_mfma / 1e9 / PEAK_BF16_TFLOPS, 4)},
+            "dma_operand_stream": {"ms": round(ms_dma, 5), "bytes_l2_to_lds": dma_bytes,
+                                   "gbs": round(dma_bytes / ms_dma / 1e6, 1)},
+            "note": "the headline kernel's MFMA work alone (operands in registers) and its operand DMA alone "
+                    "(same grid, tile order and schedule, no LDS reads or MFMA)"}
+        del pa, pb, po, psum
 
     if want("sweep") and not args.quick:
         sweep = []

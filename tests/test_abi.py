@@ -111,3 +111,18 @@ def test_prefill_workspace_size_and_short_workspace():
                                    _lib.MASK_BOOL, fake, 64, None, 0, 0, fake, 255, None)
     assert st == _lib.YTHIP_EINVAL
     assert b"workspace of 256 bytes" in lib.ythip_last_error()
+
+
+def test_probe_library_loads_and_rejects_bad_shapes():
+    """The roofline probe library (libythip_probe.so, measurement support for
+    bench.py) loads and refuses shapes it does not take before any launch
+    (the pointers are never dereferenced)."""
+    from ytensor_amd import probe
+    if not os.path.exists(probe.PROBE_LIB_PATH):
+        pytest.fail("libythip_probe.so is not built (python -m ytensor_amd.build)")
+    lib = probe.load()
+    fake = 256
+    assert lib.ythip_probe_dma(fake, fake, 300, 256, 128, fake, None) == -1  # M not a multiple of 256
+    assert lib.ythip_probe_dma(fake, fake, 256, 256, 64, fake, None) == -1   # fewer than two k steps
+    assert lib.ythip_probe_mfma(fake, fake, fake, 0, 1, None) == -1
+    assert lib.ythip_probe_mfma(fake, fake, fake, 1, 0, None) == -1

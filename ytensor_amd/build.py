@@ -5,7 +5,9 @@
 
 Every translation unit under csrc/*.hip is compiled for gfx950 only, with the
 packed-fp32 feature disabled (v_pk_*_f32 are never emitted), then linked into
-ytensor_amd/libythip.so next to this file.
+ytensor_amd/libythip.so next to this file. The roofline probes under
+csrc/probe/ (measurement support for bench.py, not part of the C ABI) are
+linked into ytensor_amd/libythip_probe.so the same way.
 """
 from __future__ import annotations
 
@@ -20,6 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libythip.so")
+PROBE_LIB = os.path.join(HERE, "libythip_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -75,16 +78,17 @@ def build_host_programs() -> list[str]:
 def build(resource: bool = False, verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        results = list(ex.map(lambda s: _compile(s, resource), srcs))
+    probe_srcs = sorted(glob.glob(os.path.join(CSRC, "probe", "*.hip")))
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs) + len(probe_srcs))) as ex:
+        results = list(ex.map(lambda s: _compile(s, resource), srcs + probe_srcs))
     for _, err in results:
         if err.strip() and (verbose or resource):
             print(err, file=sys.stderr)
     objs = [o for o, _ in results]
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lz"]
-    subprocess.check_call(cmd)
-    os.replace(tmp, LIB)
+    for lib, lib_objs, extra in ((LIB, objs[:len(srcs)], ["-lz"]), (PROBE_LIB, objs[len(srcs):], [])):
+        tmp = lib + ".tmp"
+        subprocess.check_call([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *lib_objs, *extra])
+        os.replace(tmp, lib)
     build_host_programs()
     return LIB
 

@@ -102,6 +102,35 @@ __device__ __forceinline__ f32x4 mfma_chunk(F32, u32x4 a, u32x4 b, f32x4 c) {
     return c;
 }
 
+// Tile order of the GEMM grids, XCD-aware: the hardware places workgroup w on
+// XCD w % 8, so (when the tile count is a multiple of 8) w is remapped to give
+// each XCD a contiguous range of tiles, taken 4 tile-rows at a time so that an
+// XCD's L2 holds the A panels its 32 CUs reuse.
+__device__ __forceinline__ void tile_coords(int w, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int T = tiles_m * tiles_n;
+    if ((T & 7) == 0) {
+        const int per = T >> 3;
+        w = (w & 7) * per + (w >> 3);
+    }
+    constexpr int GROUP = 4;
+    const int in_group = GROUP * tiles_n;
+    const int g = w / in_group;
+    const int first = g * GROUP;
+    const int gsize = min(tiles_m - first, GROUP);
+    const int r = w - g * in_group;
+    tm = first + r % gsize;
+    tn = r / gsize;
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
+// left at their "no wait" maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // gfx950 LDS data movers. The builtins exist only for the device target; the
 // host compilation pass of a kernel that names them directly drops the kernel's
 // launch stub, so they are wrapped here and compiled in the device pass only.

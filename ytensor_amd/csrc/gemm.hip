@@ -57,22 +57,6 @@ __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ 
 __device__ __forceinline__ int swz_dma(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 __device__ __forceinline__ int nn_blk(int row, int blk, int mask) { return blk ^ ((row ^ ((row >> 3) << 2)) & mask); }
 
-__device__ __forceinline__ void tile_coords(int w, int tiles_m, int tiles_n, int& tm, int& tn) {
-    const int T = tiles_m * tiles_n;
-    if ((T & 7) == 0) {
-        const int per = T >> 3;
-        w = (w & 7) * per + (w >> 3);
-    }
-    constexpr int GROUP = 4;
-    const int in_group = GROUP * tiles_n;
-    const int g = w / in_group;
-    const int first = g * GROUP;
-    const int gsize = min(tiles_m - first, GROUP);
-    const int r = w - g * in_group;
-    tm = first + r % gsize;
-    tn = r / gsize;
-}
-
 template <class T, class TO, int BM, int BN, int WM, int WN, bool NN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs a) {
     using raw = typename T::raw;
@@ -294,14 +278,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs a) {
 // for NN: n % 16 == 0. Rows past M / N are clamped (their outputs are never
 // stored); K has no tail.
 // ---------------------------------------------------------------------------
-// Wait until at most N vector-memory operations of this wave are outstanding
-// (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
-// left at their "no wait" maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // SOFF: every operand spans less than 2^31 bytes (checked on the host): the DMA
 // then goes from a wave-uniform base, moved by scalar adds per k step, plus a
