@@ -325,6 +325,8 @@ def test_linear_bias_and_embedding_past_65535_rows(orc, yt):
                                                                  ("bf16", torch.float32, 1.0, 1, 12288, "NN"),
                                                                  ("bf16", torch.bfloat16, 0.0, 2, 12288, "NN"),
                                                                  ("bf16", torch.bfloat16, 1.0, 1, 12176, "NN"),
+                                                                 ("bf16", torch.bfloat16, 0.0, 1, 12176, "NN"),
+                                                                 ("f16", torch.float16, 0.0, 1, 12432, "NT"),
                                                                  ("bf16", torch.bfloat16, 0.0, 1, 12288, "NT"),
                                                                  ("f16", torch.float32, 1.0, 2, 12288, "NT"),
                                                                  ("bf16", torch.bfloat16, 1.0, 1, 12432, "NT"),
@@ -354,3 +356,25 @@ def test_whole_tile_schedule_bit_identical(yt, dtype, out_dtype, beta, batch, n,
     torch.cuda.synchronize()
     iview = torch.int16 if out.element_size() == 2 else torch.int32
     assert torch.equal(out.view(iview), ref[:, :m].contiguous().view(iview))
+
+
+@pytest.mark.parametrize("pad", [4, 8, 0])
+def test_whole_tile_schedule_c_row_strides(yt, pad):
+    """The ping-pong kernel stores a 16-bit C with beta = 0 as whole 128-byte
+    lines through LDS when C's base and rows are 16-byte aligned (pad 0 and 8:
+    rows of N + pad elements), and with 8-byte fragment stores otherwise (pad 4).
+    Either way the product equals the one-phase kernel's bit for bit, and the
+    pad columns are left untouched."""
+    m, k, n = 1024, 512, 12288
+    g = torch.Generator(device="cuda").manual_seed(23 + pad)
+    ap = torch.randn(m + 16, k, device="cuda", generator=g).to(torch.bfloat16)
+    b = (torch.randn(k, n, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    ref = torch.empty(m + 16, n, device="cuda", dtype=torch.bfloat16)
+    yt.gemm(ap, b, ref, alpha=0.5)                              # M = 1040: the one-phase kernel
+    wide = torch.full((m, n + pad), 7.0, device="cuda", dtype=torch.bfloat16)
+    out = wide[:, :n]
+    yt.gemm(ap[:m].contiguous(), b, out, alpha=0.5)             # M = 1024: the ping-pong kernel
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref[:m].view(torch.int16))
+    if pad:
+        assert bool((wide[:, n:] == 7.0).all())

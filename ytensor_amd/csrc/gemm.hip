@@ -40,7 +40,8 @@ struct GemmArgs {
     int64_t sa_b, sb_b, sc_b;
     float alpha, beta;
     int tiles_m, tiles_n;
-    int c_vec_ok;  // C rows allow 4-element vector stores
+    int c_vec_ok;   // C rows allow 4-element vector stores
+    int c_line_ok;  // 16-bit C: 16-byte aligned base and rows (the ping-pong kernel's line stores)
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
@@ -542,7 +543,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_dma_kernel(GemmArgs a)
 // plus a 32-bit lane offset fixed for the kernel: A's (and NT B's) chunk
 // swizzle repeats every 32 rows of a stage and NN B's block swizzle depends on
 // the 8-k-row group only through its parity. A partial last column of NN
-// tiles re-reads B's last 16 columns and stores only columns below N.
+// tiles re-reads B's last 16 columns and stores only columns below N. A 16-bit
+// C with beta == 0 and 16-byte aligned rows leaves through LDS as whole lines.
 template <class T, class TO, bool NN>
 __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
     using raw = typename T::raw;
@@ -672,6 +674,37 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
 
     using oraw = typename TO::raw;
     oraw* Cp = static_cast<oraw*>(a.C) + bz * a.sc_b;
+    if constexpr (sizeof(oraw) == 2) {
+        if (a.beta == 0.0f && a.c_line_ok) {
+            // Whole 128-byte lines of C. A fragment store writes 32 bytes into each
+            // of 16 rows, a quarter of a line per row, and the launch then spends
+            // microseconds per tile in the store path (the LM head's 18 rounds of
+            // tiles lose ~10% to it). Instead each wave rounds its 128 x 64 tile into
+            // its own 16 KiB of the now free operand stages (row r at r * 128 bytes,
+            // 16-byte chunk c at c ^ (r & 7)) and stores 8 whole rows per instruction.
+            __syncthreads();  // every wave is done reading the operand stages
+            char* wl = reinterpret_cast<char*>(sbuf) + wave * (WTM * WTN * 2);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int r = i * 16 + lrow;
+                    const int cb = j * 32 + lgrp * 8;  // byte of the lane's 4 columns in the row
+                    *reinterpret_cast<u32x2*>(wl + r * 128 + ((((cb >> 4) ^ (r & 7)) << 4) | (cb & 15))) =
+                        u32x2{pack2<TO>(a.alpha * acc[i][j][0], a.alpha * acc[i][j][1]),
+                              pack2<TO>(a.alpha * acc[i][j][2], a.alpha * acc[i][j][3])};
+                }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < WTM / 8; ++q) {
+                const int r = q * 8 + (lane >> 3), c = lane & 7;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(wl + r * 128 + ((c ^ (r & 7)) << 4));
+                const int n = n0 + wn * WTN + c * 8;  // n % 16 == 0: the 8 columns are all in or all out
+                if (n < a.n) *reinterpret_cast<u32x4*>(Cp + (int64_t)(m0 + wm * WTM + r) * a.rsc + n) = v;
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         const int m = m0 + wm * WTM + i * 16 + lrow;
@@ -1196,6 +1229,7 @@ int gemm_typed(int batch, int m, int n, int k, const void* A, int64_t sa_b, int6
         g.sa_b = sa_b; g.sb_b = sb_b; g.sc_b = sc_b;
         g.alpha = alpha; g.beta = beta;
         g.c_vec_ok = (rsc % 4 == 0) && (sc_b % 4 == 0) && aligned(C, 4 * sizeof(oraw));
+        g.c_line_ok = sizeof(oraw) == 2 && (rsc % 8 == 0) && (sc_b % 8 == 0) && aligned(C, 16);
         if (m <= SKINNY_M) {
             if (nt) {
                 GemvArgs v{};
