@@ -358,15 +358,17 @@ def test_whole_tile_schedule_bit_identical(yt, dtype, out_dtype, beta, batch, n,
     assert torch.equal(out.view(iview), ref[:, :m].contiguous().view(iview))
 
 
-@pytest.mark.parametrize("pad", [4, 8, 0])
-def test_whole_tile_schedule_c_row_strides(yt, pad):
+@pytest.mark.parametrize("pad,k", [(4, 512), (8, 512), (0, 512), (0, 64), (8, 192)])
+def test_whole_tile_schedule_c_row_strides(yt, pad, k):
     """The ping-pong kernel stores a 16-bit C with beta = 0 as whole 128-byte
     lines through LDS when C's base and rows are 16-byte aligned (pad 0 and 8:
     rows of N + pad elements), and with 8-byte fragment stores otherwise (pad 4).
+    The two wave groups stage their tiles in different operand stages, chosen
+    by the parity of the k-step count (k = 64, 192, 512: 1, 3, 8 steps).
     Either way the product equals the one-phase kernel's bit for bit, and the
     pad columns are left untouched."""
-    m, k, n = 1024, 512, 12288
-    g = torch.Generator(device="cuda").manual_seed(23 + pad)
+    m, n = 1024, 12288
+    g = torch.Generator(device="cuda").manual_seed(23 + pad + k)
     ap = torch.randn(m + 16, k, device="cuda", generator=g).to(torch.bfloat16)
     b = (torch.randn(k, n, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
     ref = torch.empty(m + 16, n, device="cuda", dtype=torch.bfloat16)

@@ -680,10 +680,15 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
             // of 16 rows, a quarter of a line per row, and the launch then spends
             // microseconds per tile in the store path (the LM head's 18 rounds of
             // tiles lose ~10% to it). Instead each wave rounds its 128 x 64 tile into
-            // its own 16 KiB of the now free operand stages (row r at r * 128 bytes,
-            // 16-byte chunk c at c ^ (r & 7)) and stores 8 whole rows per instruction.
-            __syncthreads();  // every wave is done reading the operand stages
-            char* wl = reinterpret_cast<char*>(sbuf) + wave * (WTM * WTN * 2);
+            // 16 KiB of a free operand stage (row r at r * 128 bytes, 16-byte chunk c
+            // at c ^ (r & 7)) and stores 8 whole rows per instruction. Group A's waves
+            // take the stage no wave reads in the last k step and go at once; group
+            // B's take the other one after a barrier that group A meets once its
+            // stores are out.
+            const int sl = ((KT - 1) & 1) ^ (grpB ? 0 : 1);
+            const bool bhalf = (wave & 3) >= 2;  // waves 0, 1, 4, 5 use A's stage, 2, 3, 6, 7 B's
+            char* wl = reinterpret_cast<char*>(bhalf ? sB + sl * STB : sA + sl * STA) + (wave & 1) * (WTM * WTN * 2);
+            if (grpB) __builtin_amdgcn_s_barrier();
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -694,7 +699,10 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
                         u32x2{pack2<TO>(a.alpha * acc[i][j][0], a.alpha * acc[i][j][1]),
                               pack2<TO>(a.alpha * acc[i][j][2], a.alpha * acc[i][j][3])};
                 }
-            __syncthreads();
+            // the wave reads back only its own writes: LDS keeps a wave's accesses in order
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_s_waitcnt(LGKM0);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
             for (int q = 0; q < WTM / 8; ++q) {
                 const int r = q * 8 + (lane >> 3), c = lane & 7;
@@ -702,6 +710,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
                 const int n = n0 + wn * WTN + c * 8;  // n % 16 == 0: the 8 columns are all in or all out
                 if (n < a.n) *reinterpret_cast<u32x4*>(Cp + (int64_t)(m0 + wm * WTM + r) * a.rsc + n) = v;
             }
+            if (!grpB) __builtin_amdgcn_s_barrier();
             return;
         }
     }
