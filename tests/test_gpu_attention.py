@@ -707,3 +707,31 @@ def test_gemv_attn_merge_argument_errors(yt):
         yt.gemv_attn_merge(ws, 1, 16, 128, 1000, w, out)  # workspace too small
     with pytest.raises(ValueError):
         yt.gemv_attn_merge(ws, 1, 8, 128, 1000, w, out)  # weight width != Hq * d
+
+
+@pytest.mark.parametrize("layout", ["bshd", "padded_rows"])
+def test_prefill_pingpong_output_views(yt, layout):
+    """The paired-head ping-pong kernel (B = 4, 16 query heads over 8 KV heads,
+    S = 2048: 512 paired workgroups) stores O as whole 128-byte lines through
+    LDS when O's base, rows and heads are 16-byte aligned with unit d stride
+    ("bshd": [B, S, H, D] memory viewed as [B, H, S, D]), and with fragment
+    stores otherwise ("padded_rows": rows of D + 4 elements). Either layout
+    gives the bits of the contiguous output, and padding is left untouched."""
+    B, Hq, Hkv, S, D = 4, 16, 8, 2048, 128
+    g = torch.Generator(device="cuda").manual_seed(31)
+    q = torch.randn(B, Hq, S, D, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, device="cuda", generator=g).to(torch.bfloat16)
+    ref = torch.empty(B, Hq, S, D, device="cuda", dtype=torch.bfloat16)
+    yt.scaled_dot_product_attention(q, k, v, 0.0, mask="causal", out=ref)
+    if layout == "bshd":
+        mem = torch.full((B, S, Hq, D), 3.0, device="cuda", dtype=torch.bfloat16)
+        out = mem.permute(0, 2, 1, 3)
+    else:
+        mem = torch.full((B, Hq, S, D + 4), 3.0, device="cuda", dtype=torch.bfloat16)
+        out = mem[..., :D]
+    yt.scaled_dot_product_attention(q, k, v, 0.0, mask="causal", out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.contiguous().view(torch.int16), ref.view(torch.int16))
+    if layout == "padded_rows":
+        assert bool((mem[..., D:] == 3.0).all())

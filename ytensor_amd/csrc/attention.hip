@@ -60,6 +60,7 @@ struct AttnArgs {
     int balance;  // causal: the grid is resident at once, two workgroups per CU (see attn_fwd_mfma)
     uint8_t* tcls;        // byte mask's tile classes (mask_tile_class_kernel), or null
     int nkbt;             // 64-key blocks of the mask rows: ceil(Skv / 64)
+    int o_line;           // O: unit d stride, 16-byte aligned base, rows and heads
 };
 
 // MODE 0: no mask; 1: causal; 2: byte mask and/or bias read per element;
@@ -1107,6 +1108,41 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pingpong(AttnArgs a) {
     }
 
     raw* Op = static_cast<raw*>(a.O) + b * a.os0 + h * a.os1;
+    if (a.o_line) {
+        // Whole 128-byte lines of O: a fragment store writes 8 bytes into each of
+        // 16 rows. Every wave's K/V reads ended at the loop's last barrier, so
+        // each wave rounds its 32 x D rows into its own 64 D bytes of the stages
+        // (row r at r * 2D bytes, 16-byte chunk c at c ^ (r % (D / 8))), reads
+        // them back (LDS keeps a wave's accesses in order) and stores 512 / D rows
+        // per instruction, 16 bytes per lane.
+        constexpr int RB = 2 * D;     // bytes per row
+        constexpr int CPR = RB / 16;  // 16-byte chunks per row
+        char* wl = reinterpret_cast<char*>(wave < 4 ? sK : sV) + (wave & 3) * (WQ * RB);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const float L = lsum[qt][0];
+            const float inv = L > 0.f ? 1.0f / L : 0.f;
+            const int r = qt * 16 + l16;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int cb = dt * 32 + g * 8;
+                const f32x4 v = o[qt][dt] * inv;
+                *reinterpret_cast<u32x2*>(wl + r * RB + ((((cb >> 4) ^ (r & (CPR - 1))) << 4) | (cb & 15))) =
+                    u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int it = 0; it < WQ * CPR / 64; ++it) {
+            const int r = it * (64 / CPR) + lane / CPR, c = lane % CPR;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(wl + r * RB + ((c ^ (r & (CPR - 1))) << 4));
+            const int q = q0 + r;
+            if (q < a.Sq) *reinterpret_cast<u32x4*>(Op + (int64_t)q * a.os2 + c * 8) = v;
+        }
+        return;
+    }
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const float L = lsum[qt][0];
@@ -2250,6 +2286,7 @@ __attribute__((visibility("default"))) int ythip_attn_prefill_ws(
     a.vs0 = v_str[0]; a.vs1 = v_str[1]; a.vs2 = v_str[2];
     a.os0 = o_str[0]; a.os1 = o_str[1]; a.os2 = o_str[2];
     a.qs3 = q_str[3]; a.ks3 = k_str[3]; a.vs3 = v_str[3]; a.os3 = o_str[3];
+    a.o_line = o_str[3] == 1 && o_str[0] % 8 == 0 && o_str[1] % 8 == 0 && o_str[2] % 8 == 0 && al(O, 16);
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.Sq = q_len; a.Skv = kv_len; a.D = d; a.Dv = dv;
     a.scale_log2 = scale * LOG2E;
     a.causal = mask_kind == YTHIP_MASK_CAUSAL || mask_kind == YTHIP_MASK_DIAG;
