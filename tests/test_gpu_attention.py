@@ -710,15 +710,18 @@ def test_gemv_attn_merge_argument_errors(yt):
 
 
 @pytest.mark.parametrize("layout", ["bshd", "padded_rows"])
-def test_prefill_pingpong_output_views(yt, layout):
-    """The paired-head ping-pong kernel (B = 4, 16 query heads over 8 KV heads,
-    S = 2048: 512 paired workgroups) stores O as whole 128-byte lines through
-    LDS when O's base, rows and heads are 16-byte aligned with unit d stride
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [(4, 16, 8, 2048, 128), (1, 16, 8, 2048, 128), (8, 8, 8, 1000, 64)])
+def test_prefill_output_views(yt, layout, B, Hq, Hkv, S, D):
+    """The 16-bit prefill kernels store O as whole 128-byte lines through LDS
+    when O's base, rows and heads are 16-byte aligned with unit d stride
     ("bshd": [B, S, H, D] memory viewed as [B, H, S, D]), and with fragment
-    stores otherwise ("padded_rows": rows of D + 4 elements). Either layout
+    stores otherwise ("padded_rows": rows of D + 4 elements). Shapes: the
+    paired-head ping-pong kernel (B = 4: 512 paired workgroups), the key split
+    inside the workgroup (B = 1: 256 query blocks), and one 128-query block per
+    4-wave workgroup (no GQA pairing, 512 blocks) with D = 64 and a partial last
+    block (S = 1000). Either layout
     gives the bits of the contiguous output, and padding is left untouched."""
-    B, Hq, Hkv, S, D = 4, 16, 8, 2048, 128
-    g = torch.Generator(device="cuda").manual_seed(31)
+    g = torch.Generator(device="cuda").manual_seed(31 + B + D)
     q = torch.randn(B, Hq, S, D, device="cuda", generator=g).to(torch.bfloat16)
     k = torch.randn(B, Hkv, S, D, device="cuda", generator=g).to(torch.bfloat16)
     v = torch.randn(B, Hkv, S, D, device="cuda", generator=g).to(torch.bfloat16)

@@ -581,6 +581,43 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
     }
 
     raw* Op = static_cast<raw*>(a.O) + b * a.os0 + h * a.os1;
+    // Whole 128-byte lines of O (as in attn_fwd_pingpong): the wave rounds its
+    // WQ x D rows into LDS -- its own merge slots with the key split, else its
+    // share of the K stages, free after the loop's last barrier -- reads them
+    // back in order and stores 512 / D rows per instruction. A fragment store
+    // writes 8 bytes into each of 16 rows: S=2048 spent 3.1 of 33 us on them.
+    constexpr int RB = 2 * D, CPR = RB / 16;  // bytes and 16-byte chunks per row
+    if constexpr (KSPLIT == 2 || 4 * GH * WQ * RB <= 2 * STG * 16) {
+        if (a.o_line) {
+            char* wl = KSPLIT == 2 ? reinterpret_cast<char*>(sK + (wave & 3) * QT * (DT + 1) * 64)
+                                   : reinterpret_cast<char*>(sK) + wave * (WQ * RB);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // after the merge's reads of these slots
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const float L = lsum[qt][0];
+                const float inv = L > 0.f ? 1.0f / L : 0.f;
+                const int r = qt * 16 + l16;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const int cb = dt * 32 + g * 8;
+                    const f32x4 v = o[qt][dt] * inv;
+                    *reinterpret_cast<u32x2*>(wl + r * RB + ((((cb >> 4) ^ (r & (CPR - 1))) << 4) | (cb & 15))) =
+                        u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int it = 0; it < WQ * CPR / 64; ++it) {
+                const int r = it * (64 / CPR) + lane / CPR, c = lane % CPR;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(wl + r * RB + ((c ^ (r & (CPR - 1))) << 4));
+                const int q = q0 + r;
+                if (q < a.Sq) *reinterpret_cast<u32x4*>(Op + (int64_t)q * a.os2 + c * 8) = v;
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const float L = lsum[qt][0];
