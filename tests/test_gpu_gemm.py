@@ -380,3 +380,26 @@ def test_whole_tile_schedule_c_row_strides(yt, pad, k):
     assert torch.equal(out.view(torch.int16), ref[:m].view(torch.int16))
     if pad:
         assert bool((wide[:, n:] == 7.0).all())
+
+
+@pytest.mark.parametrize("m,n,k,layout", [(2048, 2048, 512, "NN"), (2048, 2048, 512, "NT"),
+                                          (1040, 12288, 256, "NN"), (512, 6144, 1024, "NT"),
+                                          (1000, 4000, 192, "NN")])
+def test_one_phase_tiles_c_row_strides(yt, m, n, k, layout):
+    """The one-phase DMA kernels (256 x 256 tiles of a partial last tile row,
+    128 x 128 and 64 x 64 tiles, ragged M and N) store whole tiles of a 16-bit C
+    with beta = 0 through LDS in whole rows when C's base and rows are 16-byte
+    aligned, and with 8-byte fragment stores otherwise (rows padded by 4
+    elements). Both give the same bits, edge tiles included."""
+    g = torch.Generator(device="cuda").manual_seed(m + n + k)
+    a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+    if layout == "NN":
+        b = (torch.randn(k, n, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    else:
+        b = (torch.randn(n, k, device="cuda", generator=g) * 0.05).to(torch.bfloat16).t()
+    ref = torch.empty(m, n + 4, device="cuda", dtype=torch.bfloat16)[:, :n]   # rows of n + 4: fragment stores
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)              # aligned rows: whole-row stores
+    yt.gemm(a, b, ref, alpha=0.5)
+    yt.gemm(a, b, out, alpha=0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.contiguous().view(torch.int16))
