@@ -738,3 +738,39 @@ def test_prefill_output_views(yt, layout, B, Hq, Hkv, S, D):
     assert torch.equal(out.contiguous().view(torch.int16), ref.view(torch.int16))
     if layout == "padded_rows":
         assert bool((mem[..., D:] == 3.0).all())
+
+
+@pytest.mark.parametrize("kind", ["bias", "mask_unaligned"])
+def test_prefill_per_element_mask_paired_grid(orc, yt, kind):
+    """Per-element masks and biases (a bias, or byte-mask rows that are not
+    16-byte aligned) on a grid large enough for paired heads (B = 4, 16 query
+    heads over 8, 2048 queries: 512 paired blocks) run the unpaired 128-query
+    tiles: against the oracle's flash_attention with the same mask and bias
+    (src/kernel/avx2/flash_attention.inl:335-379), fully masked rows zero."""
+    B, Hq, Hkv, Sq, Skv, D = 4, 16, 8, 2048, 2090, 128
+    rng = np.random.default_rng(7 if kind == "bias" else 8)
+    Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    Qd, Qh = make_input(orc, Q, "bf16")
+    Kd, Kh = make_input(orc, K, "bf16")
+    Vd, Vh = make_input(orc, V, "bf16")
+    scale = 1.0 / math.sqrt(D)
+    m = bnp = None
+    mask = bias = None
+    if kind == "bias":
+        bnp = (rng.standard_normal((Sq, Skv)) * 0.5).astype(np.float32)
+        bias = torch.from_numpy(bnp).cuda()
+    else:
+        m = rng.random((Sq, Skv)) > 0.3
+        m[5] = False
+        mask = torch.from_numpy(m).cuda()   # rows of 2090 bytes: not 16-byte aligned
+    r = np.zeros((B, Hq, Sq, D), np.float32)
+    for b in range(B):
+        for h in range(Hq):
+            kh = h // (Hq // Hkv)
+            r[b, h] = orc.flash_attention(Qh[b, h], Kh[b, kh], Vh[b, kh], scale, m, bnp)
+    g = host_f32(yt.scaled_dot_product_attention(Qd, Kd, Vd, scale, mask=mask, bias=bias))
+    if m is not None:
+        assert np.all(g[:, :, 5] == 0.0)
+    check16(orc, g, r, "bf16", True, f"per-element {kind} B={B} {Hq}/{Hkv} heads {Sq}x{Skv}")

@@ -2081,7 +2081,9 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
             else attn_fwd_pingpong<T, D, 0><<<grid, 512, 0, s>>>(a);
             return hipGetLastError();
         }
-        return launch_prefill_gh<T, D, 2, 2, 8>(a, mode, s);
+        // Per-element masks and biases (mode 2) run unpaired: the paired form
+        // with 128-key blocks spills ~190 VGPRs and measured 1.8-2.1x slower
+        // (B=2, S=4096, fp32 bias: 2396 against 1345 us).
     }
     // Short sequences: 16 queries per wave doubles the workgroups (two per CU)
     // and halves the per-block work on the longest causal row's serial chain;
