@@ -774,3 +774,46 @@ def test_prefill_per_element_mask_paired_grid(orc, yt, kind):
     if m is not None:
         assert np.all(g[:, :, 5] == 0.0)
     check16(orc, g, r, "bf16", True, f"per-element {kind} B={B} {Hq}/{Hkv} heads {Sq}x{Skv}")
+
+
+@pytest.mark.parametrize("pattern", ["random", "causal_bytes", "blocks"])
+@pytest.mark.parametrize("grid", ["split", "whole"])
+def test_prefill_fp32_bool_mask_words(orc, yt, pattern, grid):
+    """fp32 prefill with a byte mask whose rows are 4-byte aligned (Skv a
+    multiple of 4, no bias) reads each lane's mask bytes as words and classes
+    every 64-key block for each wave's rows: blocks no row sees are skipped,
+    blocks every row sees take no per-score test, mixed blocks test each byte.
+    Patterns: random bytes with a fully masked row, the causal mask as bytes,
+    and 64-key blocks hidden or shown whole per 16-row group. Against the
+    reference's fp32 flash_attention (src/kernel/avx2/flash_attention.inl:
+    335-379) at rel <= 1e-4, on both grids (key split and whole blocks)."""
+    if grid == "split":
+        B, Hq, Hkv, Sq, Skv = 2, 8, 2, 201, 336
+    else:
+        B, Hq, Hkv, Sq, Skv = 2, 64, 16, 520, 604
+    D = 128
+    rng = np.random.default_rng(Skv + len(pattern))
+    Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
+    if pattern == "random":
+        m = rng.random((Sq, Skv)) > 0.35
+        m[7] = False
+    elif pattern == "causal_bytes":
+        m = np.arange(Skv)[None, :] <= np.arange(Sq)[:, None] + (Skv - Sq)
+    else:
+        show = rng.random(((Sq + 15) // 16, (Skv + 63) // 64)) > 0.5
+        m = np.repeat(np.repeat(show, 16, axis=0), 64, axis=1)[:Sq, :Skv].copy()
+        m[:, 100:103] = True   # a few mixed blocks
+    g = host_f32(yt.scaled_dot_product_attention(dev_f32(Q), dev_f32(K), dev_f32(V), 0.0,
+                                                 mask=torch.from_numpy(m).cuda()))
+    r = np.zeros_like(g)
+    for b in range(B):
+        for h in range(Hq):
+            r[b, h] = orc.flash_attention(Q[b, h], K[b, h // (Hq // Hkv)], V[b, h // (Hq // Hkv)],
+                                          1.0 / math.sqrt(D), m, None)
+    e = rel_err(g, r)
+    print(f"fp32 word mask {pattern} {grid}: rel={e:.3e}", flush=True)
+    assert e <= 1e-4
+    empty = ~m.any(axis=1)
+    assert np.all(g[:, :, empty] == 0.0)

@@ -61,6 +61,7 @@ struct AttnArgs {
     uint8_t* tcls;        // byte mask's tile classes (mask_tile_class_kernel), or null
     int nkbt;             // 64-key blocks of the mask rows: ceil(Skv / 64)
     int o_line;           // O: unit d stride, 16-byte aligned base, rows and heads
+    int mask_words;       // byte mask, no bias, 4-byte aligned base and rows (attn_fwd_f32)
 };
 
 // MODE 0: no mask; 1: causal; 2: byte mask and/or bias read per element;
@@ -1398,16 +1399,43 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
         // per-element inputs of MODE 2, issued before the score MFMAs
         uint8_t mk[NKT][4];
         float bv[NKT][4];
+        uint32_t mw[NKT];   // a mask alone with 4-byte aligned rows: the lane's 4 bytes of each 16-key tile
+        bool mall = false;  // ... every score of the wave's block visible
         if constexpr (MODE == 2) {
             const int qr = min(qrow, a.Sq - 1);
+            if (a.mask_words) {
+                // Four word loads instead of sixteen byte loads, and the block's class
+                // for the wave's rows: none visible -> skip it (its p would all be 0
+                // and alpha 1, the same bits), all visible -> no per-score test.
+                const uint8_t* mrow = a.mask + (int64_t)qr * a.mask_ld;
+                bool any = false, all = true;
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt)
+                for (int kt = 0; kt < NKT; ++kt) {
+                    const int key = k0 + kofs + kt * 16 + 4 * g;
+                    uint32_t w = 0;
+                    if (key + 3 < a.Skv) {
+                        w = *reinterpret_cast<const uint32_t*>(mrow + key);
+                    } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = min(k0 + kofs + kt * 16 + 4 * g + i, a.Skv - 1);
-                    mk[kt][i] = a.mask != nullptr ? a.mask[(int64_t)qr * a.mask_ld + key] : (uint8_t)1;
-                    bv[kt][i] = a.bias != nullptr ? a.bias[(int64_t)qr * a.brs + (int64_t)key * a.bcs] * LOG2E : 0.f;
+                        for (int i = 0; i < 4; ++i)
+                            if (key + i < a.Skv) w |= (uint32_t)mrow[key + i] << (8 * i);
+                    }
+                    mw[kt] = w;
+                    any = any || w != 0;
+                    all = all && ((w - 0x01010101u) & ~w & 0x80808080u) == 0;  // no zero byte
                 }
+                if (__ballot(any) == 0) continue;  // no row of this wave sees a key of the block
+                mall = __ballot(!all) == 0;
+            } else {
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int key = min(k0 + kofs + kt * 16 + 4 * g + i, a.Skv - 1);
+                        mk[kt][i] = a.mask != nullptr ? a.mask[(int64_t)qr * a.mask_ld + key] : (uint8_t)1;
+                        bv[kt][i] = a.bias != nullptr ? a.bias[(int64_t)qr * a.brs + (int64_t)key * a.bcs] * LOG2E : 0.f;
+                    }
+            }
         }
         const u32x4* cK = sK + (kb & 1) * STG;
         const float* cV = reinterpret_cast<const float*>(sV + (kb & 1) * STG);
@@ -1439,8 +1467,12 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
                 if constexpr (MODE == 1) vis = vis && key <= qrow + a.diag_off;
                 float x = s[kt][i];
                 if constexpr (MODE == 2) {
-                    vis = vis && mk[kt][i] != 0;
-                    x += bv[kt][i];
+                    if (a.mask_words) {
+                        vis = vis && (mall || ((mw[kt] >> (8 * i)) & 0xffu) != 0);
+                    } else {
+                        vis = vis && mk[kt][i] != 0;
+                        x += bv[kt][i];
+                    }
                 }
                 s[kt][i] = vis ? x : -INFINITY;
                 mx = fmaxf(mx, s[kt][i]);
@@ -2329,6 +2361,7 @@ __attribute__((visibility("default"))) int ythip_attn_prefill_ws(
     a.os0 = o_str[0]; a.os1 = o_str[1]; a.os2 = o_str[2];
     a.qs3 = q_str[3]; a.ks3 = k_str[3]; a.vs3 = v_str[3]; a.os3 = o_str[3];
     a.o_line = o_str[3] == 1 && o_str[0] % 8 == 0 && o_str[1] % 8 == 0 && o_str[2] % 8 == 0 && al(O, 16);
+    a.mask_words = mask_kind == YTHIP_MASK_BOOL && bias == nullptr && al(mask, 4) && mask_ld % 4 == 0;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.Sq = q_len; a.Skv = kv_len; a.D = d; a.Dv = dv;
     a.scale_log2 = scale * LOG2E;
     a.causal = mask_kind == YTHIP_MASK_CAUSAL || mask_kind == YTHIP_MASK_DIAG;
