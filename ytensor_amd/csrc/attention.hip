@@ -1305,7 +1305,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
     const int nqb = (a.Sq + BQ - 1) / BQ;
     const int nbh = a.B * a.Hq;
     const int rank = blockIdx.x / nbh, bh = blockIdx.x % nbh;
-    const int qb = MODE == 1 ? nqb - 1 - rank : rank;
+    // the last query blocks first: causal rows, and the rows of causal-shaped
+    // byte masks (a KV ring's included), see more keys further down
+    const int qb = (MODE == 1 || MODE == 2) ? nqb - 1 - rank : rank;
     const int b = bh / a.Hq, h = bh % a.Hq, kvh = h / (a.Hq / a.Hkv);
     const float* Qp = static_cast<const float*>(a.Q) + b * a.qs0 + h * a.qs1;
     const float* Kp = static_cast<const float*>(a.K) + b * a.ks0 + kvh * a.ks1;
@@ -1355,15 +1357,16 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
     }
     const uint32_t ldsK0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sK[wave * 64]);
     const uint32_t ldsV0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sV[wave * 64]);
-    auto issue = [&](int kb) {
+    // block kb into the stage of list position j
+    auto issue = [&](int j, int kb) {
         const int k0 = kb * BKV;
-        u32x4* dK = sK + (kb & 1) * STG;
-        u32x4* dV = sV + (kb & 1) * STG;
+        u32x4* dK = sK + (j & 1) * STG;
+        u32x4* dV = sV + (j & 1) * STG;
         const float* kbase = Kp + (int64_t)k0 * a.ks2;
         const float* vbase = Vp + (int64_t)k0 * a.vs2;
         if (k0 + BKV <= a.Skv && soff) {
-            const uint32_t lk = ldsK0 + (uint32_t)((kb & 1) * STG) * 16u;
-            const uint32_t lv = ldsV0 + (uint32_t)((kb & 1) * STG) * 16u;
+            const uint32_t lk = ldsK0 + (uint32_t)((j & 1) * STG) * 16u;
+            const uint32_t lv = ldsV0 + (uint32_t)((j & 1) * STG) * 16u;
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 dma16_soff(kbase, kbo[i], lk + (uint32_t)(i * 64 * NW) * 16u);
@@ -1386,11 +1389,47 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < NB; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    if (nkb > 0) issue(0);
-    for (int kb = 0; kb < nkb; ++kb) {
+    // MODE 2 with the mask's tile classes (a.tcls, from mask_tile_class_kernel):
+    // the workgroup lists, in key order, the 64-key blocks some of its rows see
+    // and stages only those (a block no row sees would leave p = 0 and alpha = 1:
+    // the same bits). Otherwise every block up to nkb is visited.
+    __shared__ uint16_t slist[MODE == 2 ? PP_LIST_MAX : 1];
+    __shared__ int s_wcnt[NW];
+    const bool listed = MODE == 2 && a.tcls != nullptr;
+    int nvis = nkb;
+    if constexpr (MODE == 2) {
+        if (listed) {
+            const int rg0 = qb * BQ / 32, rg1 = min(qb * BQ + BQ - 1, a.Sq - 1) / 32;
+            int base = 0;
+            for (int c0 = 0; c0 < nkb_all; c0 += 64 * NW) {
+                const int kb = c0 + tid;
+                bool any = false;
+                if (kb < nkb_all)
+                    for (int rg = rg0; rg <= rg1; ++rg) any = any || (a.tcls[(int64_t)rg * a.nkbt + kb] & 1) != 0;
+                const uint64_t bal = __ballot(any);
+                if (lane == 0) s_wcnt[wave] = __popcll(bal);
+                __syncthreads();
+                int before = __popcll(bal & ((1ull << lane) - 1ull)), total = 0;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    before += w < wave ? s_wcnt[w] : 0;
+                    total += s_wcnt[w];
+                }
+                if (any) slist[base + before] = (uint16_t)kb;
+                base += total;
+                __syncthreads();
+            }
+            nvis = base;
+        }
+    }
+    auto block_at = [&](int j) -> int { return listed ? __builtin_amdgcn_readfirstlane((int)slist[j]) : j; };
+
+    if (nvis > 0) issue(0, block_at(0));
+    for (int j = 0; j < nvis; ++j) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (kb + 1 < nkb) issue(kb + 1);
+        const int kb = block_at(j);
+        if (j + 1 < nvis) issue(j + 1, block_at(j + 1));
         const int k0 = kb * BKV;
         if (!wave_rows) continue;
         if constexpr (MODE == 1) {
@@ -1437,8 +1476,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_f32(AttnArgs a) {
                     }
             }
         }
-        const u32x4* cK = sK + (kb & 1) * STG;
-        const float* cV = reinterpret_cast<const float*>(sV + (kb & 1) * STG);
+        const u32x4* cK = sK + (j & 1) * STG;
+        const float* cV = reinterpret_cast<const float*>(sV + (j & 1) * STG);
         f32x4 s[NKT];
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -2131,7 +2170,15 @@ hipError_t launch_prefill_mfma(AttnArgs a, int mode, hipStream_t s) {
 }
 
 template <int D>
-hipError_t launch_prefill_f32(const AttnArgs& a, int mode, hipStream_t s) {
+hipError_t launch_prefill_f32(AttnArgs a, int mode, hipStream_t s) {
+    // a byte mask alone with 16-byte aligned rows and a workspace: its tile
+    // classes first, then each workgroup stages only the blocks its rows see
+    if (mode == 2 && a.tcls != nullptr && a.mask_words && al(a.mask, 16) && a.mask_ld % 16 == 0) {
+        dim3 cgrid((a.Sq + 31) / 32, (a.nkbt + 15) / 16);
+        mask_tile_class_kernel<<<cgrid, 256, 0, s>>>(a.mask, a.mask_ld, a.Sq, a.Skv, a.nkbt, a.tcls);
+    } else {
+        a.tcls = nullptr;
+    }
     const int64_t nqb = (a.Sq + 127) / 128;
     if (nqb * a.B * a.Hq < 2 * (int64_t)device_cus()) {
         // fewer than two 128-query blocks per CU: 64-query blocks with the
