@@ -12,7 +12,8 @@ the kernels are launched on):
                   operands) and its global -> LDS operand stream alone, same grid
   gemm_sweep      the other configs[1] shapes (NN and the W^T "linear" layout)
   gemm_fp32       configs[0] (fp32 1024^3)
-  attn_prefill    configs[2] causal flash prefill S = 512/2048/8192 (TFLOP/s)
+  attn_prefill    configs[2] causal flash prefill S = 512/2048/8192 (TFLOP/s), the
+                  causal mask as bytes, and fp32 (the reference flash backend's dtype)
   attn_decode     configs[3] decode attention (GB/s of K/V read)
   rmsnorm_rope    fused RMSNorm+RoPE on configs[2] shapes at S=8192 (GB/s)
   attn_math       the MATH attention backend (materialised scores) at S=2048, and
@@ -649,6 +650,25 @@ def main() -> int:
                           "frac_fp32_peak": round(fl / t / 1e9 / PEAK_FP32_TFLOPS, 4)})
             del q, k, v, o
         sections["attn_prefill_causal_fp32"] = pre32
+        # fp32 with the causal mask given as bytes: the reference Qwen3's call form
+        # on its own flash backend (fp32-only; get_mask's bool tensor)
+        pre32b = []
+        for S in (2048, 8192):
+            q = torch.randn(1, 16, S, 128, device=dev)
+            k = torch.randn(1, 8, S, 128, device=dev)
+            v = torch.randn(1, 8, S, 128, device=dev)
+            o = torch.empty_like(q)
+            mk = torch.ones(S, S, device=dev, dtype=torch.bool).tril()
+            ws = torch.empty(int(yt._lib.lib().ythip_attn_sdpa_workspace_size(1, 16, S, S, 128)), dtype=torch.uint8,
+                             device=dev)
+            fl = 4.0 * 1 * 16 * 128 * S * (S + 1) / 2
+            t = time_launches(lambda: ops.scaled_dot_product_attention(q, k, v, 1 / math.sqrt(128), mk, out=o,
+                                                                       workspace=ws),
+                              max(args.steps // 4, 5), min(args.warmup, 3), torch)
+            pre32b.append({"S": S, "ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                           "frac_fp32_peak": round(fl / t / 1e9 / PEAK_FP32_TFLOPS, 4)})
+            del q, k, v, o, mk, ws
+        sections["attn_prefill_bool_mask_fp32"] = pre32b
 
     if want("decode") and not args.quick:
         dec = []
