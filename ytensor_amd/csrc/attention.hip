@@ -149,9 +149,10 @@ __global__ __launch_bounds__(256 * GH * KSPLIT, 2 / (GH * KSPLIT)) void attn_fwd
     // a CU pairs a heavy block with a light one. Per unit the order stays a
     // permutation of its query blocks.
     const bool light_first = a.balance && (unit & 1);
-    // the staged-mask kernel with block skipping also starts from the last query
-    // block: in causal-shaped masks (the KV ring's included) later rows see more keys
-    constexpr bool HEAVY_FIRST = MODE == 1 || (MODE == 3 && GH == 2);
+    // the staged-mask kernel also starts from the last query block: in
+    // causal-shaped masks (the KV ring's included) later rows see more keys
+    // (S=2048 causal as bytes, one head per workgroup: 48.8 -> 45.4 us)
+    constexpr bool HEAVY_FIRST = MODE == 1 || MODE == 3;
     const int qb = (HEAVY_FIRST && !light_first) ? (a.nqb - 1 - qi) : qi;
     const int b = unit / (a.Hkv * hgroups);
     const int rem = unit % (a.Hkv * hgroups);
