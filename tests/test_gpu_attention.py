@@ -776,9 +776,10 @@ def test_prefill_per_element_mask_paired_grid(orc, yt, kind):
     check16(orc, g, r, "bf16", True, f"per-element {kind} B={B} {Hq}/{Hkv} heads {Sq}x{Skv}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("pattern", ["random", "causal_bytes", "blocks"])
 @pytest.mark.parametrize("grid", ["split", "whole"])
-def test_prefill_fp32_bool_mask_words(orc, yt, pattern, grid):
+def test_prefill_fp32_bool_mask_words(orc, yt, pattern, grid, D):
     """fp32 prefill with a byte mask whose rows are 4-byte aligned (Skv a
     multiple of 4, no bias) reads each lane's mask bytes as words and classes
     every 64-key block for each wave's rows: blocks no row sees are skipped,
@@ -786,13 +787,14 @@ def test_prefill_fp32_bool_mask_words(orc, yt, pattern, grid):
     Patterns: random bytes with a fully masked row, the causal mask as bytes,
     and 64-key blocks hidden or shown whole per 16-row group. Against the
     reference's fp32 flash_attention (src/kernel/avx2/flash_attention.inl:
-    335-379) at rel <= 1e-4, on both grids (key split and whole blocks)."""
+    335-379) at rel <= 1e-4, on both grids (key split and whole blocks) and
+    both head dims. Skv = 336 has 16-byte mask rows (tile classes and block
+    lists from the workspace); Skv = 604 only 4-byte ones (no lists)."""
     if grid == "split":
         B, Hq, Hkv, Sq, Skv = 2, 8, 2, 201, 336
     else:
         B, Hq, Hkv, Sq, Skv = 2, 64, 16, 520, 604
-    D = 128
-    rng = np.random.default_rng(Skv + len(pattern))
+    rng = np.random.default_rng(Skv + len(pattern) + D)
     Q = rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)
     K = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
     V = rng.standard_normal((B, Hkv, Skv, D)).astype(np.float32)
@@ -813,7 +815,7 @@ def test_prefill_fp32_bool_mask_words(orc, yt, pattern, grid):
             r[b, h] = orc.flash_attention(Q[b, h], K[b, h // (Hq // Hkv)], V[b, h // (Hq // Hkv)],
                                           1.0 / math.sqrt(D), m, None)
     e = rel_err(g, r)
-    print(f"fp32 word mask {pattern} {grid}: rel={e:.3e}", flush=True)
+    print(f"fp32 word mask {pattern} {grid} D={D}: rel={e:.3e}", flush=True)
     assert e <= 1e-4
     empty = ~m.any(axis=1)
     assert np.all(g[:, :, empty] == 0.0)
