@@ -717,7 +717,7 @@ private:
                                       nullptr, nullptr, 0.f, ws, ws_bytes_, s),
                "qwen3: q/k norm + rope + attention");
             ck(ythip_gemv_attn_merge(code, YTHIP_F32, 1, H, nh, hd, splits_, ws, ld_part, L.o_proj.deviceData(),
-                                     nh * hd, x, H, 1.f, 1.f, s),
+                                     nh * hd, x, H, 1.f, 1.f, st, max_ctx_, s),
                "qwen3: merge + o_proj");
             ck(ythip_gemv_swiglu(1, code, 1, I, H, x, H, L.norm2.deviceData(), eps, L.gate_up.deviceData(), H, act, I,
                                  s),

@@ -58,7 +58,7 @@ enum ythip_mask_kind {
 };
 
 /* ABI version of this header; bumped on any signature change. */
-#define YTHIP_ABI_VERSION 2
+#define YTHIP_ABI_VERSION 3
 int ythip_abi_version(void);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
@@ -412,10 +412,15 @@ int ythip_gemv_fused(int prologue, int dtype_in, int dtype_out, int m, int n, in
  *   C[m, n] = alpha * A' . W[n, hq*hd]^T + beta * C   (dtype W, dtype_out C).
  * Same bits as the merge inside ythip_attn_decode_rope(O given) followed by
  * ythip_gemv_fused(prologue 0). The attention output is never written.
+ * dev_state / max_ctx: the decode-state record and ring size the split kernel
+ * ran with; the splits are cut by the visible key count min(KV_LEN, max_ctx)
+ * at run time, so only the splits holding keys are read. NULL: every split is
+ * read (the empty ones add exact zeros; same bits).
  */
 int ythip_gemv_attn_merge(int dtype, int dtype_out, int m, int n, int hq, int hd, int splits,
                           const float* partials, int64_t ld_part, const void* W, int64_t ldw,
-                          void* C, int64_t ldc, float alpha, float beta, void* stream);
+                          void* C, int64_t ldc, float alpha, float beta,
+                          const int32_t* dev_state, int max_ctx, void* stream);
 
 int ythip_gemv_swiglu(int prologue, int dtype, int m, int inter, int k, const void* A,
                       int64_t lda, const float* norm_w, float eps, const void* W, int64_t ldw,

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_argument_errors():
     import ytensor_amd
     lib = ytensor_amd.load()
-    assert lib.ythip_abi_version() == 2
+    assert lib.ythip_abi_version() == 3
     # invalid dtype / negative sizes are rejected before any HIP call
     st = lib.ythip_gemm(7, 0, 1, 2, 2, 2, None, 0, 2, 1, None, 0, 2, 1, None, 0, 2, 1, 1.0, 0.0, None)
     assert st == -1 and b"dtype" in lib.ythip_last_error()

@@ -671,7 +671,9 @@ def test_decode_attention_rope_equals_unfused(orc, yt, dtype, Hq, Hkv, d):
 def test_gemv_attn_merge_equals_merge_then_gemv(yt, dtype, out_dtype, B, Hq, Hkv, d, max_ctx):
     """The o projection with the split-K merge as its prologue equals the merged
     attention output (decode_attention_rope with O) fed to gemv_fused, bit for
-    bit, including positions where some splits hold no key (m = -inf)."""
+    bit, including positions where some splits hold no key (m = -inf), both
+    reading every split and, given the decode-state record, only the splits
+    the run-time partition filled."""
     rng = np.random.default_rng(B * 100 + Hq + d + max_ctx)
     dt = TORCH_DT[dtype]
     width = (Hq + 2 * Hkv) * d
@@ -694,8 +696,11 @@ def test_gemv_attn_merge_equals_merge_then_gemv(yt, dtype, out_dtype, B, Hq, Hkv
         yt.ops.decode_attention_rope(qkv, Hq, Hkv, d, None, None, 1e-6, None, None, p, k2, v2, None, ws)
         got = base.clone()
         yt.gemv_attn_merge(ws, B, Hq, d, max_ctx, w, got, alpha=0.5, beta=1.0)
+        got_used = base.clone()
+        yt.gemv_attn_merge(ws, B, Hq, d, max_ctx, w, got_used, alpha=0.5, beta=1.0, dev_state=p)
         torch.cuda.synchronize()
         assert torch.equal(got, want), (pos, splits)
+        assert torch.equal(got_used, want), (pos, splits)
         assert torch.equal(k1, k2) and torch.equal(v1, v2)
 
 

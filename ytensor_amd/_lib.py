@@ -76,7 +76,7 @@ SIGNATURES = {
     "ythip_argmax_step": (_I, [_I, _P, _P, _P, _P, _P]),
     "ythip_gemv_fused": (_I, [_I, _I, _I, _I, _I, _I, _P, _L, _P, _F, _P, _L, _P, _L, _F, _F, _P, _P]),
     "ythip_gemv_swiglu": (_I, [_I, _I, _I, _I, _I, _P, _L, _P, _F, _P, _L, _P, _L, _P]),
-    "ythip_gemv_attn_merge": (_I, [_I, _I, _I, _I, _I, _I, _I, _P, _L, _P, _L, _P, _L, _F, _F, _P]),
+    "ythip_gemv_attn_merge": (_I, [_I, _I, _I, _I, _I, _I, _I, _P, _L, _P, _L, _P, _L, _F, _F, _P, _I, _P]),
     "ythip_argmax_finish": (_I, [_P, _I, _P, _P, _P, _P]),
     "ythip_rope_tables": (_I, [_I, _I, _F, _P, _P]),
     "ythip_yt_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),

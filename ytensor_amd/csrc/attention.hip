@@ -1675,7 +1675,6 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int slot = tid / LPK, part = tid % LPK;
-    const int kbeg = split * a.chunk;
     // Fused: the new token's q rows (and its k / v rows, used by the workgroup that
     // owns the position) and the norm weights are loaded before anything else,
     // in parallel with the position read; the RoPE rows follow once the position
@@ -1716,15 +1715,21 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
         len = max(0, min(a.dev_state[YTHIP_ST_KV_LEN], a.max_ctx));
         const bool slot_ok = pos >= 0 && pos < a.max_ctx;
         rope_ok = rpos >= 0 && rpos < a.tab_rows;
-        owner = slot_ok && pos >= kbeg && pos < kbeg + a.chunk;
+        // the split whose chunk holds the row (the last split for a row past them all)
+        owner = slot_ok && min(pos / decode_chunk(len, a.splits), a.splits - 1) == split;
         if (tid == 0 && split == 0 && kvh == 0 && b == 0) {
             if (!slot_ok) atomicOr(&a.dev_state[YTHIP_ST_ERROR], (int)YTHIP_ST_ERR_CACHE);
             if (a.cos_tab != nullptr && !rope_ok) atomicOr(&a.dev_state[YTHIP_ST_ERROR], (int)YTHIP_ST_ERR_ROPE);
         }
     } else {
-        len = a.kv_len ? min(a.kv_len[b], a.max_ctx) : a.max_ctx;
+        len = a.kv_len ? max(0, min(a.kv_len[b], a.max_ctx)) : a.max_ctx;
     }
-    const int kend = min(len, kbeg + a.chunk);
+    // this split's keys [kb0, kend) of the len visible ones (none when kb0 >= len);
+    // keys past kend load the row kbeg instead, which stays inside the cache
+    const int chunk = decode_chunk(len, a.splits);
+    const int kb0 = split * chunk;
+    const int kend = min(len, kb0 + chunk);
+    const int kbeg = min(kb0, max(a.max_ctx - 1, 0));
 
     float m[G], l[G], o[G][8];
 #pragma unroll
@@ -1803,7 +1808,7 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     // issued unconditionally (rows past the end are clamped and masked): a branch
     // around the loads would make the compiler's wait before the prologue
     // arithmetic cover the batch as well
-    int k0 = kbeg + slot;
+    int k0 = kb0 + slot;
     load_batch(k0);
 
     float q[G][8];

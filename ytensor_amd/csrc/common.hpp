@@ -298,4 +298,22 @@ __device__ inline void decode_state_advance(int32_t* st, int32_t* history, int t
     decode_state_derive(st);
 }
 
+// Split-K decode partition. The grid holds `splits` workgroups per (batch, kv
+// head), sized for the cache's capacity; the keys visible at run time, len,
+// are cut into chunks of len / splits keys (rounded up), at least
+// DEC_MIN_CHUNK, so a short context in a large ring fills only the first few
+// splits with full chunks and the merges read only those. Splits past the last
+// used one hold empty partials (m = -inf, l = 0, o = 0).
+constexpr int DEC_MIN_CHUNK = 128;
+__host__ __device__ inline int decode_chunk(int len, int splits) {
+    const int c = splits > 0 ? (len + splits - 1) / splits : len;
+    return c > DEC_MIN_CHUNK ? c : DEC_MIN_CHUNK;
+}
+// splits holding keys (at least 1, at most splits)
+__host__ __device__ inline int decode_used(int len, int splits) {
+    if (len <= 0) return 1;
+    const int c = decode_chunk(len, splits), u = (len + c - 1) / c;
+    return u < splits ? u : (splits > 0 ? splits : 1);
+}
+
 }  // namespace ythip

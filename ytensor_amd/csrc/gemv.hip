@@ -77,6 +77,7 @@ struct GemvPrologue {
     float xr[PRO == 1 ? 4 : 1];                        // RMSNorm: first reduction group of row 0
     float opre[PRO == 3 ? 2 : 1][PRO == 3 ? MS : 1];   // merge: o of this thread's 2 elements
     float mreg[PRO == 3 ? MS : 1], lreg[PRO == 3 ? MS : 1];
+    int used = 0;                                      // merge: splits holding keys
 
     __device__ __forceinline__ void load_elem(const GemvArgs& a, int bz, int e, float& x0, float& x1) const {
         const int row = e / a.k, col = e - row * a.k;
@@ -116,6 +117,8 @@ struct GemvPrologue {
         }
         if constexpr (PRO == 3) {
             const int S = a.splits, stride = a.hd + 2;
+            // the split kernel's partition (decode_used); the loads below do not wait for it
+            used = a.dstate != nullptr ? decode_used(max(0, min(a.dstate[YTHIP_ST_KV_LEN], a.max_ctx)), S) : S;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int e = tid + j * NT;
@@ -194,7 +197,9 @@ struct GemvPrologue {
             __syncthreads();
         }
         if constexpr (PRO == 3) {
-            const int S = a.splits, hs = a.hq * S, stride = a.hd + 2;
+            // splits from U on hold no key (m = -inf): their terms are skipped as
+            // every empty split's is, so reading U splits gives the bits of reading S
+            const int S = a.splits, U = used, hs = a.hq * S, stride = a.hd + 2;
             float* s_w = reinterpret_cast<float*>(sAp + ((total + 7) & ~7));
             float* s_L = s_w + a.m * hs;
             if (tid < a.m * a.hq) {  // this thread owns (row, head) rh = tid
@@ -202,13 +207,13 @@ struct GemvPrologue {
                 float M = -INFINITY;
 #pragma unroll
                 for (int q = 0; q < MS; ++q)
-                    if (q < S) M = fmaxf(M, mreg[q]);
-                for (int q = MS; q < S; ++q) M = fmaxf(M, msrc[q * stride]);
+                    if (q < U) M = fmaxf(M, mreg[q]);
+                for (int q = MS; q < U; ++q) M = fmaxf(M, msrc[q * stride]);
                 float L = 0.f;
                 float* w = s_w + tid * S;
 #pragma unroll
                 for (int q = 0; q < MS; ++q) {
-                    if (q < S) {
+                    if (q < U) {
                         float ws = -INFINITY;
                         if (M != -INFINITY && mreg[q] != -INFINITY) {
                             ws = exp2f(mreg[q] - M);
@@ -217,7 +222,7 @@ struct GemvPrologue {
                         w[q] = ws;
                     }
                 }
-                for (int q = MS; q < S; ++q) {
+                for (int q = MS; q < U; ++q) {
                     const float ms = msrc[q * stride];
                     float ws = -INFINITY;
                     if (M != -INFINITY && ms != -INFINITY) {
@@ -238,13 +243,13 @@ struct GemvPrologue {
                 float acc = 0.f;
 #pragma unroll
                 for (int q = 0; q < MS; ++q) {
-                    if (q < S) {
+                    if (q < U) {
                         const float ws = w[q];
                         const float o = have_pre ? pre[q] : src[q * stride];
                         if (ws != -INFINITY) acc = fmaf(o, ws, acc);
                     }
                 }
-                for (int q = MS; q < S; ++q) {
+                for (int q = MS; q < U; ++q) {
                     const float ws = w[q];
                     if (ws != -INFINITY) acc = fmaf(src[q * stride], ws, acc);
                 }
@@ -749,9 +754,11 @@ __attribute__((visibility("default"))) int ythip_gemv_swiglu(int prologue, int d
 __attribute__((visibility("default"))) int ythip_gemv_attn_merge(int dtype, int dtype_out, int m, int n, int hq,
                                                                  int hd, int splits, const float* partials,
                                                                  int64_t ld_part, const void* W, int64_t ldw, void* C,
-                                                                 int64_t ldc, float alpha, float beta, void* stream) {
+                                                                 int64_t ldc, float alpha, float beta,
+                                                                 const int32_t* dev_state, int max_ctx, void* stream) {
     const char* who = "ythip_gemv_attn_merge";
     if (m < 0 || n < 0 || hq < 0 || hd <= 0 || splits <= 0) return fail(YTHIP_EINVAL, "%s: bad size", who);
+    if (dev_state != nullptr && max_ctx <= 0) return fail(YTHIP_EINVAL, "%s: max_ctx must be positive", who);
     if (m > GEMV_M) return fail(YTHIP_EUNSUPPORTED, "%s: m = %d (at most %d rows)", who, m, GEMV_M);
     if (m == 0 || n == 0 || hq == 0) return 0;
     if (!partials || !W || !C) return fail(YTHIP_EINVAL, "%s: NULL partials, W or C", who);
@@ -770,6 +777,7 @@ __attribute__((visibility("default"))) int ythip_gemv_attn_merge(int dtype, int 
     a.W = W; a.ldw = ldw; a.C = C; a.ldc = ldc;
     a.m = m; a.n = n; a.k = (int)k; a.alpha = alpha; a.beta = beta;
     a.hq = hq; a.hd = hd; a.splits = splits;
+    a.dstate = dev_state; a.max_ctx = max_ctx;
     return gemv_merge_dispatch(dtype, dtype_out, a, static_cast<hipStream_t>(stream));
 }
 

@@ -36,6 +36,11 @@ struct GemvArgs {
     float alpha, beta;
     float* amax;  // optional: per 16-column tile (max, index) of row 0
     int hq, hd, splits;  // prologue 3: A = split-K decode partials [m][hq][splits][hd + 2]
+    // prologue 3: the decode-state record whose KV_LEN (clamped to max_ctx) the
+    // split kernel partitioned, so only the splits holding keys are read (NULL:
+    // every split; the empty ones add exact zeros)
+    const int32_t* dstate;
+    int max_ctx;
 };
 
 int gemv_dispatch(int prologue, int dtype_in, int dtype_out, const GemvArgs& a, int batch, hipStream_t s);

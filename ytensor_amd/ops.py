@@ -652,12 +652,19 @@ def gemv_fused(a: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, prologu
 
 
 def gemv_attn_merge(workspace: torch.Tensor, B: int, Hq: int, d: int, max_ctx: int, weight: torch.Tensor,
-                    out: torch.Tensor, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+                    out: torch.Tensor, alpha: float = 1.0, beta: float = 0.0,
+                    dev_state: torch.Tensor | None = None) -> torch.Tensor:
     """Decode-step o projection straight from the split-K partials that
     decode_attention_rope(out=None) left in `workspace`: out [B, N] = alpha *
     merge(partials) @ weight.T + beta * out, weight [N, Hq*d]. Same bits as
-    decode_attention_rope(out=attn) followed by gemv_fused(attn, weight, out)."""
+    decode_attention_rope(out=attn) followed by gemv_fused(attn, weight, out).
+    dev_state: the decode-state record that call ran with; only the splits
+    holding keys are then read (None: all of them, same bits)."""
     _dev(workspace, weight, out)
+    if dev_state is not None:
+        _dev(dev_state)
+        if dev_state.dtype != torch.int32 or not dev_state.is_contiguous():
+            raise ValueError("dev_state must be a contiguous int32 decode-state record")
     splits = decode_splits(B, Hq, max_ctx)
     n, k = weight.shape
     if k != Hq * d:
@@ -670,7 +677,9 @@ def gemv_attn_merge(workspace: torch.Tensor, B: int, Hq: int, d: int, max_ctx: i
         raise ValueError("workspace smaller than the partials")
     check(_lib.lib().ythip_gemv_attn_merge(_code(weight), _code(out), B, n, Hq, d, splits, workspace.data_ptr(), ld,
                                            weight.data_ptr(), weight.stride(0), o2.data_ptr(), o2.stride(0),
-                                           float(alpha), float(beta), _stream()), "ythip_gemv_attn_merge")
+                                           float(alpha), float(beta),
+                                           None if dev_state is None else dev_state.data_ptr(), int(max_ctx),
+                                           _stream()), "ythip_gemv_attn_merge")
     return out
 
 

@@ -331,7 +331,7 @@ class Qwen3:
         # projection's prologue
         ops.decode_attention_rope(self.qkv[:1], nh, nkv, hd, L["qn"], L["kn"], cfg.eps, self.cos, self.sin,
                                   self.state, kc, vc, None, self.ws)
-        ops.gemv_attn_merge(self.ws, 1, nh, hd, self.max_ctx, L["o"], x, beta=1.0)  # x += attn . Wo^T
+        ops.gemv_attn_merge(self.ws, 1, nh, hd, self.max_ctx, L["o"], x, beta=1.0, dev_state=self.state)  # x += attn . Wo^T
         ops.gemv_swiglu(x, L["gu"], self.act[:1], "rmsnorm", L["n2"], cfg.eps)    # act = swiglu(norm(x) . Wgu^T)
         ops.gemv_fused(self.act[:1], L["down"], x, beta=1.0)                      # x += act . Wdown^T
 
