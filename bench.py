@@ -18,7 +18,9 @@ the kernels are launched on):
   rmsnorm_rope    fused RMSNorm+RoPE on configs[2] shapes at S=8192 (GB/s)
   attn_math       the MATH attention backend (materialised scores) at S=2048, and
                   a causal masked matmul at 4096^3
-  qwen3_0p6b      configs[4] shape: 512-token prefill + greedy decode tok/s
+  qwen3_0p6b      configs[4] shape: 512-token prefill + greedy decode tok/s (a KV
+                  ring sized to the run, and the reference's max_position_embeddings
+                  ring; bf16 and fp16; the C++ host)
   yt_checkpoint   .yt checkpoint of the Qwen3-0.6B shape loaded to the device (GB/s)
   roofline        the headline kernel against MI355X dense bf16 MFMA peak
   cpu_baseline    YTensor's own CPU sgemm (compiled reference when present,
@@ -332,11 +334,13 @@ def cpu_rows(path, kind: str) -> dict:
     return rows
 
 
-def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=None) -> dict:
+def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=None, ring: str = "fit") -> dict:
     """configs[4] shape: random-init Qwen3-0.6B (synthetic N(0, 0.02) weights,
     bf16 (or `dtype`) matrices, fp32 norms), 512-token prompt, then greedy
     decode with each step replayed from one captured HIP graph. tok/s counts the
-    decode steps."""
+    decode steps. ring "fit": a KV ring of prompt + tokens + 64 rows; "default":
+    max_position_embeddings rows, the size the reference's KVCache::init gives
+    it (example/qwen3/src/qwen3.cpp:415-421)."""
     import numpy as np
     from ytensor_amd.qwen3 import Qwen3, Qwen3Config, weight_layout
     cfg = Qwen3Config()
@@ -344,7 +348,8 @@ def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=No
     g = torch.Generator(device=dev)
     g.manual_seed(3)
     W = torch.randn(total, device=dev, generator=g) * 0.02
-    m = Qwen3(cfg, W, max_ctx=prompt_len + n_tokens + 64, max_prompt=prompt_len, dtype=dtype or torch.bfloat16)
+    max_ctx = prompt_len + n_tokens + 64 if ring == "fit" else None
+    m = Qwen3(cfg, W, max_ctx=max_ctx, max_prompt=prompt_len, dtype=dtype or torch.bfloat16)
     del W
     torch.cuda.empty_cache()
     rng = np.random.default_rng(4)
@@ -386,7 +391,7 @@ def bench_qwen3(torch, dev, prompt_len: int = 512, n_tokens: int = 256, dtype=No
             "prefill_note": "prefill_ms_512: the prompt's launches replayed as one HIP graph (captured once per "
                             "prompt length); _eager: the same launches issued one by one from Python",
             "bytes_per_token": w_bytes + kv_bytes, "hbm_gbs": round(gbs, 1),
-            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "tokens_generated": int(n_tokens),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "tokens_generated": int(n_tokens), "kv_ring_rows": m.max_ctx,
             "distinct_tokens": int(len(set(toks.tolist()))),
             "note": "batch 1, greedy, decode step = one HIP graph replay of 143 kernels (5 per layer: "
                     "RMSNorm fused into the GEMV prologues, SwiGLU into the gate_up GEMV epilogue, q/k norm + "
@@ -769,6 +774,8 @@ def main() -> int:
 
     if want("qwen3") and not args.quick:
         sections["qwen3_0p6b_decode"] = bench_qwen3(torch, dev)
+        torch.cuda.empty_cache()
+        sections["qwen3_0p6b_decode_default_ring"] = bench_qwen3(torch, dev, ring="default")
         torch.cuda.empty_cache()
         sections["qwen3_0p6b_decode_cpp_host"] = bench_qwen3_cpp()
         sections["qwen3_0p6b_decode_fp16"] = bench_qwen3(torch, dev, dtype=torch.float16)

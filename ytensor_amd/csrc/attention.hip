@@ -1730,6 +1730,25 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
     const int kb0 = split * chunk;
     const int kend = min(len, kb0 + chunk);
     const int kbeg = min(kb0, max(a.max_ctx - 1, 0));
+    if (kb0 >= len && !owner) {
+        // a split past the visible keys (a short context in a large ring): the
+        // partials of an empty split, m = -inf, l = 0, o = 0 (zeros when direct),
+        // the values the key loop below would leave
+        for (int idx = tid; idx < G * D; idx += NTH) {
+            const int gi = idx / D, d = idx % D, h = kvh * G + gi;
+            if (a.direct) {
+                store_from_f32<T>(a.O, b * a.os0 + h * a.os1 + d, 0.f);
+                continue;
+            }
+            float* dst = a.ws + (((int64_t)b * a.Hq + h) * a.splits + split) * (D + 2);
+            dst[2 + d] = 0.f;
+            if (d == 0) {
+                dst[0] = -INFINITY;
+                dst[1] = 0.f;
+            }
+        }
+        return;
+    }
 
     float m[G], l[G], o[G][8];
 #pragma unroll
@@ -2264,15 +2283,19 @@ int decode_splits(int B, int Hq, int max_ctx) {
 }
 
 // The workgroup size is a function of the launch shape only, so the fused and
-// the unfused decode paths produce the same partials.
-inline bool decode_wide(int B, int Hkv, int splits, int G, int D) {
-    return (int64_t)B * Hkv * splits < 256 && (int64_t)(512 / (D / 8)) * G * D * 4 <= 64 * 1024;
+// the unfused decode paths produce the same partials. 512 threads when the grid
+// does not cover the CUs, or when no split exceeds DEC_MIN_CHUNK keys (one
+// batch of 128 keys per split instead of two).
+inline bool decode_wide(int B, int Hkv, int splits, int G, int D, int max_ctx) {
+    const bool small_grid = (int64_t)B * Hkv * splits < 256;
+    const bool short_splits = splits > 0 && (max_ctx + splits - 1) / splits <= DEC_MIN_CHUNK;
+    return (small_grid || short_splits) && (int64_t)(512 / (D / 8)) * G * D * 4 <= 64 * 1024;
 }
 
 template <class T, int D, int G>
 hipError_t launch_decode_g(const DecodeArgs& a, hipStream_t s) {
     dim3 grid(a.splits, a.Hkv, a.B);
-    const bool wide = decode_wide(a.B, a.Hkv, a.splits, G, D);
+    const bool wide = decode_wide(a.B, a.Hkv, a.splits, G, D, a.max_ctx);
     const bool mk = a.mask != nullptr || a.bias != nullptr;
     if constexpr ((512 / (D / 8)) * G * D * 4 <= 64 * 1024) {
         if (wide) {
