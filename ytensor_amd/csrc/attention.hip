@@ -2284,12 +2284,14 @@ int decode_splits(int B, int Hq, int max_ctx) {
 
 // The workgroup size is a function of the launch shape only, so the fused and
 // the unfused decode paths produce the same partials. 512 threads when the grid
-// does not cover the CUs, or when no split exceeds DEC_MIN_CHUNK keys (one
-// batch of 128 keys per split instead of two).
+// does not cover the CUs, or covers them exactly once with no split longer than
+// DEC_MIN_CHUNK keys (one batch of 128 keys per split instead of two). A larger
+// grid keeps 256: the fused and masked kernels hold one 512-thread workgroup per
+// CU, so 512 of them would run in two rounds.
 inline bool decode_wide(int B, int Hkv, int splits, int G, int D, int max_ctx) {
-    const bool small_grid = (int64_t)B * Hkv * splits < 256;
+    const int64_t wgs = (int64_t)B * Hkv * splits;
     const bool short_splits = splits > 0 && (max_ctx + splits - 1) / splits <= DEC_MIN_CHUNK;
-    return (small_grid || short_splits) && (int64_t)(512 / (D / 8)) * G * D * 4 <= 64 * 1024;
+    return (wgs < 256 || (wgs == 256 && short_splits)) && (int64_t)(512 / (D / 8)) * G * D * 4 <= 64 * 1024;
 }
 
 template <class T, int D, int G>
