@@ -1612,7 +1612,7 @@ struct DecodeArgs {
     const uint8_t* mask;
     const float* bias;
     int64_t bcs;
-    int B, Hq, Hkv, max_ctx, splits, chunk;
+    int B, Hq, Hkv, max_ctx, splits;  // keys per split: decode_chunk(kv_len, splits)
     float scale_log2;
     float* ws;  // [B, Hq, splits, D + 2]
     // fused decode step (ythip_attn_decode_rope): the new token's q/k/v come
@@ -2372,7 +2372,6 @@ int decode_route(int dtype, const AttnArgs& p, int mask_kind, const uint8_t* mas
     if (splits < 1) splits = 1;
     a.splits = splits;
     a.direct = splits == 1;  // one split: the split kernel stores O, no merge
-    a.chunk = (int)((n + splits - 1) / splits);
     a.scale_log2 = p.scale_log2;
     a.ws = splits > 1 ? static_cast<float*>(workspace) : nullptr;
     a.mask = mask_kind == YTHIP_MASK_BOOL ? mask : nullptr;
@@ -2527,7 +2526,6 @@ __attribute__((visibility("default"))) int ythip_attn_decode(int dtype, int B, i
     a.kv_len = kv_len;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_ctx = max_ctx;
     a.splits = decode_splits(B, Hq, max_ctx > 0 ? max_ctx : 1);
-    a.chunk = max_ctx > 0 ? (max_ctx + a.splits - 1) / a.splits : 0;
     a.scale_log2 = scale * LOG2E;
     a.ws = static_cast<float*>(workspace);
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -2653,7 +2651,6 @@ __attribute__((visibility("default"))) int ythip_attn_decode_rope(
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_ctx = max_ctx;
     a.splits = decode_splits(B, Hq, max_ctx);
     a.direct = O != nullptr && a.splits == 1;  // one split: no merge launch
-    a.chunk = (max_ctx + a.splits - 1) / a.splits;
     a.scale_log2 = scale * LOG2E;
     a.ws = static_cast<float*>(workspace);
     a.qkv = qkv; a.ld_qkv = ld_qkv; a.wq = wq; a.wk = wk; a.eps = eps;
