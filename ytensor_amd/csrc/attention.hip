@@ -2052,7 +2052,10 @@ __global__ __launch_bounds__(NTH) void attn_decode_split(DecodeArgs a) {
 // so the merge pays one memory round trip; the arithmetic is the sequential
 // log-sum-exp combine over s = 0, 1, ... (the order the o projection's merge
 // prologue reproduces).
-constexpr int DEC_MAX_SPLITS = 64;
+// At most 32 splits: a batch-1, 16-head (8 kv-head) call then fills 256
+// workgroups, one per CU, of 512 threads (a 40960-row ring: 1203 -> 1318 tok/s
+// for the Qwen3-0.6B decode step, batch 1 ctx 8192 11.95 -> 11.4 us).
+constexpr int DEC_MAX_SPLITS = 32;
 template <class T, int D, int MAXS>  // MAXS >= splits: 8 or DEC_MAX_SPLITS
 __global__ __launch_bounds__(D) void attn_decode_merge(DecodeArgs a) {
     static_assert(MAXS <= D, "one thread stages each split's m and l");
@@ -2283,21 +2286,18 @@ int decode_splits(int B, int Hq, int max_ctx) {
 }
 
 // The workgroup size is a function of the launch shape only, so the fused and
-// the unfused decode paths produce the same partials. 512 threads when the grid
-// does not cover the CUs, or covers them exactly once with no split longer than
-// DEC_MIN_CHUNK keys (one batch of 128 keys per split instead of two). A larger
-// grid keeps 256: the fused and masked kernels hold one 512-thread workgroup per
-// CU, so 512 of them would run in two rounds.
-inline bool decode_wide(int B, int Hkv, int splits, int G, int D, int max_ctx) {
-    const int64_t wgs = (int64_t)B * Hkv * splits;
-    const bool short_splits = splits > 0 && (max_ctx + splits - 1) / splits <= DEC_MIN_CHUNK;
-    return (wgs < 256 || (wgs == 256 && short_splits)) && (int64_t)(512 / (D / 8)) * G * D * 4 <= 64 * 1024;
+// the unfused decode paths produce the same partials. 512 threads (32 keys in
+// flight, a 128-key batch per round) while the grid holds at most one workgroup
+// per CU; a larger grid keeps 256: the fused and masked kernels fit one
+// 512-thread workgroup per CU, so more of them would run in two rounds.
+inline bool decode_wide(int B, int Hkv, int splits, int G, int D) {
+    return (int64_t)B * Hkv * splits <= 256 && (int64_t)(512 / (D / 8)) * G * D * 4 <= 64 * 1024;
 }
 
 template <class T, int D, int G>
 hipError_t launch_decode_g(const DecodeArgs& a, hipStream_t s) {
     dim3 grid(a.splits, a.Hkv, a.B);
-    const bool wide = decode_wide(a.B, a.Hkv, a.splits, G, D, a.max_ctx);
+    const bool wide = decode_wide(a.B, a.Hkv, a.splits, G, D);
     const bool mk = a.mask != nullptr || a.bias != nullptr;
     if constexpr ((512 / (D / 8)) * G * D * 4 <= 64 * 1024) {
         if (wide) {
