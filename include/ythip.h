@@ -266,7 +266,9 @@ int ythip_attn_decode_noalloc(int dtype, int B, int Hq, int Hkv, int d, int max_
  * O == NULL only the split-K partials are produced, in the workspace as
  * fp32 [B][Hq][S][d + 2] = (running max m in log2 units, sum l, o[d]) per
  * split, S = ythip_attn_decode_splits(B, Hq, max_ctx), for a caller that
- * merges them itself.
+ * merges them itself. Split s holds keys [s*c, (s+1)*c) of the n visible
+ * ones, c = max(128, ceil(n / S)); splits past them hold m = -inf, l = 0,
+ * o = 0.
  * qkv rows, norm weights and cos/sin rows must be 16-byte aligned.
  */
 int ythip_attn_decode_splits(int B, int Hq, int max_ctx);
