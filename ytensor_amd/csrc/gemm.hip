@@ -620,12 +620,16 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
     }
     const uint32_t ldsA = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sA[(wave & 3) * 64]);
     const uint32_t ldsB = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sB[(wave & 3) * 64]);
-    auto issue = [&](int kt) {
+    // the DMA of step kt: A's slice, then B's
+    auto issueA = [&](int kt) {
         const int st = kt & 1;
         const char* bA = reinterpret_cast<const char*>(Ap) + (int64_t)kt * BK * 2;
 #pragma unroll
         for (int i = 0; i < A_PT; ++i)
             dma16_soff(bA + (int64_t)i * 32 * a.rsa * 2, offA, ldsA + (uint32_t)(st * STA + i * GT) * 16u);
+    };
+    auto issueB = [&](int kt) {
+        const int st = kt & 1;
         const char* bB = reinterpret_cast<const char*>(Bp) + (int64_t)kt * BK * (NN ? a.rsb : (int64_t)1) * 2;
 #pragma unroll
         for (int i = 0; i < B_PT; ++i) {
@@ -662,16 +666,18 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     u32x4 fa[2][FM], fb[2][FN];
-    auto X = [&](int kt) {
+    // the fragments of step kt's 32-wide k chunk ks
+    auto Xk = [&](int kt, int ks) {
         const u32x4* cA = sA + (kt & 1) * STA;
         const u32x4* cB = sB + (kt & 1) * STB;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int j = 0; j < FN; ++j) fb[ks][j] = ldB(cB, ks, j);
 #pragma unroll
-            for (int j = 0; j < FN; ++j) fb[ks][j] = ldB(cB, ks, j);
-#pragma unroll
-            for (int i = 0; i < FM; ++i) fa[ks][i] = ldA(cA, ks, i);
-        }
+        for (int i = 0; i < FM; ++i) fa[ks][i] = ldA(cA, ks, i);
+    };
+    auto X = [&](int kt) {
+        Xk(kt, 0);
+        Xk(kt, 1);
     };
     // the MFMA order of gemm_mfma_dma_kernel: per output fragment, k chunk 0 then 1
     auto Y = [&]() {
@@ -686,12 +692,18 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
     };
     constexpr int LGKM0 = 0xc07f;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt not waited
     if (!grpB) {
-        issue(0);
+        issueA(0);
+        issueB(0);
         for (int kt = 0; kt < KT; ++kt) {
             wait_vmcnt<0>();               // this wave's share of step kt has landed
             __builtin_amdgcn_s_barrier();  // step kt in LDS; group B done with stage (kt+1)&1
-            if (kt + 1 < KT) issue(kt + 1);
-            X(kt);
+            // step kt+1's DMA interleaved with step kt's fragment reads (A's slice,
+            // the first k chunk, B's slice, the second): 4096^3 NN 97.1 -> 96.0 us,
+            // NT 96.7 -> 94.6 us, the LM head 576 -> 563 us, the same bits
+            if (kt + 1 < KT) issueA(kt + 1);
+            Xk(kt, 0);
+            if (kt + 1 < KT) issueB(kt + 1);
+            Xk(kt, 1);
             Y();
         }
     } else {
