@@ -637,6 +637,23 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
             dma16_soff(bB + step, (i & 1) ? offB1 : offB0, ldsB + (uint32_t)(st * STB + i * GT) * 16u);
         }
     };
+    // half hf of A's or B's slice of step kt
+    auto issueAh = [&](int kt, int hf) {
+        const int st = kt & 1;
+        const char* bA = reinterpret_cast<const char*>(Ap) + (int64_t)kt * BK * 2;
+#pragma unroll
+        for (int i = hf * (A_PT / 2); i < (hf + 1) * (A_PT / 2); ++i)
+            dma16_soff(bA + (int64_t)i * 32 * a.rsa * 2, offA, ldsA + (uint32_t)(st * STA + i * GT) * 16u);
+    };
+    auto issueBh = [&](int kt, int hf) {
+        const int st = kt & 1;
+        const char* bB = reinterpret_cast<const char*>(Bp) + (int64_t)kt * BK * (NN ? a.rsb : (int64_t)1) * 2;
+#pragma unroll
+        for (int i = hf * (B_PT / 2); i < (hf + 1) * (B_PT / 2); ++i) {
+            const int64_t step = NN ? (int64_t)i * 8 * a.rsb * 2 : (int64_t)i * 32 * a.csb * 2;
+            dma16_soff(bB + step, (i & 1) ? offB1 : offB0, ldsB + (uint32_t)(st * STB + i * GT) * 16u);
+        }
+    };
     auto ldA = [&](const u32x4* s, int ks, int i) -> u32x4 {
         const int r = wm * WTM + i * 16 + lrow;
         return s[r * 8 + swz_dma(r, ks * 4 + lgrp)];
@@ -679,6 +696,16 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
         Xk(kt, 0);
         Xk(kt, 1);
     };
+    auto XB = [&](int kt, int ks) {
+        const u32x4* cB = sB + (kt & 1) * STB;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[ks][j] = ldB(cB, ks, j);
+    };
+    auto XA = [&](int kt, int ks) {
+        const u32x4* cA = sA + (kt & 1) * STA;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fa[ks][i] = ldA(cA, ks, i);
+    };
     // the MFMA order of gemm_mfma_dma_kernel: per output fragment, k chunk 0 then 1
     auto Y = [&]() {
         __builtin_amdgcn_s_setprio(1);
@@ -697,13 +724,28 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmArgs a) {
         for (int kt = 0; kt < KT; ++kt) {
             wait_vmcnt<0>();               // this wave's share of step kt has landed
             __builtin_amdgcn_s_barrier();  // step kt in LDS; group B done with stage (kt+1)&1
-            // step kt+1's DMA interleaved with step kt's fragment reads (A's slice,
-            // the first k chunk, B's slice, the second): 4096^3 NN 97.1 -> 96.0 us,
-            // NT 96.7 -> 94.6 us, the LM head 576 -> 563 us, the same bits
-            if (kt + 1 < KT) issueA(kt + 1);
-            Xk(kt, 0);
-            if (kt + 1 < KT) issueB(kt + 1);
-            Xk(kt, 1);
+            // step kt+1's DMA interleaved with step kt's fragment reads, the same
+            // bits. NT: A's slice, the first k chunk, B's slice, the second (4096^3
+            // NT 96.7 -> 94.6 us, the LM head 563 -> 559 us). NN, in quarters: half
+            // of A's slice before each of the first chunk's B and A fragment reads,
+            // then half of B's before the second chunk's (4096^3 NN 98.7 -> 98.0 ->
+            // 97.0 us over the two steps)
+            const bool nx = kt + 1 < KT;
+            if constexpr (NN) {
+                if (nx) issueAh(kt + 1, 0);
+                XB(kt, 0);
+                if (nx) issueAh(kt + 1, 1);
+                XA(kt, 0);
+                if (nx) issueBh(kt + 1, 0);
+                XB(kt, 1);
+                if (nx) issueBh(kt + 1, 1);
+                XA(kt, 1);
+            } else {
+                if (nx) issueA(kt + 1);
+                Xk(kt, 0);
+                if (nx) issueB(kt + 1);
+                Xk(kt, 1);
+            }
             Y();
         }
     } else {
