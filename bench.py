@@ -11,7 +11,7 @@ the kernels are launched on):
   gemm_4096_ceilings  the headline kernel's MFMA stream alone (register
                   operands) and its global -> LDS operand stream alone, same grid
   gemm_sweep      the other configs[1] shapes (NN and the W^T "linear" layout)
-  gemm_fp32       configs[0] (fp32 1024^3)
+  gemm_fp32       configs[0] (fp32 1024^3), and the same kernel at 4096^3
   attn_prefill    configs[2] causal flash prefill S = 512/2048/8192 (TFLOP/s), the
                   causal mask as bytes, and fp32 (the reference flash backend's dtype)
   attn_decode     configs[3] decode attention (GB/s of K/V read)
@@ -609,6 +609,16 @@ def main() -> int:
         fl = 2.0 * 1024 ** 3
         sections["gemm_fp32_1024"] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
                                       "frac_fp32_peak": round(fl / t / 1e9 / PEAK_FP32_TFLOPS, 4)}
+        del a32, b32, c32
+        # the same fp32 kernel at 4096^3 (enough tiles to fill the CUs several times)
+        a32 = torch.randn(4096, 4096, device=dev)
+        b32 = torch.randn(4096, 4096, device=dev)
+        c32 = torch.empty(4096, 4096, device=dev)
+        t = time_launches(lambda: ops.gemm(a32, b32, c32), max(args.steps // 4, 5), min(args.warmup, 3), torch)
+        fl = 2.0 * 4096 ** 3
+        sections["gemm_fp32_4096"] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                                      "frac_fp32_peak": round(fl / t / 1e9 / PEAK_FP32_TFLOPS, 4)}
+        del a32, b32, c32
 
     if want("prefill") and not args.quick:
         pre = []
